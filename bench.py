@@ -1,0 +1,327 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X W8A8 FP8 linear path (one JSON line on stdout).
+
+Workload: the M = 1 decode GEMV over every
+Qwen3-4B FP8 linear shape -- fused QKV 6144x2560, o_proj 2560x4096, fused
+gate_up 19456x2560, down_proj 2560x9728 -- each with dynamic 1x128-group
+activation quantization, 128x128 block-scaled E4M3 weights, fp32
+accumulation and bf16 output. One step is one pass over the four shapes
+(one decoder layer's FP8 linears). Inputs are synthetic and seeded on the
+GPU (W ~ N(0, 0.02) quantized per 128x128 block, x ~ N(0, 1) in bf16).
+Every shape's weights are rotated over enough distinct copies (>= 640 MB)
+that the 256 MB Infinity Cache cannot hold them between launches.
+
+value = algorithmic bytes per step / wall time per step (GB/s), timed over
+exactly --steps steps bracketed by device synchronizations. Algorithmic
+bytes of one FP8 linear = N*K + ceil(N/128)*(K/128)*4 + M*K*2 + M*N*2.
+
+"roofline" covers the dominant kernel (the fused M = 1 weight-streaming
+kernel): achieved = algorithmic bytes / kernel duration, both summed over
+the timed launches, with durations stamped at the kernel's own begin and
+end by HIP events (hipExtLaunchKernel) on the launch stream.
+"detail" adds per-shape figures, the bf16 lm_head, the batched-decode M
+sweep and the prefill GEMM at M = 512 and 4096
+in TFLOP/s against the 5.0 PFLOP/s dense FP8 peak.
+"cpu_baseline" times the CPU restatement of the same arithmetic
+(oracle/heph_oracle.c: quantize, dequantize, f32-accumulated matmul) on the
+host's cores over a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+FP8_PEAK_TFLOPS = 5000.0       # MI355X dense FP8 MFMA
+ROTATE_BYTES = 640 << 20       # > 2x the 256 MB Infinity Cache
+
+SHAPES = [("qkv", 6144, 2560), ("o_proj", 2560, 4096), ("gate_up", 19456, 2560),
+          ("down", 2560, 9728)]
+Q_PROJ = ("q_proj", 4096, 2560)
+LM_HEAD = ("lm_head", 151936, 2560)
+
+
+def fp8_bytes(M, N, K):
+    return N * K + (-(-N // 128)) * (K // 128) * 4 + M * K * 2 + M * N * 2
+
+
+def bf16_bytes(M, N, K, out_bytes=4):
+    return 2 * N * K + 2 * M * K + out_bytes * M * N
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--quick", action="store_true", help="skip the detail sweeps")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    return ap.parse_args()
+
+
+class Linear:
+    """One FP8 linear with rotated weight copies and its own workspace."""
+
+    def __init__(self, name, N, K, M_max, seed, rotate=True):
+        import torch
+        from hephaestus_amd import kernels as HK
+        from hephaestus_amd.weights import quantize_weight_fp8
+        self.name, self.N, self.K = name, N, K
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        w = (torch.randn(N, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+        q, s = quantize_weight_fp8(w)
+        del w
+        copies = max(1, math.ceil(ROTATE_BYTES / (N * K))) if rotate else 1
+        self.w = [q] + [q.clone() for _ in range(copies - 1)]
+        self.s = [s] + [s.clone() for _ in range(copies - 1)]
+        self.q_ws, self.s_ws = HK.workspace(M_max, K)
+        self.i = 0
+
+    def next(self):
+        w, s = self.w[self.i], self.s[self.i]
+        self.i = (self.i + 1) % len(self.w)
+        return w, s
+
+
+def act(M, K, seed, outliers=False):
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn(M, K, generator=g, device="cuda")
+    if outliers:
+        u = torch.rand(M, K, generator=g, device="cuda")
+        x = torch.where(u < 1e-3, x * 50.0, x)
+    return x.to(torch.bfloat16)
+
+
+def time_calls(fn, n, timer):
+    """Run fn() n times with kernel-boundary timing; returns summed ms."""
+    import torch
+    timer.reset()
+    for _ in range(n):
+        timer.arm()
+        fn()
+    torch.cuda.synchronize()
+    return sum(timer.durations_ms())
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the FP8 linear path has no multi-GPU mode here)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from hephaestus_amd import kernels as HK
+    from hephaestus_amd.timing import KernelTimer
+
+    torch.cuda.set_device(0)
+    props = torch.cuda.get_device_properties(0)
+    lins = [Linear(n, N, K, 32, seed=100 + i) for i, (n, N, K) in enumerate(SHAPES)]
+    xs = {K: act(1, K, seed=K) for K in {K for _, _, K in SHAPES}}
+    outs = [torch.empty(1, N, dtype=torch.bfloat16, device="cuda") for _, N, _ in SHAPES]
+
+    def step(timer=None):
+        for lin, c in zip(lins, outs):
+            w, s = lin.next()
+            if timer is not None:
+                timer.arm()
+            HK.linear_fp8(c, xs[lin.K], w, s, lin.q_ws, lin.s_ws, 1, lin.N, lin.K)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timer = KernelTimer(len(lins) * args.steps)
+    kernel_names = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(timer)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_names.append(HK.last_kernel())
+    durs = timer.durations_ms()
+    timer.close()
+
+    step_bytes = sum(fp8_bytes(1, N, K) for _, N, K in SHAPES)
+    ms_per_step = wall * 1e3 / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    per_shape = {}
+    for j, (name, N, K) in enumerate(SHAPES):
+        d = durs[j::len(SHAPES)]
+        avg_us = 1e3 * sum(d) / len(d)
+        per_shape[name] = {"N": N, "K": K, "kernel_us": round(avg_us, 3),
+                           "GBs": round(fp8_bytes(1, N, K) / (avg_us * 1e-6) / 1e9, 1),
+                           "copies": len(lins[j].w)}
+    kern_ms = sum(durs)
+    achieved = step_bytes * args.steps / (kern_ms * 1e-3) / 1e9
+
+    detail = {"m1_shapes": per_shape,
+              "kernel_time_per_step_us": round(1e3 * kern_ms / args.steps, 3)}
+    if not args.quick:
+        detail.update(detail_sweeps(lins))
+
+    cpu = None if args.no_cpu else cpu_baseline(lins, xs, args.cpu_seconds)
+
+    line = {
+        "metric": "FP8 GEMV GB/s (% of HBM peak) at M=1; prefill FP8 GEMM TFLOP/s at M=4096",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3 x fp8_e4m3 -> f32 acc -> bf16",
+        "data": "synthetic (seeded GPU randn; weights quantized per 128x128 block)",
+        "config": {"workload": "configs[1]: M=1 FP8 GEMV over Qwen3-4B linears "
+                               "(qkv 6144x2560, o 2560x4096, gate_up 19456x2560, "
+                               "down 2560x9728), fused 1x128 act quant, bf16 out",
+                   "M": 1, "step": "one pass over the 4 shapes", "device": props.name,
+                   "arch": props.gcnArchName},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": kernel_names[-1],
+                     "bytes_per_step": step_bytes},
+        "cpu_baseline": cpu,
+        "detail": detail,
+    }
+    print(json.dumps(line))
+
+
+def detail_sweeps(lins):
+    import torch
+    from hephaestus_amd import kernels as HK
+    from hephaestus_amd.timing import KernelTimer
+    out = {}
+    timer = KernelTimer(64)
+
+    # config 0: q_proj at M = 1
+    qp = Linear(*Q_PROJ, 1, seed=7)
+    x = act(1, qp.K, seed=8)
+    c = torch.empty(1, qp.N, dtype=torch.bfloat16, device="cuda")
+
+    def run_q():
+        w, s = qp.next()
+        HK.linear_fp8(c, x, w, s, qp.q_ws, qp.s_ws, 1, qp.N, qp.K)
+    run_q()
+    ms = time_calls(run_q, 50, timer) / 50
+    out["config0_q_proj_m1"] = {"kernel_us": round(ms * 1e3, 3),
+                                "GBs": round(fp8_bytes(1, qp.N, qp.K) / (ms * 1e-3) / 1e9, 1)}
+    del qp
+
+    # bf16 lm_head at M = 1 (f32 logits), two weight copies (> 1.5 GB)
+    name, N, K = LM_HEAD
+    g = torch.Generator(device="cuda").manual_seed(9)
+    lw = [(torch.randn(N, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+          for _ in range(2)]
+    xl = act(1, K, seed=10)
+    logits = torch.empty(1, N, dtype=torch.float32, device="cuda")
+    it = [0]
+
+    def run_lm():
+        HK.linear(logits, xl, lw[it[0] % 2], 1, N, K)
+        it[0] += 1
+    run_lm()
+    ms = time_calls(run_lm, 20, timer) / 20
+    out["lm_head_bf16_m1"] = {"kernel_us": round(ms * 1e3, 3),
+                              "GBs": round(bf16_bytes(1, N, K) / (ms * 1e-3) / 1e9, 1),
+                              "frac": round(bf16_bytes(1, N, K) / (ms * 1e-3) / 1e9
+                                            / HBM_PEAK_GBS, 4)}
+    del lw
+
+    # batched decode M in {2..32}; path time = quant + kernel
+    small = {}
+    for M in (2, 4, 8, 16, 32):
+        row = {}
+        for lin in lins:
+            xm = act(M, lin.K, seed=M)
+            cm = torch.empty(M, lin.N, dtype=torch.bfloat16, device="cuda")
+
+            def run_m(lin=lin, xm=xm, cm=cm, M=M):
+                w, s = lin.next()
+                HK.linear_fp8(cm, xm, w, s, lin.q_ws, lin.s_ws, M, lin.N, lin.K)
+            run_m()
+            ms = time_calls(run_m, 20, timer) / 20
+            row[lin.name] = round(fp8_bytes(M, lin.N, lin.K) / (ms * 1e-3) / 1e9, 1)
+        small[f"M={M}"] = row
+    out["small_m_GBs"] = small
+
+    # prefill GEMM, quant + GEMM path time, TFLOP/s
+    pre = {}
+    for M in (512, 4096):
+        row = {}
+        for lin in lins:
+            xm = act(M, lin.K, seed=M + 1, outliers=True)
+            cm = torch.empty(M, lin.N, dtype=torch.bfloat16, device="cuda")
+            q_ws, s_ws = HK.workspace(M, lin.K)
+            w, s = lin.w[0], lin.s[0]
+
+            def run_p(lin=lin, xm=xm, cm=cm, M=M, q_ws=q_ws, s_ws=s_ws, w=w, s=s):
+                HK.linear_fp8(cm, xm, w, s, q_ws, s_ws, M, lin.N, lin.K)
+            run_p()
+            n = 10
+            ms = time_calls(run_p, n, timer) / n
+            tf = 2.0 * M * lin.N * lin.K / (ms * 1e-3) / 1e12
+            row[lin.name] = {"us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
+                             "frac": round(tf / FP8_PEAK_TFLOPS, 4)}
+        pre[f"M={M}"] = row
+    out["prefill"] = pre
+    t4096 = sum(2.0 * 4096 * l.N * l.K for l in lins)
+    us4096 = sum(v["us"] for v in pre["M=4096"].values())
+    out["prefill_m4096_TFLOPs"] = round(t4096 / (us4096 * 1e-6) / 1e12, 1)
+    out["prefill_m4096_frac"] = round(out["prefill_m4096_TFLOPs"] / FP8_PEAK_TFLOPS, 4)
+    timer.close()
+    return out
+
+
+def cpu_baseline(lins, xs, seconds):
+    """The oracle's quantize + dequant-matmul on host cores, M = 1, over the
+    same four shapes (same weights and activations, copied to the host)."""
+    import numpy as np
+    import torch
+    from oracle import oracle as O
+    O.build()
+    threads = max(1, min(16, os.cpu_count() or 1))
+    os.environ.setdefault("OMP_NUM_THREADS", str(threads))
+    host = []
+    for lin in lins:
+        host.append((lin.w[0].cpu().numpy(), lin.s[0].cpu().numpy(),
+                     xs[lin.K].view(torch.int16).cpu().numpy().view(np.uint16),
+                     lin.N, lin.K))
+    budget = seconds / len(host)
+    tot_bytes, tot_s, reps = 0, 0.0, {}
+    for qw, sw, x, N, K in host:
+        O.quant_linear(x, qw, sw, nthreads=threads)       # warm
+        n, t0 = 0, time.perf_counter()
+        while True:
+            O.quant_linear(x, qw, sw, nthreads=threads)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                break
+        tot_bytes += n * fp8_bytes(1, N, K)
+        tot_s += el
+        reps[N * 100000 + K] = n
+    cpu_name = ""
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                cpu_name = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(tot_bytes / tot_s / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle quant + f32 dequant-matmul, M=1, the 4 config-1 shapes, "
+                      f"~{seconds:.0f} s total ({sum(reps.values())} calls); CPU: {cpu_name}"}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,92 @@
+"""ctypes binding of libhephfp8.so (the C ABI declared in include/hephfp8.h).
+
+The library is built in-tree by hephaestus_amd/build.py. There is no
+fallback: if the shared object is missing, loading raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libhephfp8.so")
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                      "include", "hephfp8.h")
+
+_lib = None
+
+HEPH_OK = 0
+HEPH_ERR_NULL = -1
+HEPH_ERR_SHAPE = -2
+HEPH_ERR_ALIGN = -3
+HEPH_ERR_GROUP = -4
+HEPH_ERR_DTYPE = -5
+HEPH_ERR_WORKSPACE = -6
+HEPH_ERR_FLAGS = -7
+HEPH_ERR_DEVICE = -8
+HEPH_ERR_LAUNCH = -9
+
+HEPH_DTYPE_BF16 = 0
+HEPH_DTYPE_F32 = 1
+
+FLAG_ADD_RESIDUAL = 0x1
+FLAG_SKIP_QUANT = 0x2
+FLAG_FORCE_SKINNY = 0x4
+FLAG_FORCE_GEMM = 0x8
+FLAG_NO_FUSE = 0x10
+
+SKINNY_MAX_M = 32
+
+TUNE_SKINNY_WAVES = 1
+TUNE_SKINNY_U = 2
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_sz = ctypes.c_size_t
+
+SIGNATURES = {
+    "heph_fp8_quant_act": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "heph_fp8_quant_weight": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "heph_fp8_linear": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _vp, _sz, _vp, _sz,
+                             _i, _i, _i, _i, _i, _vp]),
+    "heph_bf16_linear": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "heph_fp8_q_ws_bytes": (_sz, [_i, _i]),
+    "heph_fp8_s_ws_floats": (_sz, [_i, _i, _i]),
+    "heph_strerror": (ctypes.c_char_p, [_i]),
+    "heph_abi_version": (_i, []),
+    "heph_profile_next_launch": (_i, [_vp, _vp]),
+    "heph_last_kernel": (ctypes.c_char_p, []),
+    "heph_set_tuning": (_i, [_i, _i]),
+}
+
+
+class HephLibraryMissing(ImportError):
+    pass
+
+
+def lib():
+    """Load libhephfp8.so once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise HephLibraryMissing(
+                f"{LIB_PATH} not found: build it with `python hephaestus_amd/build.py` "
+                "(or __graft_entry__.build()); there is no non-HIP fallback")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def header_functions() -> list[str]:
+    """Names of the functions include/hephfp8.h declares."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(heph_[a-z0-9_]+)\s*\(", text)))
+
+
+def strerror(status: int) -> str:
+    return lib().heph_strerror(status).decode()

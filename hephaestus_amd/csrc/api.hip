@@ -1,0 +1,236 @@
+// api.hip - the C ABI (include/hephfp8.h): argument checks and dispatch.
+//
+// Mirrors the reference's FP8 linear dispatch (src/hephaestus/kernels.mojo:
+// 410-470 linear_fp8, :473-527 linear_add_residual_fp8, :372-407 gemv_fp8):
+// M <= 32 goes to the weight-streaming kernel (the reference sends M == 1
+// to its GEMV and 2..32 to its small-M kernel), larger M to the tiled GEMM;
+// do_quantize=False becomes HEPH_FLAG_SKIP_QUANT. Unlike the reference,
+// whose shape preconditions are debug_assert only
+// (wmma_gfx12.mojo:731-732, :872-874, :996-1005), every precondition is
+// checked here on every call and reported as a status code.
+#include <cstring>
+#include <mutex>
+
+#include "../../include/hephfp8.h"
+#include "heph_kernels.h"
+
+using namespace heph;
+
+namespace {
+
+thread_local LaunchTiming g_next_timing;
+thread_local const char* g_last_kernel = "none";
+
+constexpr int kMaxDevices = 64;
+int g_dev_ok[kMaxDevices];  // 0 unknown, 1 gfx950, -1 other
+std::mutex g_dev_mu;
+
+int check_device()
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return HEPH_ERR_DEVICE;
+    if (dev < 0 || dev >= kMaxDevices) return HEPH_ERR_DEVICE;
+    int state = __atomic_load_n(&g_dev_ok[dev], __ATOMIC_ACQUIRE);
+    if (state == 0) {
+        std::lock_guard<std::mutex> lk(g_dev_mu);
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, dev) != hipSuccess) return HEPH_ERR_DEVICE;
+        state = strncmp(p.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
+        __atomic_store_n(&g_dev_ok[dev], state, __ATOMIC_RELEASE);
+    }
+    return state == 1 ? HEPH_OK : HEPH_ERR_DEVICE;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+LaunchTiming take_timing()
+{
+    LaunchTiming t = g_next_timing;
+    g_next_timing = LaunchTiming{};
+    return t;
+}
+
+int launch_status(hipError_t e) { return e == hipSuccess ? HEPH_OK : HEPH_ERR_LAUNCH; }
+
+int check_quant_args(const void* x, const void* q, const void* s, int M, int K, int group_k)
+{
+    if (!x || !q || !s) return HEPH_ERR_NULL;
+    if (M < 1 || K < kChunk || K % kChunk) return HEPH_ERR_SHAPE;
+    if ((long)M * K > (1L << 40)) return HEPH_ERR_SHAPE;
+    if (group_k != kChunk && group_k != K) return HEPH_ERR_GROUP;
+    if (!aligned16(x) || !aligned16(q)) return HEPH_ERR_ALIGN;
+    return HEPH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t heph_fp8_q_ws_bytes(int M, int K)
+{
+    if (M < 1 || K < 1) return 0;
+    return (size_t)M * (size_t)K;
+}
+
+size_t heph_fp8_s_ws_floats(int M, int K, int group_k)
+{
+    if (M < 1 || K < 1 || group_k < 1 || K % group_k) return 0;
+    return (size_t)M * (size_t)(K / group_k);
+}
+
+int heph_fp8_quant_act(const uint16_t* x_bf16, uint8_t* q, float* scales, int M,
+                       int K, int group_k, void* stream)
+{
+    int st = check_quant_args(x_bf16, q, scales, M, K, group_k);
+    if (st != HEPH_OK) return st;
+    if ((st = check_device()) != HEPH_OK) return st;
+    return launch_status(launch_quant(x_bf16, q, scales, M, K, group_k,
+                                      static_cast<hipStream_t>(stream)));
+}
+
+int heph_fp8_quant_weight(const uint16_t* w_bf16, uint8_t* q, float* scale_inv, int N,
+                          int K, void* stream)
+{
+    if (!w_bf16 || !q || !scale_inv) return HEPH_ERR_NULL;
+    if (N < 1 || K < kChunk || K % kChunk || (long)N * K > (1L << 40)) return HEPH_ERR_SHAPE;
+    if (!aligned16(w_bf16) || !aligned16(q)) return HEPH_ERR_ALIGN;
+    int st = check_device();
+    if (st != HEPH_OK) return st;
+    return launch_status(launch_wquant(w_bf16, q, scale_inv, N, K,
+                                       static_cast<hipStream_t>(stream)));
+}
+
+int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t* w,
+                    const float* w_scale, int w_block_n, int w_block_k, uint8_t* q_ws,
+                    size_t q_ws_bytes, float* s_ws, size_t s_ws_floats, int M, int N,
+                    int K, int group_k, int flags, void* stream)
+{
+    const int known = HEPH_FLAG_ADD_RESIDUAL | HEPH_FLAG_SKIP_QUANT |
+                      HEPH_FLAG_FORCE_SKINNY | HEPH_FLAG_FORCE_GEMM | HEPH_FLAG_NO_FUSE;
+    if (flags & ~known) return HEPH_ERR_FLAGS;
+    if ((flags & HEPH_FLAG_FORCE_SKINNY) && (flags & HEPH_FLAG_FORCE_GEMM))
+        return HEPH_ERR_FLAGS;
+    const bool skip_quant = flags & HEPH_FLAG_SKIP_QUANT;
+    if (!c || !w || !w_scale || !q_ws || !s_ws) return HEPH_ERR_NULL;
+    if (!skip_quant && !x_bf16) return HEPH_ERR_NULL;
+    if (c_dtype != HEPH_DTYPE_BF16 && c_dtype != HEPH_DTYPE_F32) return HEPH_ERR_DTYPE;
+    if (M < 1 || N < 16 || K < kChunk || N % 16 || K % kChunk) return HEPH_ERR_SHAPE;
+    if ((long)M * K > (1L << 40) || (long)N * K > (1L << 40) || (long)M * N > (1L << 40))
+        return HEPH_ERR_SHAPE;
+    if ((flags & HEPH_FLAG_FORCE_SKINNY) && M > HEPH_SKINNY_MAX_M) return HEPH_ERR_FLAGS;
+    if (group_k != kChunk && group_k != K) return HEPH_ERR_GROUP;
+    bool w_block;
+    if (w_block_n == kChunk && w_block_k == kChunk) w_block = true;
+    else if (w_block_n == 1 && w_block_k == K) w_block = false;
+    else return HEPH_ERR_GROUP;
+    if (q_ws_bytes < heph_fp8_q_ws_bytes(M, K) ||
+        s_ws_floats < heph_fp8_s_ws_floats(M, K, group_k))
+        return HEPH_ERR_WORKSPACE;
+    if (!aligned16(c) || !aligned16(w) || !aligned16(q_ws) || (x_bf16 && !aligned16(x_bf16)))
+        return HEPH_ERR_ALIGN;
+    int st = check_device();
+    if (st != HEPH_OK) return st;
+
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    Fp8Operands op{};
+    op.w = w;
+    op.sw = w_scale;
+    op.sw_ld = w_block ? K / kChunk : 1;
+    op.w_block = w_block;
+    op.x = x_bf16;
+    op.q = q_ws;
+    op.s = s_ws;
+    op.s_ld = K / group_k;
+    op.s_step = group_k == kChunk ? 1 : 0;
+    op.c = c;
+    op.c_f32 = c_dtype == HEPH_DTYPE_F32;
+    op.residual = flags & HEPH_FLAG_ADD_RESIDUAL;
+    op.M = M;
+    op.N = N;
+    op.K = K;
+
+    const bool skinny = (flags & HEPH_FLAG_FORCE_SKINNY) ||
+                        (!(flags & HEPH_FLAG_FORCE_GEMM) && M <= HEPH_SKINNY_MAX_M);
+    const bool fused = skinny && !skip_quant && !(flags & HEPH_FLAG_NO_FUSE) &&
+                       group_k == kChunk && M <= kFusedMaxM;
+    LaunchTiming t = take_timing();
+    if (!skip_quant && !fused) {
+        // A timed call spans both kernels: the quantizer carries the start
+        // stamp and the main kernel the stop stamp.
+        hipError_t e = launch_quant(x_bf16, q_ws, s_ws, M, K, group_k, s,
+                                    LaunchTiming{t.start, nullptr});
+        if (e != hipSuccess) return HEPH_ERR_LAUNCH;
+        t.start = nullptr;
+    }
+    hipError_t e = skinny ? launch_fp8_skinny(op, fused, s, t, &g_last_kernel)
+                          : launch_fp8_gemm(op, s, t, &g_last_kernel);
+    return launch_status(e);
+}
+
+int heph_bf16_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint16_t* w_bf16,
+                     int M, int N, int K, int flags, void* stream)
+{
+    if (flags & ~HEPH_FLAG_ADD_RESIDUAL) return HEPH_ERR_FLAGS;
+    if (!c || !x_bf16 || !w_bf16) return HEPH_ERR_NULL;
+    if (c_dtype != HEPH_DTYPE_BF16 && c_dtype != HEPH_DTYPE_F32) return HEPH_ERR_DTYPE;
+    if (M < 1 || M > HEPH_SKINNY_MAX_M || N < 16 || N % 16 || K < kChunk || K % kChunk)
+        return HEPH_ERR_SHAPE;
+    if ((long)N * K > (1L << 40)) return HEPH_ERR_SHAPE;
+    if (!aligned16(c) || !aligned16(x_bf16) || !aligned16(w_bf16)) return HEPH_ERR_ALIGN;
+    int st = check_device();
+    if (st != HEPH_OK) return st;
+    const LaunchTiming t = take_timing();
+    return launch_status(launch_bf16_skinny(c, c_dtype == HEPH_DTYPE_F32,
+                                            flags & HEPH_FLAG_ADD_RESIDUAL, x_bf16, w_bf16,
+                                            M, N, K, static_cast<hipStream_t>(stream), t,
+                                            &g_last_kernel));
+}
+
+const char* heph_strerror(int status)
+{
+    switch (status) {
+    case HEPH_OK: return "ok";
+    case HEPH_ERR_NULL: return "a required pointer is NULL";
+    case HEPH_ERR_SHAPE: return "M, N or K out of range (need M>=1, N%16==0, K%128==0)";
+    case HEPH_ERR_ALIGN: return "pointer not 16-byte aligned";
+    case HEPH_ERR_GROUP: return "unsupported activation group or weight block";
+    case HEPH_ERR_DTYPE: return "unknown output dtype";
+    case HEPH_ERR_WORKSPACE: return "workspace smaller than required";
+    case HEPH_ERR_FLAGS: return "unknown or contradictory flags";
+    case HEPH_ERR_DEVICE: return "current HIP device is not gfx950 (MI355X)";
+    case HEPH_ERR_LAUNCH: return "HIP kernel launch failed";
+    default: return "unknown status";
+    }
+}
+
+int heph_abi_version(void) { return HEPH_ABI_VERSION; }
+
+int heph_profile_next_launch(void* start_event, void* stop_event)
+{
+    g_next_timing.start = static_cast<hipEvent_t>(start_event);
+    g_next_timing.stop = static_cast<hipEvent_t>(stop_event);
+    return HEPH_OK;
+}
+
+const char* heph_last_kernel(void) { return g_last_kernel; }
+
+int heph_set_tuning(int knob, int value)
+{
+    static int waves = 0, u = 0;
+    switch (knob) {
+    case HEPH_TUNE_SKINNY_WAVES:
+        if (value != 0 && value != 2 && value != 4 && value != 8 && value != 16)
+            return HEPH_ERR_FLAGS;
+        waves = value;
+        break;
+    case HEPH_TUNE_SKINNY_U:
+        if (value != 0 && value != 2 && value != 4) return HEPH_ERR_FLAGS;
+        u = value;
+        break;
+    default: return HEPH_ERR_FLAGS;
+    }
+    skinny_tune(waves, u);
+    return HEPH_OK;
+}
+
+}  // extern "C"

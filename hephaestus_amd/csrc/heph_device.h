@@ -1,0 +1,122 @@
+// heph_device.h - gfx950 device helpers shared by the FP8 linear kernels.
+//
+// Operand layout used by every MFMA kernel here (v_mfma_f32_16x16x128_f8f6f4,
+// wave64): lane l holds row (l & 15) of the A tile and column (l & 15) of the
+// B tile; its 32 operand bytes are the K positions
+//   [s*16, s*16+16) and [64 + s*16, 64 + s*16 + 16)   with s = l >> 4
+// of the 128-wide K chunk. A and B use the same lane -> K assignment, so the
+// contraction is exact whatever order the hardware walks the 32 bytes in.
+// Result layout (4 floats per lane): element i is row (l >> 4) * 4 + i,
+// column l & 15 of the 16x16 tile.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "scale_tables.h"
+
+namespace heph {
+
+typedef int      i32x4 __attribute__((ext_vector_type(4)));
+typedef int      i32x8 __attribute__((ext_vector_type(8)));
+typedef float    f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16   bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr float kE4M3Max = 448.0f;
+constexpr int kChunk = 128;  // K positions per MFMA / per scale group
+
+// D = A(16x128, e4m3) * B(128x16, e4m3) + C, fp32 accumulation.
+// The scale operands are zero, so the compiler emits the unscaled
+// v_mfma_f32_16x16x128_f8f6f4 (format code 0 = E4M3 for both operands).
+__device__ __forceinline__ f32x4 mfma_e4m3(const i32x8& a, const i32x8& b,
+                                           const f32x4& c)
+{
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0,
+                                                            0, 0);
+}
+
+// D = A(16x32, bf16) * B(32x16, bf16) + C.
+__device__ __forceinline__ f32x4 mfma_bf16(const bf16x8& a, const bf16x8& b,
+                                           const f32x4& c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ i32x8 join(const i32x4& lo, const i32x4& hi)
+{
+    return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// Two bf16 packed in a dword -> two floats (exact).
+__device__ __forceinline__ float bf16lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+
+// f32 -> bf16 bits, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f)
+{
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// Four floats -> four E4M3FN codes (byte i = code of value i) with the
+// hardware converter (round to nearest even).
+__device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d)
+{
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+    return (uint32_t)w;
+}
+
+__device__ __forceinline__ float absmax8(const uint4& v, float m)
+{
+    m = fmaxf(m, fabsf(bf16lo(v.x))); m = fmaxf(m, fabsf(bf16hi(v.x)));
+    m = fmaxf(m, fabsf(bf16lo(v.y))); m = fmaxf(m, fabsf(bf16hi(v.y)));
+    m = fmaxf(m, fabsf(bf16lo(v.z))); m = fmaxf(m, fabsf(bf16hi(v.z)));
+    m = fmaxf(m, fabsf(bf16lo(v.w))); m = fmaxf(m, fabsf(bf16hi(v.w)));
+    return m;
+}
+
+// Eight bf16 times inv -> eight codes in two dwords.
+__device__ __forceinline__ uint2 quant8(const uint4& v, float inv)
+{
+    uint2 r;
+    r.x = pack4_e4m3(bf16lo(v.x) * inv, bf16hi(v.x) * inv, bf16lo(v.y) * inv,
+                     bf16hi(v.y) * inv);
+    r.y = pack4_e4m3(bf16lo(v.z) * inv, bf16hi(v.z) * inv, bf16lo(v.w) * inv,
+                     bf16hi(v.w) * inv);
+    return r;
+}
+
+// Group scale of the reference quantizer for a bf16 amax: s = RN(amax/448)
+// (1.0 when below 1e-12) and inv = RN(1/s), from the exact mantissa tables
+// of scale_tables.h plus one ldexp each (no division). amax must be the
+// magnitude of a bf16 value (low 16 bits zero); zero and subnormal amax
+// take the floor, an infinite amax gives s = inf, inv = 0 as the division
+// would.
+static __constant__ ScaleTables g_scale_tab = make_scale_tables();
+
+__device__ __forceinline__ void group_scale(float amax, float& s, float& inv)
+{
+    const uint32_t u = __float_as_uint(amax);
+    const int e = (int)(u >> 23);
+    const int m = (int)((u >> 16) & 0x7Fu);
+    if (e == 0) { s = 1.0f; inv = 1.0f; return; }
+    if (e == 255) { s = __builtin_inff(); inv = 0.0f; return; }
+    s = ldexpf(g_scale_tab.scale[m], e - 134);
+    inv = ldexpf(g_scale_tab.inv[m], 134 - e);
+    if (s < 1e-12f) { s = 1.0f; inv = 1.0f; }
+}
+
+__device__ __forceinline__ i32x4 ldg16(const void* p)
+{
+    return *reinterpret_cast<const i32x4*>(p);
+}
+
+__device__ __forceinline__ uint4 ldg16u(const void* p)
+{
+    return *reinterpret_cast<const uint4*>(p);
+}
+
+}  // namespace heph

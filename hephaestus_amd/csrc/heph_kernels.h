@@ -1,0 +1,79 @@
+// heph_kernels.h - host-side launchers of the gfx950 kernels (internal to
+// the library; the public surface is include/hephfp8.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
+#include <stdint.h>
+
+#include "heph_device.h"
+
+namespace heph {
+
+// Optional kernel-boundary timestamps for the main kernel of a call.
+struct LaunchTiming {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+
+template <typename... KArgs, typename... Args>
+hipError_t launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t shmem,
+                  hipStream_t stream, const LaunchTiming& t, Args... args)
+{
+    if (t.start || t.stop)
+        hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, t.start, t.stop,
+                              0u, static_cast<KArgs>(args)...);
+    else
+        kernel<<<grid, block, shmem, stream>>>(static_cast<KArgs>(args)...);
+    return hipGetLastError();
+}
+
+// Activation scale addressing shared by the kernels: chunk j of row m uses
+// s[m * s_ld + j * s_step]; group 128: s_ld = K/128, s_step = 1;
+// per-token (group K): s_ld = 1, s_step = 0.
+// Weight scale addressing: block-128 uses sw[(n / 128) * sw_ld + j] with
+// sw_ld = K / 128; per-channel uses sw[n].
+struct Fp8Operands {
+    const uint8_t* w;      // [N, K] e4m3
+    const float* sw;       // weight scales
+    int sw_ld;
+    bool w_block;          // true: 128x128 blocks, false: per-channel [N,1]
+    const uint16_t* x;     // [M, K] bf16 (fused quantization only)
+    uint8_t* q;            // [M, K] e4m3 codes (workspace)
+    float* s;              // activation scales (workspace)
+    int s_ld;
+    int s_step;
+    void* c;               // [M, N] bf16 or f32
+    bool c_f32;
+    bool residual;
+    int M, N, K;
+};
+
+hipError_t launch_quant(const uint16_t* x, uint8_t* q, float* scales, int M,
+                        int K, int group_k, hipStream_t stream,
+                        const LaunchTiming& t = LaunchTiming{});
+
+// bf16 [N,K] -> e4m3 codes + f32 scale_inv [ceil(N/128), K/128].
+hipError_t launch_wquant(const uint16_t* w, uint8_t* q, float* scale_inv, int N, int K,
+                         hipStream_t stream);
+
+// M <= 32 weight-streaming kernel. fused: quantize x inside the kernel
+// (group 128, M <= kFusedMaxM); workgroup 0 also writes q/s.
+constexpr int kFusedMaxM = 4;
+hipError_t launch_fp8_skinny(const Fp8Operands& op, bool fused, hipStream_t stream,
+                             const LaunchTiming& t, const char** name);
+
+// Overrides for the skinny kernel's launch shape (0 = automatic).
+void skinny_tune(int waves, int u);
+
+// Tiled MFMA GEMM for any M (prefill); reads q/s from the workspace.
+hipError_t launch_fp8_gemm(const Fp8Operands& op, hipStream_t stream,
+                           const LaunchTiming& t, const char** name);
+
+// bf16 x [M,K] @ w [N,K]^T, f32 accumulation, M <= 32.
+hipError_t launch_bf16_skinny(void* c, bool c_f32, bool residual, const uint16_t* x,
+                              const uint16_t* w, int M, int N, int K,
+                              hipStream_t stream, const LaunchTiming& t,
+                              const char** name);
+
+}  // namespace heph

@@ -1,0 +1,161 @@
+/*
+ * hephfp8.h - C ABI of the MI355X (gfx950) W8A8 FP8 linear-layer library.
+ *
+ * The library replaces the matmul dispatch of the Hephaestus engine's FP8
+ * linear layer. Every entry point takes caller-owned device pointers and a
+ * HIP stream, allocates nothing, never synchronizes, and is reentrant.
+ * Shapes are checked on the host on every call; a bad call returns a
+ * negative HEPH_ERR_* code and launches nothing.
+ *
+ * Data layouts (all row-major, device memory):
+ *   activations x    bf16 [M, K]                  (uint16_t bit patterns)
+ *   weight w         OCP E4M3FN codes [N, K]      (safetensors [out, in])
+ *   weight scale     f32, one of
+ *                      block-128: [ceil(N/128), ceil(K/128)]
+ *                                 (the weight_scale_inv dequant multiplier)
+ *                      per-channel: [N, 1]  (block 1 x K)
+ *   act codes q      E4M3FN [M, K]
+ *   act scales s     f32 [M, K / group_k]; group_k is 128 or K
+ *   output c         bf16 or f32 [M, N]
+ *
+ * Arithmetic: c[m,n] = sum over 128-wide K chunks j of
+ *     sa[m, j*128/group_k] * sw[n/bn, j*128/bk] * sum_{k in j} q[m,k]*w[n,k]
+ * with fp32 accumulation, then (ADD_RESIDUAL) + f32(c[m,n]), then the cast.
+ * Activation quantization per group: scale = amax/448 (1.0 when below
+ * 1e-12), q = e4m3_rne(x * (1/scale)).
+ *
+ * Requirements: K % 128 == 0, N % 16 == 0, M >= 1, 16-byte aligned
+ * pointers for x, w, q and c.
+ */
+#ifndef HEPHFP8_H
+#define HEPHFP8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HEPH_ABI_VERSION 1
+
+/* status codes */
+#define HEPH_OK                 0
+#define HEPH_ERR_NULL         (-1)  /* a required pointer is NULL */
+#define HEPH_ERR_SHAPE        (-2)  /* M, N or K out of range / not aligned */
+#define HEPH_ERR_ALIGN        (-3)  /* pointer not 16-byte aligned */
+#define HEPH_ERR_GROUP        (-4)  /* group_k or weight block unsupported */
+#define HEPH_ERR_DTYPE        (-5)  /* unknown output dtype */
+#define HEPH_ERR_WORKSPACE    (-6)  /* workspace smaller than required */
+#define HEPH_ERR_FLAGS        (-7)  /* unknown or contradictory flags */
+#define HEPH_ERR_DEVICE       (-8)  /* current device is not gfx950 */
+#define HEPH_ERR_LAUNCH       (-9)  /* HIP reported an error at launch */
+
+/* output dtypes */
+#define HEPH_DTYPE_BF16 0
+#define HEPH_DTYPE_F32  1
+
+/* flags for heph_fp8_linear / heph_bf16_linear */
+#define HEPH_FLAG_ADD_RESIDUAL 0x1  /* c += result (c is read, then written) */
+#define HEPH_FLAG_SKIP_QUANT   0x2  /* q_ws / s_ws already hold this x's codes */
+#define HEPH_FLAG_FORCE_SKINNY 0x4  /* use the M <= 32 kernel (tests) */
+#define HEPH_FLAG_FORCE_GEMM   0x8  /* use the tiled MFMA GEMM (tests) */
+#define HEPH_FLAG_NO_FUSE      0x10 /* quantize in its own kernel (tests) */
+
+/* Largest M served by the weight-streaming (skinny) kernel. */
+#define HEPH_SKINNY_MAX_M 32
+
+/*
+ * Dynamic activation quantization, bf16 [M,K] -> E4M3 codes + f32 scales.
+ * Replaces quantize_act_rows_fp8 / quantize_act_fp8_pad
+ * (reference src/hephaestus/kernels.mojo:196-211, :270-287); group_k == K is
+ * the reference's per-token quantizer, group_k == 128 the 1x128 groups.
+ * scales has M * (K / group_k) floats.
+ */
+int heph_fp8_quant_act(const uint16_t* x_bf16, uint8_t* q, float* scales,
+                       int M, int K, int group_k, void* stream);
+
+/*
+ * Block weight quantization, bf16 [N,K] -> E4M3 codes [N,K] + f32
+ * scale_inv [ceil(N/128), K/128]: per 128x128 block s = amax/448 (1.0 when
+ * amax is 0 or s < 1e-12), codes = e4m3(w / s). Produces the
+ * weight / weight_scale_inv format from a bf16 tensor. Replaces the
+ * reference's offline per-row quantizer
+ * (reference scripts/stage_tiny_fp8_from_bf16.py:59-71) with its block form.
+ */
+int heph_fp8_quant_weight(const uint16_t* w_bf16, uint8_t* q, float* scale_inv,
+                          int N, int K, void* stream);
+
+/*
+ * W8A8 linear: c = x @ dequant(w)^T with dynamic activation quantization.
+ * Replaces linear_fp8, linear_add_residual_fp8 and gemv_fp8
+ * (reference src/hephaestus/kernels.mojo:372-407, :410-470, :473-527):
+ *   c, c_dtype           the reference's `c` (or `residual` with
+ *                        HEPH_FLAG_ADD_RESIDUAL, updated in place)
+ *   x_bf16               `a`
+ *   w, w_scale           `w`, `scale` (block given by w_block_n/w_block_k:
+ *                        (128,128) or (1,K))
+ *   q_ws, s_ws           `a_fp8_ws`, `act_scale_ws`; sizes in bytes / floats
+ *   M, N, K              `m`, `n`, `k`
+ *   group_k              activation group: 128 or K
+ *   flags                HEPH_FLAG_SKIP_QUANT is the reference's
+ *                        do_quantize=False
+ *   stream               the stream of the reference's DeviceContext
+ * On return the workspaces hold x's codes and scales (unless SKIP_QUANT),
+ * so later calls on the same x can pass SKIP_QUANT.
+ */
+int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16,
+                    const uint8_t* w, const float* w_scale, int w_block_n,
+                    int w_block_k, uint8_t* q_ws, size_t q_ws_bytes,
+                    float* s_ws, size_t s_ws_floats, int M, int N, int K,
+                    int group_k, int flags, void* stream);
+
+/*
+ * Unquantized bf16 linear with f32 accumulation: c = x @ w^T.
+ * Replaces `linear` for the lm_head (reference
+ * src/hephaestus/kernels.mojo:89-121, which keeps F32 logits); accepts
+ * M <= 32 (the decode and batched-decode rows). flags: ADD_RESIDUAL only.
+ */
+int heph_bf16_linear(void* c, int c_dtype, const uint16_t* x_bf16,
+                     const uint16_t* w_bf16, int M, int N, int K, int flags,
+                     void* stream);
+
+/* Workspace sizes heph_fp8_linear needs for (M, K, group_k). */
+size_t heph_fp8_q_ws_bytes(int M, int K);
+size_t heph_fp8_s_ws_floats(int M, int K, int group_k);
+
+/* Message for a status code (static storage). */
+const char* heph_strerror(int status);
+
+/* HEPH_ABI_VERSION of the built library. */
+int heph_abi_version(void);
+
+/*
+ * Timing hook: the next heph_fp8_linear / heph_bf16_linear call on the
+ * calling thread records start_event at the begin of its first kernel and
+ * stop_event at the end of its last kernel (hipEvent_t, stamped through
+ * hipExtLaunchKernel); a call that runs one kernel (fused quantization, or
+ * SKIP_QUANT) times exactly that kernel. Cleared after one call.
+ * No counterpart in the reference; it exists for kernel-duration
+ * measurement without a profiler.
+ */
+int heph_profile_next_launch(void* start_event, void* stop_event);
+
+/* Name of the main kernel the last call on this thread selected. */
+const char* heph_last_kernel(void);
+
+/*
+ * Launch-shape overrides for measurement sweeps (process-wide; 0 restores
+ * the built-in choice). No counterpart in the reference.
+ *   HEPH_TUNE_SKINNY_WAVES  waves per workgroup of the M <= 32 kernel:
+ *                           0, 2, 4, 8 or 16
+ *   HEPH_TUNE_SKINNY_U      chunks per load batch: 0, 2 or 4
+ */
+#define HEPH_TUNE_SKINNY_WAVES 1
+#define HEPH_TUNE_SKINNY_U     2
+int heph_set_tuning(int knob, int value);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HEPHFP8_H */

@@ -1,0 +1,136 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+include/hephfp8.h declares, and rejects bad calls with status codes before
+touching a device (the reference only debug_asserts its preconditions,
+src/hephaestus/wmma_gfx12.mojo:731-732, :872-874, :996-1005)."""
+import ctypes
+
+import pytest
+
+from hephaestus_amd import _lib as L
+
+FAKE = 0x10000          # 16-byte aligned, never dereferenced by validation
+ODD = 0x10001
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return L.lib()
+
+
+def test_exports_every_declared_symbol(lib):
+    names = L.header_functions()
+    assert len(names) >= 9
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(L.SIGNATURES) == set(names)
+
+
+def test_version_and_strerror(lib):
+    assert lib.heph_abi_version() == 1
+    for code in range(0, -10, -1):
+        msg = L.strerror(code)
+        assert msg and msg != "unknown status", code
+    assert L.strerror(-99) == "unknown status"
+
+
+def test_workspace_sizes(lib):
+    assert lib.heph_fp8_q_ws_bytes(4, 2560) == 4 * 2560
+    assert lib.heph_fp8_s_ws_floats(4, 2560, 128) == 4 * 20
+    assert lib.heph_fp8_s_ws_floats(4, 2560, 2560) == 4
+    assert lib.heph_fp8_s_ws_floats(4, 2560, 100) == 0
+    assert lib.heph_fp8_q_ws_bytes(0, 2560) == 0
+
+
+def lin(lib, **kw):
+    a = dict(c=FAKE, c_dtype=0, x=FAKE, w=FAKE, sw=FAKE, bn=128, bk=128, q=FAKE,
+             qn=1 << 30, s=FAKE, sn=1 << 30, M=1, N=256, K=2560, g=128, flags=0)
+    a.update(kw)
+    return lib.heph_fp8_linear(a["c"], a["c_dtype"], a["x"], a["w"], a["sw"], a["bn"],
+                               a["bk"], a["q"], a["qn"], a["s"], a["sn"], a["M"], a["N"],
+                               a["K"], a["g"], a["flags"], None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(c=None), L.HEPH_ERR_NULL),
+    (dict(w=None), L.HEPH_ERR_NULL),
+    (dict(sw=None), L.HEPH_ERR_NULL),
+    (dict(q=None), L.HEPH_ERR_NULL),
+    (dict(s=None), L.HEPH_ERR_NULL),
+    (dict(x=None), L.HEPH_ERR_NULL),
+    (dict(M=0), L.HEPH_ERR_SHAPE),
+    (dict(N=8), L.HEPH_ERR_SHAPE),
+    (dict(N=264), L.HEPH_ERR_SHAPE),
+    (dict(K=2500), L.HEPH_ERR_SHAPE),
+    (dict(K=64, g=64), L.HEPH_ERR_SHAPE),
+    (dict(g=64), L.HEPH_ERR_GROUP),
+    (dict(g=256), L.HEPH_ERR_GROUP),
+    (dict(bn=64, bk=64), L.HEPH_ERR_GROUP),
+    (dict(bn=1, bk=128), L.HEPH_ERR_GROUP),
+    (dict(c_dtype=7), L.HEPH_ERR_DTYPE),
+    (dict(qn=2559), L.HEPH_ERR_WORKSPACE),
+    (dict(sn=19), L.HEPH_ERR_WORKSPACE),
+    (dict(M=3, qn=3 * 2560, sn=3), L.HEPH_ERR_WORKSPACE),
+    (dict(flags=0x100), L.HEPH_ERR_FLAGS),
+    (dict(flags=L.FLAG_FORCE_GEMM | L.FLAG_FORCE_SKINNY), L.HEPH_ERR_FLAGS),
+    (dict(M=33, flags=L.FLAG_FORCE_SKINNY), L.HEPH_ERR_FLAGS),
+    (dict(c=ODD), L.HEPH_ERR_ALIGN),
+    (dict(w=ODD), L.HEPH_ERR_ALIGN),
+    (dict(x=ODD), L.HEPH_ERR_ALIGN),
+    (dict(q=ODD), L.HEPH_ERR_ALIGN),
+])
+def test_linear_rejects(lib, kw, status):
+    assert lin(lib, **kw) == status
+
+
+def test_skip_quant_allows_null_x(lib):
+    # do_quantize=False needs no activation pointer; with every argument
+    # valid, a machine without a gfx950 device reports HEPH_ERR_DEVICE.
+    st = lin(lib, x=None, flags=L.FLAG_SKIP_QUANT)
+    assert st in (L.HEPH_ERR_DEVICE, L.HEPH_OK)
+
+
+def test_valid_call_without_gpu_reports_device(lib):
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    assert lin(lib) == L.HEPH_ERR_DEVICE
+    assert lin(lib, bn=1, bk=2560, g=2560, sn=1) == L.HEPH_ERR_DEVICE
+
+
+def test_quant_rejects(lib):
+    q = lib.heph_fp8_quant_act
+    assert q(None, FAKE, FAKE, 1, 2560, 128, None) == L.HEPH_ERR_NULL
+    assert q(FAKE, FAKE, FAKE, 0, 2560, 128, None) == L.HEPH_ERR_SHAPE
+    assert q(FAKE, FAKE, FAKE, 1, 2600, 128, None) == L.HEPH_ERR_SHAPE
+    assert q(FAKE, FAKE, FAKE, 1, 2560, 512, None) == L.HEPH_ERR_GROUP
+    assert q(ODD, FAKE, FAKE, 1, 2560, 128, None) == L.HEPH_ERR_ALIGN
+
+
+def test_bf16_rejects(lib):
+    b = lib.heph_bf16_linear
+    assert b(None, 1, FAKE, FAKE, 1, 151936, 2560, 0, None) == L.HEPH_ERR_NULL
+    assert b(FAKE, 1, FAKE, FAKE, 33, 151936, 2560, 0, None) == L.HEPH_ERR_SHAPE
+    assert b(FAKE, 1, FAKE, FAKE, 1, 151930, 2560, 0, None) == L.HEPH_ERR_SHAPE
+    assert b(FAKE, 3, FAKE, FAKE, 1, 151936, 2560, 0, None) == L.HEPH_ERR_DTYPE
+    assert b(FAKE, 1, FAKE, FAKE, 1, 151936, 2560, L.FLAG_SKIP_QUANT, None) == L.HEPH_ERR_FLAGS
+    assert b(FAKE, 1, FAKE, ODD, 1, 151936, 2560, 0, None) == L.HEPH_ERR_ALIGN
+
+
+def test_profile_hook_and_last_kernel(lib):
+    assert lib.heph_profile_next_launch(None, None) == 0
+    assert isinstance(lib.heph_last_kernel(), bytes)
+
+
+def test_python_mirror_rejects_host_tensors():
+    import torch
+    from hephaestus_amd import kernels as K
+    c = torch.zeros(1, 256, dtype=torch.bfloat16)
+    a = torch.zeros(1, 2560, dtype=torch.bfloat16)
+    w = torch.zeros(256, 2560, dtype=torch.uint8)
+    s = torch.ones(2, 20)
+    qws = torch.zeros(2560, dtype=torch.uint8)
+    sws = torch.zeros(20)
+    with pytest.raises(ValueError, match="device memory"):
+        K.linear_fp8(c, a, w, s, qws, sws, 1, 256, 2560)
+    with pytest.raises(ValueError, match="neither"):
+        K.linear_fp8(c, a, w, torch.ones(3, 20), qws, sws, 1, 256, 2560)

@@ -1,0 +1,338 @@
+"""GPU parity of the HIP path against the oracle (run on an MI355X).
+
+Bars: activation codes and scales bit-exact; exact-integer inputs give
+bit-exact bf16 outputs; random inputs stay within the north star's
+max-abs-rel 1e-2 of the oracle's fp32-accumulated dequant-matmul (and,
+element-wise, within bf16 output rounding plus 1e-3 of the row scale);
+kernel variants that must agree (skinny vs GEMM, fused vs separate
+quantization, fused residual vs separate add) agree bit for bit.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from hephaestus_amd import _lib as L
+from hephaestus_amd import kernels as HK
+from oracle import oracle as O
+from tests._gpu import (bf16_of, dev, f32_of_bf16, host_bf16, max_abs_rel, run_linear,
+                        smoke_codes)
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2  # north star: max-abs-rel vs the fp32-accumulated dequant-matmul
+
+SHAPES = {  # Qwen3-4B linears (N, K)
+    "q_proj": (4096, 2560), "qkv": (6144, 2560), "o_proj": (2560, 4096),
+    "gate_up": (19456, 2560), "down": (2560, 9728),
+}
+
+
+def check_close(got_bf16: np.ndarray, ref_f32: np.ndarray, what: str):
+    got = f32_of_bf16(got_bf16)
+    r = max_abs_rel(got, ref_f32)
+    assert r <= TOL, f"{what}: max-abs-rel {r:.3e} > {TOL}"
+    # element-wise: bf16 rounding of the output plus a small absolute slack
+    scale = np.abs(ref_f32).max()
+    err = np.abs(got.astype(np.float64) - ref_f32)
+    bound = 2.0 ** -8 * np.abs(ref_f32) + 1e-3 * scale
+    bad = np.flatnonzero(err > bound)
+    assert bad.size == 0, f"{what}: {bad.size} elements outside bf16 bound, first {bad[:5]}"
+    return r
+
+
+# ---------------------------------------------------------------- KATs ----
+
+def test_device_is_gfx950():
+    p = torch.cuda.get_device_properties(0)
+    assert "gfx950" in p.gcnArchName
+
+
+def test_mfma_all_ones_kat():
+    # All-ones E4M3 (0x38) through one 128-wide chunk gives 128 in every
+    # output (the reference's 16-per-16-K KAT, exp3g_fp8_wmma_gfx12.mojo:27-36).
+    M, N, K = 1, 16, 128
+    q = torch.full((M * K,), 0x38, dtype=torch.uint8, device="cuda")
+    s = torch.ones(M, dtype=torch.float32, device="cuda")
+    w = dev(np.full((N, K), 0x38, np.uint8))
+    for sw in (torch.ones(1, 1, device="cuda"), torch.ones(N, 1, device="cuda")):
+        for flags in (L.FLAG_FORCE_SKINNY, L.FLAG_FORCE_GEMM):
+            c = torch.zeros(M, N, dtype=torch.float32, device="cuda")
+            HK.linear_fp8(c, None, w, sw, q, s, M, N, K, do_quantize=False, group_k=K,
+                          flags=flags)
+            torch.cuda.synchronize()
+            assert torch.all(c == 128.0), (flags, c)
+
+
+def test_kat_1280():
+    # scale * sum(fp8(1) * bf16(1)) at N = K = 2560, scale 0.5 -> 1280
+    # (reference bench/1b-fp8-decode.md:83).
+    N = K = 2560
+    x = bf16_of(np.ones((1, K), np.float32))
+    qw = np.full((N, K), 0x38, np.uint8)
+    sw = np.full((N // 128, K // 128), 0.5, np.float32)
+    c, _, _ = run_linear(qw, sw, x, M=1, N=N, K=K)
+    assert np.all(f32_of_bf16(host_bf16(c)) == 1280.0)
+
+
+# ------------------------------------------------------- quantization ----
+
+@pytest.fixture(scope="module")
+def quant_cases():
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "quant_cases.npz"))
+    return {k: z[k] for k in z.files}
+
+
+def test_quant_codes_bit_exact_golden(quant_cases):
+    names = sorted({k.split("__")[0] for k in quant_cases})
+    for name in names:
+        x = quant_cases[f"{name}__x"]
+        M, K = x.shape
+        for tag, g in (("g128", 128), ("token", K)):
+            q = torch.zeros(M * K, dtype=torch.uint8, device="cuda")
+            s = torch.zeros(M * (K // g), dtype=torch.float32, device="cuda")
+            HK.quantize_act_rows_fp8(q, s, dev(x), M, K, group_k=g)
+            torch.cuda.synchronize()
+            qh = q.cpu().numpy().reshape(M, K)
+            sh = s.cpu().numpy().reshape(M, K // g)
+            assert np.array_equal(sh, quant_cases[f"{name}__{tag}__s"]), (name, tag)
+            bad = np.argwhere(qh != quant_cases[f"{name}__{tag}__q"])
+            assert bad.size == 0, (name, tag, bad[:8].tolist())
+
+
+@pytest.mark.parametrize("M,K", [(1, 2560), (3, 4096), (64, 9728), (1000, 2560)])
+def test_quant_codes_bit_exact_oracle(M, K):
+    x = O.gen_act_bf16(M * 7 + K, M, K, outlier_p=1e-3)
+    for g in (128, K):
+        q = torch.zeros(M * K, dtype=torch.uint8, device="cuda")
+        s = torch.zeros(M * (K // g), dtype=torch.float32, device="cuda")
+        HK.quantize_act_rows_fp8(q, s, dev(x), M, K, group_k=g)
+        torch.cuda.synchronize()
+        qo, so = O.quant_act(x, g)
+        assert np.array_equal(s.cpu().numpy().reshape(so.shape), so)
+        assert np.array_equal(q.cpu().numpy().reshape(qo.shape), qo)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_fused_quant_writes_workspace(M):
+    N, K = 256, 4096
+    x = O.gen_act_bf16(40 + M, M, K)
+    qw, sw = O.gen_weight(41, N, K)
+    _, q_ws, s_ws = run_linear(qw, sw, x, M=M, N=N, K=K)
+    assert HK.last_kernel() == "fp8_skinny_fused_m4"
+    qo, so = O.quant_act(x, 128)
+    assert np.array_equal(q_ws.cpu().numpy().reshape(M, K), qo)
+    assert np.array_equal(s_ws.cpu().numpy().reshape(M, K // 128), so)
+
+
+# ------------------------------------------------ exact-integer parity ----
+
+def lattice(n_rows, K, seed):
+    """Integers in [-8, 8] (codes of v/4, exact in E4M3), seeded; unlike the
+    reference's smoke pattern they vary along K and across rows, so a
+    transposed operand or a K permutation changes the sums."""
+    ints = np.random.default_rng(seed).integers(-8, 9, size=(n_rows, K))
+    return ints, O.e4m3_encode((ints.astype(np.float32) * 0.25))
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 16, 17, 31, 32, 33, 64, 129])
+@pytest.mark.parametrize("N,K", [(16, 128), (144, 2560), (1024, 9728)])
+def test_exact_integer_bit_exact(M, N, K):
+    ia, qa = lattice(M, K, 1000 + M)
+    iw, qw = lattice(N, K, 2000 + N)
+    sa = np.full(M * (K // 128), 2.0 ** -3, np.float32)
+    sw = np.full((-(-N // 128), K // 128), 2.0 ** -2, np.float32)
+    # |sum| <= 64 K / 16 on a 1/16 grid: exact in f32 in any order
+    ref = (ia.astype(np.float64) @ iw.astype(np.float64).T) * 0.0625 * 2.0 ** -5
+    want = bf16_of(ref.astype(np.float32))
+    for flags in ((L.FLAG_FORCE_SKINNY,) if M <= 32 else ()) + (L.FLAG_FORCE_GEMM,):
+        c, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, flags=flags, skip_quant=True,
+                             q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
+        got = host_bf16(c)
+        assert np.array_equal(got, want), (flags, np.argwhere(got != want)[:5].tolist())
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (2, 2560, 2560), (8, 2560, 2560), (16, 2560, 2560), (8, 4096, 2560), (8, 1024, 2560),
+    (32, 2560, 2560), (8, 2560, 4096), (8, 2560, 9728), (8, 9728, 2560), (8, 151936, 2560),
+    (1, 4096, 2560)])
+def test_reference_smoke_cross_kernel(M, N, K):
+    # The reference's own FP8 GEMM test and its cases
+    # (src/qwen_small_m_gemm_smoke.mojo:54-118): codes from
+    # ((i*17 + seed*31) % 17 - 8) * 0.25, which is constant over i (1.5 for
+    # A, 0.75 for W), per-channel w_scale 0.01 and per-token act_scale 0.02;
+    # small-M and prefill kernels must agree bitwise. Both must also equal
+    # the reference epilogue on the exact sum: acc*(sa*sw) at M = 1
+    # (wmma_gfx12.mojo:711-712), (acc*sa)*sw otherwise (:973, :848).
+    qa = smoke_codes(M * K, 1)
+    qw = np.full((N, K), smoke_codes(1, 2)[0], np.uint8)
+    assert np.all(qa == qa[0])
+    sa = np.full(M, 0.02, np.float32)
+    sw = np.full((N, 1), 0.01, np.float32)
+    acc = np.float32(K * 1.5 * 0.75)
+    if M == 1:
+        ref = acc * (np.float32(0.02) * np.float32(0.01))
+    else:
+        ref = (acc * np.float32(0.02)) * np.float32(0.01)
+    want = bf16_of(np.float32([ref]))[0]
+    outs = []
+    for flags in (L.FLAG_FORCE_SKINNY, L.FLAG_FORCE_GEMM):
+        c, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, group_k=K, flags=flags,
+                             skip_quant=True, q_ws=dev(qa), s_ws=dev(sa))
+        outs.append(host_bf16(c))
+    assert np.array_equal(outs[0], outs[1])
+    assert np.all(outs[0] == want)
+
+
+def test_reference_granularity_random_cross_kernel():
+    # Per-channel weights + per-token activations on random data: both
+    # kernels accumulate unscaled MFMA sums and scale once in the epilogue;
+    # each must stay within tolerance of the oracle.
+    M, N, K = 8, 2560, 2560
+    x = O.gen_act_bf16(31, M, K)
+    w = O.gen_normal(32, N * K, 0.0, 0.02).reshape(N, K)
+    qw, sw = O.quant_weight(w, 1, K)
+    outs = []
+    for flags in (L.FLAG_FORCE_SKINNY, L.FLAG_FORCE_GEMM):
+        c, _, _ = run_linear(qw, sw, x, M=M, N=N, K=K, group_k=K, flags=flags)
+        outs.append(host_bf16(c))
+    ref = O.quant_linear(x, qw, sw, group_k=K, bn=1, bk=K)
+    check_close(outs[0], ref, "per-channel skinny")
+    check_close(outs[1], ref, "per-channel gemm")
+
+
+# ----------------------------------------------------- random parity ----
+
+@pytest.mark.parametrize("name", sorted(SHAPES))
+def test_config_shapes_m1(name):
+    N, K = SHAPES[name]
+    x = O.gen_act_bf16(0, 1, K)
+    qw, sw = O.gen_weight(1000 + N + K, N, K)
+    c, q_ws, s_ws = run_linear(qw, sw, x, M=1, N=N, K=K)
+    ref = O.quant_linear(x, qw, sw)
+    check_close(host_bf16(c), ref, f"{name} M=1")
+    qo, so = O.quant_act(x, 128)
+    assert np.array_equal(q_ws.cpu().numpy().reshape(1, K), qo)
+
+
+@pytest.mark.parametrize("M", [2, 4, 8, 16, 32])
+@pytest.mark.parametrize("name", ["qkv", "down"])
+def test_small_m(M, name):
+    N, K = SHAPES[name]
+    x = O.gen_act_bf16(100 + M, M, K)
+    qw, sw = O.gen_weight(1000 + N + K, N, K)
+    c, _, _ = run_linear(qw, sw, x, M=M, N=N, K=K)
+    check_close(host_bf16(c), O.quant_linear(x, qw, sw), f"{name} M={M}")
+
+
+@pytest.mark.parametrize("M,name", [(512, "o_proj"), (512, "qkv"), (100, "down"), (129, "q_proj")])
+def test_prefill_vs_oracle(M, name):
+    N, K = SHAPES[name]
+    x = O.gen_act_bf16(300 + M, M, K, outlier_p=1e-3)    # config 3 outliers
+    qw, sw = O.gen_weight(1000 + N + K, N, K)
+    c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K)
+    assert HK.last_kernel().startswith("fp8_gemm")
+    check_close(host_bf16(c), O.quant_linear(x, qw, sw), f"{name} M={M}")
+    qo, _ = O.quant_act(x, 128)
+    assert np.array_equal(q_ws.cpu().numpy().reshape(M, K), qo)
+
+
+def test_prefill_m4096_sampled_rows():
+    # Full config-3 size on the GPU; the oracle checks 24 sampled rows
+    # (rows of C are independent) and the quant codes of every row.
+    M = 4096
+    N, K = SHAPES["gate_up"]
+    x = O.gen_act_bf16(3, M, K, outlier_p=1e-3)
+    qw, sw = O.gen_weight(1000 + N + K, N, K)
+    c, q_ws, s_ws = run_linear(qw, sw, x, M=M, N=N, K=K)
+    rows = np.sort(np.random.default_rng(0).choice(M, 24, replace=False))
+    qo, so = O.quant_act(x, 128)
+    assert np.array_equal(q_ws.cpu().numpy().reshape(M, K), qo)
+    ref = O.linear(qo[rows], so[rows], qw, sw)
+    check_close(host_bf16(c)[rows], ref, "gate_up M=4096 rows")
+
+
+# ------------------------------------------------ variant equivalence ----
+
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_fused_equals_separate_quant(M):
+    N, K = SHAPES["o_proj"]
+    x = O.gen_act_bf16(7 + M, M, K)
+    qw, sw = O.gen_weight(5, N, K)
+    a, _, _ = run_linear(qw, sw, x, M=M, N=N, K=K)
+    b, _, _ = run_linear(qw, sw, x, M=M, N=N, K=K, flags=L.FLAG_NO_FUSE)
+    assert np.array_equal(host_bf16(a), host_bf16(b))
+
+
+@pytest.mark.parametrize("M", [1, 5, 40])
+def test_fused_residual_equals_separate_add(M):
+    N, K = 1024, 2560
+    x = O.gen_act_bf16(9, M, K)
+    qw, sw = O.gen_weight(6, N, K)
+    r = bf16_of(O.gen_normal(10, M * N).reshape(M, N))
+    v, _, _ = run_linear(qw, sw, x, M=M, N=N, K=K, out=torch.float32)
+    c, _, _ = run_linear(qw, sw, x, M=M, N=N, K=K, residual=dev(r))
+    want = bf16_of(v.cpu().numpy() + f32_of_bf16(r))
+    assert np.array_equal(host_bf16(c), want)
+
+
+def test_skip_quant_reuses_workspace():
+    # q, k and v share one quantization (reference forward.mojo:434-472).
+    M, K = 1, 2560
+    x = O.gen_act_bf16(12, M, K)
+    qw1, sw1 = O.gen_weight(13, 4096, K)
+    qw2, sw2 = O.gen_weight(14, 1024, K)
+    c1, q_ws, s_ws = run_linear(qw1, sw1, x, M=M, N=4096, K=K)
+    c2, _, _ = run_linear(qw2, sw2, None, M=M, N=1024, K=K, skip_quant=True,
+                          q_ws=q_ws, s_ws=s_ws)
+    c3, _, _ = run_linear(qw2, sw2, x, M=M, N=1024, K=K)
+    assert np.array_equal(host_bf16(c2), host_bf16(c3))
+
+
+def test_f32_output_and_stream():
+    M, N, K = 3, 512, 1024
+    x = O.gen_act_bf16(15, M, K)
+    qw, sw = O.gen_weight(16, N, K)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        c = torch.zeros(M, N, dtype=torch.float32, device="cuda")
+        q_ws, s_ws = HK.workspace(M, K)
+        HK.linear_fp8(c, dev(x), dev(qw), dev(sw), q_ws, s_ws, M, N, K, ctx=s)
+    s.synchronize()
+    ref = O.quant_linear(x, qw, sw)
+    # f32 output: the FP8 MFMA's own sums are not fp32-exact (about 2e-5 of
+    # max|C| measured on gfx950), so the bound sits above that, far below
+    # the 1e-2 parity bar.
+    assert max_abs_rel(c.cpu().numpy(), ref) < 1e-4
+
+
+# --------------------------------------------------------- bf16 lm_head ----
+
+@pytest.mark.parametrize("M", [1, 4, 32])
+def test_bf16_lm_head(M):
+    N, K = 151936, 2560
+    x = O.gen_act_bf16(20 + M, M, K)
+    w = bf16_of(O.gen_normal(21, N * K, 0.0, 0.02)).reshape(N, K)
+    c = torch.zeros(M, N, dtype=torch.float32, device="cuda")
+    HK.linear(c, dev(x), dev(w), M, N, K)
+    torch.cuda.synchronize()
+    got = c.cpu().numpy()
+    ref = O.bf16_linear(x, w)
+    assert max_abs_rel(got, ref) < 1e-5
+    # greedy argmax agrees (lowest index on ties, reference kernels.mojo:1424-1428)
+    g, r = got.argmax(axis=1), ref.argmax(axis=1)
+    for i in range(M):
+        assert g[i] == r[i] or abs(ref[i, g[i]] - ref[i, r[i]]) <= 1e-5 * np.abs(ref).max()
+
+
+# ------------------------------------------------------------ errors ----
+
+def test_errors_raise():
+    c = torch.zeros(1, 100, dtype=torch.bfloat16, device="cuda")
+    x = torch.zeros(1, 256, dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(100, 256, dtype=torch.uint8, device="cuda")
+    q, s = HK.workspace(1, 256)
+    with pytest.raises(HK.HephError) as e:
+        HK.linear_fp8(c, x, w, torch.ones(1, 2, device="cuda"), q, s, 1, 100, 256)
+    assert e.value.status == L.HEPH_ERR_SHAPE
