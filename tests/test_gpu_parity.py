@@ -336,3 +336,76 @@ def test_errors_raise():
     with pytest.raises(HK.HephError) as e:
         HK.linear_fp8(c, x, w, torch.ones(1, 2, device="cuda"), q, s, 1, 100, 256)
     assert e.value.status == L.HEPH_ERR_SHAPE
+
+
+# --------------------------------------------- scales, weights, graphs ----
+
+def test_scale_tables_every_bf16_amax():
+    # One 128-group per positive finite bf16 value v: the group holds v at a
+    # position that moves with the group, and v/2, v/3 ... elsewhere, so
+    # every possible amax is met once; scales and codes must match the
+    # oracle bit for bit (the table path replaces a division).
+    vals = np.arange(0x0001, 0x7F80, dtype=np.uint32)          # +finite bf16
+    G = vals.size
+    v = O.bf16_to_f32(vals.astype(np.uint16))
+    frac = np.linspace(-0.99, 0.99, 128).astype(np.float32)
+    grp = (v[:, None] * frac[None, :]).astype(np.float32)
+    grp[np.arange(G), np.arange(G) % 128] = v
+    K = 2560
+    rows = -(-G * 128 // K)
+    flat = np.zeros(rows * K, np.float32)
+    flat[: G * 128] = grp.reshape(-1)
+    x = bf16_of(flat).reshape(rows, K)
+    q = torch.zeros(rows * K, dtype=torch.uint8, device="cuda")
+    s = torch.zeros(rows * (K // 128), dtype=torch.float32, device="cuda")
+    HK.quantize_act_rows_fp8(q, s, dev(x), rows, K, group_k=128)
+    torch.cuda.synchronize()
+    qo, so = O.quant_act(x, 128)
+    assert np.array_equal(s.cpu().numpy().reshape(so.shape), so)
+    assert np.array_equal(q.cpu().numpy().reshape(qo.shape), qo)
+
+
+@pytest.mark.parametrize("N,K", [(256, 384), (300, 2560), (19456, 2560)])
+def test_weight_quant_vs_oracle(N, K):
+    from hephaestus_amd.weights import quantize_weight_fp8
+    w = bf16_of(O.gen_normal(N + K, N * K, 0.0, 0.02)).reshape(N, K)
+    w[0, :7] = bf16_of(np.float32([0.5, -0.7, 1e-3, 0, 0, 3.0, -3.0]))   # a wide block
+    q, s = quantize_weight_fp8(dev(w))
+    torch.cuda.synchronize()
+    qo, so = O.quant_weight(f32_of_bf16(w), 128, 128)
+    assert np.array_equal(s.cpu().numpy(), so)
+    assert np.array_equal(q.cpu().numpy(), qo)
+
+
+def test_graph_capture_replays_match_eager():
+    # The linear launches are capturable (no memsets, no host sync); every
+    # replay, with eager work and syncs between, equals the eager result.
+    M, K = 1, 2560
+    shapes = [(6144, 2560), (2560, 2560)]
+    x = dev(O.gen_act_bf16(50, M, K))
+    ws = [(dev(a), dev(b)) for a, b in (O.gen_weight(51 + i, N, K) for i, (N, _) in enumerate(shapes))]
+    outs = [torch.zeros(M, N, dtype=torch.bfloat16, device="cuda") for N, _ in shapes]
+    q_ws, s_ws = HK.workspace(M, K)
+
+    def run():
+        for (N, _), (w, sw), c in zip(shapes, ws, outs):
+            HK.linear_fp8(c, x, w, sw, q_ws, s_ws, M, N, K)
+    run()
+    torch.cuda.synchronize()
+    eager = [c.clone() for c in outs]
+    stream = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        run()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            run()
+    for rep in range(4):
+        for c in outs:
+            c.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for c, e in zip(outs, eager):
+            assert torch.equal(c, e), rep
+        run()                               # eager work between replays
+        torch.cuda.synchronize()
