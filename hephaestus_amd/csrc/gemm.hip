@@ -128,9 +128,14 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8Operands op)
     lstore(0);
     __syncthreads();
 
+    // The block scale of chunk j + 1 is loaded with chunk j + 1's tiles.
+    float sw_cur = SM == 0 ? swb[0] : 1.0f, sw_nxt = 1.0f;
     for (int j = 0; j < KC; ++j) {
         const int cur = j & 1;
-        if (j + 1 < KC) gload(j + 1);
+        if (j + 1 < KC) {
+            gload(j + 1);
+            if constexpr (SM == 0) sw_nxt = swb[j + 1];
+        }
 
         i32x8 a[4], b[4];
 #pragma unroll
@@ -149,7 +154,7 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8Operands op)
 #pragma unroll
                 for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma_e4m3(a[mi], b[ni], acc[mi][ni]);
         } else {
-            const float swj = SM == 0 ? swb[j] : 1.0f;
+            const float swj = sw_cur;
             float sc[4][4];
 #pragma unroll
             for (int mi = 0; mi < 4; ++mi) {
@@ -169,6 +174,7 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8Operands op)
                 }
         }
 
+        sw_cur = sw_nxt;
         if (j + 1 < KC) lstore(cur ^ 1);
         __syncthreads();
     }
@@ -202,9 +208,258 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8Operands op)
         }
 }
 
+// ---------------------------------------------------------------------------
+// Large-M kernel: 256x256 tile per 512-thread workgroup (8 waves of 128x64,
+// 8x4 MFMA 16x16x128 each). Operand tiles reach LDS by direct DMA
+// (global_load_lds_dwordx4, 1 KB = 8 rows per instruction, no VGPR
+// staging); a 16-byte piece p of row r lands in slot p ^ (r & 7), which
+// spreads the fragment reads over the banks. Two stages of
+// A 32 KB + B 32 KB + row scales 1 KB; one barrier per 128-wide chunk:
+//   wait own DMA of chunk j -> barrier (chunk j visible everywhere, and
+//   every wave is done with the other buffer) -> DMA chunk j+1 into the
+//   other buffer -> contract chunk j.
+// The compiler does not model the DMA's LDS writes, so the waits are
+// explicit s_waitcnt vmcnt(0) plus compiler memory barriers.
+// Epilogue: accumulators staged through LDS in f32, 128 rows at a time, then
+// written as coalesced 16-byte rows (residual added before the one rounding):
+// full 128-byte lines per store, which measured far cheaper than storing
+// the MFMA layout from registers.
+namespace {
+constexpr int L_BM = 256, L_BN = 256;
+constexpr int L_WM = 128, L_WN = 64;
+constexpr int L_MT = L_WM / 16, L_NT = L_WN / 16;
+constexpr int L_STAGE_A = L_BM * kChunk, L_STAGE_B = L_BN * kChunk, L_STAGE_S = L_BM * 4;
+constexpr int L_STAGE = L_STAGE_A + L_STAGE_B + L_STAGE_S;
+
+__device__ __forceinline__ void dma16(const void* g, void* lds)
+{
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* g, void* lds)
+{
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+}
+__device__ __forceinline__ void wait_dma()
+{
+    // vmcnt(0), expcnt and lgkmcnt left at their maxima (no wait)
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    asm volatile("" ::: "memory");
+}
+}  // namespace
+
+template <int SM>
+__global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * L_STAGE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, slice = lane >> 4;
+    const int wm = wave >> 2, wn = wave & 3;
+    const int M = op.M, N = op.N, K = op.K, KC = K >> 7;
+    const int tiles_m = (M + L_BM - 1) / L_BM, tiles_n = (N + L_BN - 1) / L_BN;
+    int tm, tn;
+    tile_of_block(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+    const int m0 = tm * L_BM, n0 = tn * L_BN;
+
+    // DMA sources: wave w moves operand rows [32w, 32w+32) of A and of B
+    // (4 instructions each); lane i covers row 8q + (i >> 3) of block q and
+    // global piece (i & 7) ^ (row & 7). Rows past M (N) are clamped to the
+    // last row: they feed output rows (columns) that are never stored. One
+    // 32-bit offset per block and operand is kept, not a pointer.
+    const int lr = lane >> 3;
+    const int piece = ((lane & 7) ^ lr) * 16;     // rows 8q + lr share r & 7 = lr
+    uint32_t aoff[4], boff[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int r = wave * 32 + q * 8 + lr;
+        aoff[q] = (uint32_t)min(m0 + r, M - 1) * (uint32_t)K + piece;
+        boff[q] = (uint32_t)min(n0 + r, N - 1) * (uint32_t)K + piece;
+    }
+    const float* ssrc = op.s + (size_t)min(m0 + wave * 64 + lane, M - 1) * op.s_ld;
+
+    auto issue = [&](int j, int buf) {
+        uint8_t* st = smem + buf * L_STAGE;
+        const uint8_t* qa = op.q + (size_t)j * kChunk;
+        const uint8_t* wb = op.w + (size_t)j * kChunk;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            dma16(qa + aoff[q], st + (wave * 32 + q * 8) * kChunk);
+            dma16(wb + boff[q], st + L_STAGE_A + (wave * 32 + q * 8) * kChunk);
+        }
+        if (SM != 2 && wave < 4)
+            dma4(ssrc + j * op.s_step, st + L_STAGE_A + L_STAGE_B + wave * 256);
+    };
+
+    float swc[L_NT];
+#pragma unroll
+    for (int ni = 0; ni < L_NT; ++ni) {
+        const int n = min(n0 + wn * L_WN + ni * 16 + r16, N - 1);
+        swc[ni] = SM == 1 ? op.sw[n] : 0.0f;
+    }
+    // A wave whose columns all lie past N still reads a valid scale row
+    // (its results are never stored).
+    const int wblk = min((n0 + wn * L_WN) >> 7, (N - 1) >> 7);
+    const float* swb = op.sw + (size_t)wblk * op.sw_ld;
+
+    f32x4 acc[L_MT][L_NT];
+#pragma unroll
+    for (int mi = 0; mi < L_MT; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < L_NT; ++ni) acc[mi][ni] = f32x4{0, 0, 0, 0};
+
+    issue(0, 0);
+    // The block scale of chunk j + 1 is fetched with chunk j + 1's DMA, so
+    // the wait at the top of the next iteration covers it too.
+    float sw_cur = SM == 0 ? swb[0] : 1.0f, sw_nxt = 1.0f;
+    for (int j = 0; j < KC; ++j) {
+        const int buf = j & 1;
+        wait_dma();
+        __syncthreads();
+        if (j + 1 < KC) {
+            issue(j + 1, buf ^ 1);
+            if constexpr (SM == 0) sw_nxt = swb[j + 1];
+        }
+
+        const uint8_t* As = smem + buf * L_STAGE;
+        const uint8_t* Bs = As + L_STAGE_A;
+        const float* Ss = reinterpret_cast<const float*>(As + L_STAGE_A + L_STAGE_B);
+        const int sl0 = (slice ^ (r16 & 7)) * 16, sl1 = ((slice + 4) ^ (r16 & 7)) * 16;
+
+        i32x8 b[L_NT];
+#pragma unroll
+        for (int ni = 0; ni < L_NT; ++ni) {
+            const uint8_t* row = Bs + (wn * L_WN + ni * 16 + r16) * kChunk;
+            b[ni] = join(*reinterpret_cast<const i32x4*>(row + sl0),
+                         *reinterpret_cast<const i32x4*>(row + sl1));
+        }
+        const float swj = sw_cur;
+        sw_cur = sw_nxt;
+        if constexpr (SM == 2) {
+#pragma unroll
+            for (int mi = 0; mi < L_MT; ++mi) {
+                const uint8_t* row = As + (wm * L_WM + mi * 16 + r16) * kChunk;
+                const i32x8 a = join(*reinterpret_cast<const i32x4*>(row + sl0),
+                                     *reinterpret_cast<const i32x4*>(row + sl1));
+#pragma unroll
+                for (int ni = 0; ni < L_NT; ++ni) acc[mi][ni] = mfma_e4m3(a, b[ni], acc[mi][ni]);
+            }
+        } else {
+            // Software pipeline: the rescale FMAs of m-tile mi - 1 run while
+            // the MFMAs of m-tile mi execute, so no FMA waits on the MFMA it
+            // reads.
+            f32x4 p[2][L_NT];
+            float sc[2][4];
+#pragma unroll
+            for (int mi = 0; mi <= L_MT; ++mi) {
+                const int cur = mi & 1, prv = cur ^ 1;
+                if (mi < L_MT) {
+                    const uint8_t* row = As + (wm * L_WM + mi * 16 + r16) * kChunk;
+                    const i32x8 a = join(*reinterpret_cast<const i32x4*>(row + sl0),
+                                         *reinterpret_cast<const i32x4*>(row + sl1));
+                    const f32x4 s4 =
+                        *reinterpret_cast<const f32x4*>(Ss + wm * L_WM + mi * 16 + slice * 4);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) sc[cur][i] = s4[i] * swj;
+#pragma unroll
+                    for (int ni = 0; ni < L_NT; ++ni)
+                        p[cur][ni] = mfma_e4m3(a, b[ni], f32x4{0, 0, 0, 0});
+                }
+                if (mi > 0) {
+#pragma unroll
+                    for (int ni = 0; ni < L_NT; ++ni)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            acc[mi - 1][ni][i] +=
+                                p[prv][ni][i] * (SM == 0 ? sc[prv][i] : sc[prv][i] * swc[ni]);
+                }
+            }
+        }
+    }
+
+    // ---- epilogue: two passes of 128 rows through LDS (f32) ----
+    // Rows are padded to 260 floats (4 banks of skew per row), so every
+    // lane's address is one base plus immediate offsets.
+    constexpr int CST = L_BN + 4;
+    static_assert(128 * CST * 4 <= 2 * L_STAGE, "epilogue tile must fit the stage buffers");
+    float* Cs = reinterpret_cast<float*>(smem);
+    float* cw = Cs + (slice * 4) * CST + wn * L_WN + r16;
+    for (int pass = 0; pass < 2; ++pass) {
+        __syncthreads();
+        if (wm == pass) {
+#pragma unroll
+            for (int mi = 0; mi < L_MT; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < L_NT; ++ni)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        cw[(mi * 16 + i) * CST + ni * 16] = acc[mi][ni][i];
+        }
+        __syncthreads();
+        // 128 rows x 256 cols: each thread writes 8 consecutive outputs
+        for (int e = tid; e < 128 * (L_BN / 8); e += 512) {
+            const int r = e / (L_BN / 8);
+            const int c8 = (e % (L_BN / 8)) * 8;
+            const int grow = m0 + pass * 128 + r;
+            const int gcol = n0 + c8;
+            if (grow >= M || gcol >= N) continue;
+            const f32x4 lo = *reinterpret_cast<const f32x4*>(&Cs[r * CST + c8]);
+            const f32x4 hi = *reinterpret_cast<const f32x4*>(&Cs[r * CST + c8 + 4]);
+            float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            if constexpr (SM == 2) {
+                // reference association (acc * sa) * sw (M >= 1024 here)
+                const float sa = op.s[grow];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) v[t] = (v[t] * sa) * op.sw[gcol + t];
+            }
+            const size_t o = (size_t)grow * N + gcol;
+            if (op.c_f32) {
+                float* c = static_cast<float*>(op.c) + o;
+                if (op.residual) {
+                    const float4 r0 = *reinterpret_cast<const float4*>(c);
+                    const float4 r1 = *reinterpret_cast<const float4*>(c + 4);
+                    v[0] += r0.x; v[1] += r0.y; v[2] += r0.z; v[3] += r0.w;
+                    v[4] += r1.x; v[5] += r1.y; v[6] += r1.z; v[7] += r1.w;
+                }
+                *reinterpret_cast<float4*>(c) = make_float4(v[0], v[1], v[2], v[3]);
+                *reinterpret_cast<float4*>(c + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            } else {
+                uint16_t* c = static_cast<uint16_t*>(op.c) + o;
+                if (op.residual) {
+                    const uint4 rr = *reinterpret_cast<const uint4*>(c);
+                    v[0] += bf16lo(rr.x); v[1] += bf16hi(rr.x);
+                    v[2] += bf16lo(rr.y); v[3] += bf16hi(rr.y);
+                    v[4] += bf16lo(rr.z); v[5] += bf16hi(rr.z);
+                    v[6] += bf16lo(rr.w); v[7] += bf16hi(rr.w);
+                }
+                uint4 out;
+                out.x = f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+                out.y = f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+                out.z = f32_to_bf16(v[4]) | ((uint32_t)f32_to_bf16(v[5]) << 16);
+                out.w = f32_to_bf16(v[6]) | ((uint32_t)f32_to_bf16(v[7]) << 16);
+                *reinterpret_cast<uint4*>(c) = out;
+            }
+        }
+    }
+}
+
 hipError_t launch_fp8_gemm(const Fp8Operands& op, hipStream_t stream,
                            const LaunchTiming& t, const char** name)
 {
+    // Large M: the 256x256 DMA kernel (N % 16 == 0 keeps every 8-wide
+    // output group inside the row; its 32-bit operand offsets need
+    // M*K and N*K below 2^31). Otherwise the 128x128 kernel.
+    const bool small_offsets = (long)op.M * op.K < (1L << 31) && (long)op.N * op.K < (1L << 31);
+    if (op.M >= 1024 && small_offsets) {
+        const int tiles = ((op.M + L_BM - 1) / L_BM) * ((op.N + L_BN - 1) / L_BN);
+        *name = "fp8_gemm_256x256";
+        if (op.w_block)
+            return launch(fp8_gemm256_kernel<0>, dim3(tiles), dim3(512), 0, stream, t, op);
+        if (op.s_step == 0)
+            return launch(fp8_gemm256_kernel<2>, dim3(tiles), dim3(512), 0, stream, t, op);
+        return launch(fp8_gemm256_kernel<1>, dim3(tiles), dim3(512), 0, stream, t, op);
+    }
     const int tiles = ((op.M + BM - 1) / BM) * ((op.N + BN - 1) / BN);
     *name = "fp8_gemm_128x128";
     if (op.w_block)

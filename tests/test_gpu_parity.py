@@ -409,3 +409,46 @@ def test_graph_capture_replays_match_eager():
             assert torch.equal(c, e), rep
         run()                               # eager work between replays
         torch.cuda.synchronize()
+
+
+# ------------------------------------------------ large-M GEMM variants ----
+
+@pytest.mark.parametrize("mode", ["block", "channel_token", "channel_g128"])
+@pytest.mark.parametrize("out,resid", [("bf16", False), ("bf16", True), ("f32", False), ("f32", True)])
+def test_large_m_gemm_modes(mode, out, resid):
+    # M >= 1024 takes the 256x256 kernel; ragged M and N, every scale mode,
+    # both output types, with and without the fused residual.
+    M, N, K = 1300, 400, 1024
+    x = O.gen_act_bf16(60, M, K, outlier_p=1e-3)
+    if mode == "block":
+        qw, sw = O.gen_weight(61, N, K)
+        bn, bk, g = 128, 128, 128
+    else:
+        qw, sw = O.quant_weight(O.gen_normal(61, N * K, 0.0, 0.02).reshape(N, K), 1, K)
+        bn, bk, g = 1, K, (K if mode == "channel_token" else 128)
+    dt = torch.bfloat16 if out == "bf16" else torch.float32
+    r = O.gen_normal(62, M * N).reshape(M, N).astype(np.float32)
+    res_t = (dev(bf16_of(r)) if out == "bf16" else dev(r)) if resid else None
+    c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K, group_k=g, out=dt, residual=res_t)
+    assert HK.last_kernel() == "fp8_gemm_256x256"
+    ref = O.quant_linear(x, qw, sw, group_k=g, bn=bn, bk=bk)
+    if resid:
+        ref = ref + (f32_of_bf16(bf16_of(r)) if out == "bf16" else r)
+    got = f32_of_bf16(host_bf16(c)) if out == "bf16" else c.cpu().numpy()
+    assert max_abs_rel(got, ref) <= TOL
+    qo, _ = O.quant_act(x, g)
+    assert np.array_equal(q_ws.cpu().numpy().reshape(M, K), qo)
+
+
+@pytest.mark.parametrize("M", [1024, 1100])
+def test_large_m_exact_integer(M):
+    N, K = 272, 2560
+    ia, qa = lattice(M, K, 3000 + M)
+    iw, qw = lattice(N, K, 4000)
+    sa = np.full(M * (K // 128), 2.0 ** -3, np.float32)
+    sw = np.full((-(-N // 128), K // 128), 2.0 ** -2, np.float32)
+    ref = (ia.astype(np.float64) @ iw.astype(np.float64).T) * 0.0625 * 2.0 ** -5
+    c, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, skip_quant=True,
+                         q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
+    assert HK.last_kernel() == "fp8_gemm_256x256"
+    assert np.array_equal(host_bf16(c), bf16_of(ref.astype(np.float32)))
