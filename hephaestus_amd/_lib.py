@@ -39,6 +39,9 @@ SKINNY_MAX_M = 32
 
 TUNE_SKINNY_WAVES = 1
 TUNE_SKINNY_U = 2
+TUNE_GEMV_KS = 3
+TUNE_GEMV_WAVES = 4
+TUNE_GEMV_U = 5
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int

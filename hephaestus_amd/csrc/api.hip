@@ -151,7 +151,9 @@ int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
 
     const bool skinny = (flags & HEPH_FLAG_FORCE_SKINNY) ||
                         (!(flags & HEPH_FLAG_FORCE_GEMM) && M <= HEPH_SKINNY_MAX_M);
-    const bool fused = skinny && !skip_quant && !(flags & HEPH_FLAG_NO_FUSE) &&
+    // M = 1 takes the chunk-slot GEMV unless a kernel is forced.
+    const bool gemv = M == 1 && !(flags & (HEPH_FLAG_FORCE_SKINNY | HEPH_FLAG_FORCE_GEMM));
+    const bool fused = (skinny || gemv) && !skip_quant && !(flags & HEPH_FLAG_NO_FUSE) &&
                        group_k == kChunk && M <= kFusedMaxM;
     LaunchTiming t = take_timing();
     if (!skip_quant && !fused) {
@@ -162,8 +164,10 @@ int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
         if (e != hipSuccess) return HEPH_ERR_LAUNCH;
         t.start = nullptr;
     }
-    hipError_t e = skinny ? launch_fp8_skinny(op, fused, s, t, &g_last_kernel)
-                          : launch_fp8_gemm(op, s, t, &g_last_kernel);
+    hipError_t e;
+    if (gemv) e = launch_fp8_gemv(op, fused, s, t, &g_last_kernel);
+    else if (skinny) e = launch_fp8_skinny(op, fused, s, t, &g_last_kernel);
+    else e = launch_fp8_gemm(op, s, t, &g_last_kernel);
     return launch_status(e);
 }
 
@@ -216,7 +220,9 @@ const char* heph_last_kernel(void) { return g_last_kernel; }
 
 int heph_set_tuning(int knob, int value)
 {
-    static int waves = 0, u = 0;
+    static std::mutex mu;
+    static int waves = 0, u = 0, gks = 0, gwaves = 0, gu = 0;
+    std::lock_guard<std::mutex> lock(mu);
     switch (knob) {
     case HEPH_TUNE_SKINNY_WAVES:
         if (value != 0 && value != 2 && value != 4 && value != 8 && value != 16)
@@ -227,9 +233,23 @@ int heph_set_tuning(int knob, int value)
         if (value != 0 && value != 2 && value != 4) return HEPH_ERR_FLAGS;
         u = value;
         break;
+    case HEPH_TUNE_GEMV_KS:
+        if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
+            return HEPH_ERR_FLAGS;
+        gks = value;
+        break;
+    case HEPH_TUNE_GEMV_WAVES:
+        if (value != 0 && value != 4 && value != 8) return HEPH_ERR_FLAGS;
+        gwaves = value;
+        break;
+    case HEPH_TUNE_GEMV_U:
+        if (value != 0 && value != 1 && value != 2) return HEPH_ERR_FLAGS;
+        gu = value;
+        break;
     default: return HEPH_ERR_FLAGS;
     }
     skinny_tune(waves, u);
+    gemv_tune(gks, gwaves, gu);
     return HEPH_OK;
 }
 

@@ -66,6 +66,16 @@ hipError_t launch_fp8_skinny(const Fp8Operands& op, bool fused, hipStream_t stre
 // Overrides for the skinny kernel's launch shape (0 = automatic).
 void skinny_tune(int waves, int u);
 
+// M = 1 kernel with K-chunk slots in the MFMA rows. fused: quantize x
+// inside the kernel (group 128); workgroup 0 also writes q/s.
+hipError_t launch_fp8_gemv(const Fp8Operands& op, bool fused, hipStream_t stream,
+                           const LaunchTiming& t, const char** name);
+
+// Its launch shape (chunk slots, waves, steps per batch) for N x K, and
+// overrides of each (0 = automatic).
+void gemv_shape(int N, int K, int* ks, int* waves, int* u);
+void gemv_tune(int ks, int waves, int u);
+
 // Tiled MFMA GEMM for any M (prefill); reads q/s from the workspace.
 hipError_t launch_fp8_gemm(const Fp8Operands& op, hipStream_t stream,
                            const LaunchTiming& t, const char** name);

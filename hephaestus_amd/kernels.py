@@ -172,3 +172,9 @@ def workspace(m: int, k: int, device="cuda", group_k: int = 128):
 def last_kernel() -> str:
     """Name of the main kernel the last call on this thread launched."""
     return L.lib().heph_last_kernel().decode()
+
+
+def set_tuning(knob: int, value: int) -> None:
+    """Override one launch-shape choice process-wide (0 restores the
+    built-in choice); knobs are the TUNE_* constants of _lib."""
+    _check(L.lib().heph_set_tuning(knob, value), "set_tuning")

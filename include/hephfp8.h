@@ -147,12 +147,19 @@ const char* heph_last_kernel(void);
 /*
  * Launch-shape overrides for measurement sweeps (process-wide; 0 restores
  * the built-in choice). No counterpart in the reference.
- *   HEPH_TUNE_SKINNY_WAVES  waves per workgroup of the M <= 32 kernel:
+ *   HEPH_TUNE_SKINNY_WAVES  waves per workgroup of the 2 <= M <= 32 kernel:
  *                           0, 2, 4, 8 or 16
  *   HEPH_TUNE_SKINNY_U      chunks per load batch: 0, 2 or 4
+ *   HEPH_TUNE_GEMV_KS       K-chunk slots per MFMA of the M = 1 kernel:
+ *                           0, 1, 2, 4 or 8
+ *   HEPH_TUNE_GEMV_WAVES    waves per workgroup of the M = 1 kernel: 0, 4, 8
+ *   HEPH_TUNE_GEMV_U        steps per load batch of the M = 1 kernel: 0, 1, 2
  */
 #define HEPH_TUNE_SKINNY_WAVES 1
 #define HEPH_TUNE_SKINNY_U     2
+#define HEPH_TUNE_GEMV_KS      3
+#define HEPH_TUNE_GEMV_WAVES   4
+#define HEPH_TUNE_GEMV_U       5
 int heph_set_tuning(int knob, int value);
 
 #ifdef __cplusplus

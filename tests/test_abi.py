@@ -116,6 +116,21 @@ def test_bf16_rejects(lib):
     assert b(FAKE, 1, FAKE, ODD, 1, 151936, 2560, 0, None) == L.HEPH_ERR_ALIGN
 
 
+def test_set_tuning_validates(lib):
+    ok = [(L.TUNE_SKINNY_WAVES, 16), (L.TUNE_SKINNY_U, 4), (L.TUNE_GEMV_KS, 8),
+          (L.TUNE_GEMV_WAVES, 4), (L.TUNE_GEMV_U, 2)]
+    bad = [(L.TUNE_SKINNY_WAVES, 3), (L.TUNE_SKINNY_U, 1), (L.TUNE_GEMV_KS, 16),
+           (L.TUNE_GEMV_WAVES, 16), (L.TUNE_GEMV_U, 4), (99, 0)]
+    try:
+        for knob, v in ok:
+            assert lib.heph_set_tuning(knob, v) == L.HEPH_OK, (knob, v)
+        for knob, v in bad:
+            assert lib.heph_set_tuning(knob, v) == L.HEPH_ERR_FLAGS, (knob, v)
+    finally:
+        for knob, _ in ok:
+            assert lib.heph_set_tuning(knob, 0) == L.HEPH_OK
+
+
 def test_profile_hook_and_last_kernel(lib):
     assert lib.heph_profile_next_launch(None, None) == 0
     assert isinstance(lib.heph_last_kernel(), bytes)

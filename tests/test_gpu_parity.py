@@ -57,7 +57,7 @@ def test_mfma_all_ones_kat():
     s = torch.ones(M, dtype=torch.float32, device="cuda")
     w = dev(np.full((N, K), 0x38, np.uint8))
     for sw in (torch.ones(1, 1, device="cuda"), torch.ones(N, 1, device="cuda")):
-        for flags in (L.FLAG_FORCE_SKINNY, L.FLAG_FORCE_GEMM):
+        for flags in (0, L.FLAG_FORCE_SKINNY, L.FLAG_FORCE_GEMM):
             c = torch.zeros(M, N, dtype=torch.float32, device="cuda")
             HK.linear_fp8(c, None, w, sw, q, s, M, N, K, do_quantize=False, group_k=K,
                           flags=flags)
@@ -120,7 +120,7 @@ def test_fused_quant_writes_workspace(M):
     x = O.gen_act_bf16(40 + M, M, K)
     qw, sw = O.gen_weight(41, N, K)
     _, q_ws, s_ws = run_linear(qw, sw, x, M=M, N=N, K=K)
-    assert HK.last_kernel() == "fp8_skinny_fused_m4"
+    assert HK.last_kernel() == ("fp8_gemv_fused_m1" if M == 1 else "fp8_skinny_fused_m4")
     qo, so = O.quant_act(x, 128)
     assert np.array_equal(q_ws.cpu().numpy().reshape(M, K), qo)
     assert np.array_equal(s_ws.cpu().numpy().reshape(M, K // 128), so)
@@ -146,7 +146,8 @@ def test_exact_integer_bit_exact(M, N, K):
     # |sum| <= 64 K / 16 on a 1/16 grid: exact in f32 in any order
     ref = (ia.astype(np.float64) @ iw.astype(np.float64).T) * 0.0625 * 2.0 ** -5
     want = bf16_of(ref.astype(np.float32))
-    for flags in ((L.FLAG_FORCE_SKINNY,) if M <= 32 else ()) + (L.FLAG_FORCE_GEMM,):
+    forced = ((L.FLAG_FORCE_SKINNY,) if M <= 32 else ()) + (L.FLAG_FORCE_GEMM,)
+    for flags in ((0,) if M == 1 else ()) + forced:
         c, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, flags=flags, skip_quant=True,
                              q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
         got = host_bf16(c)
@@ -177,11 +178,12 @@ def test_reference_smoke_cross_kernel(M, N, K):
         ref = (acc * np.float32(0.02)) * np.float32(0.01)
     want = bf16_of(np.float32([ref]))[0]
     outs = []
-    for flags in (L.FLAG_FORCE_SKINNY, L.FLAG_FORCE_GEMM):
+    for flags in ((0,) if M == 1 else ()) + (L.FLAG_FORCE_SKINNY, L.FLAG_FORCE_GEMM):
         c, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, group_k=K, flags=flags,
                              skip_quant=True, q_ws=dev(qa), s_ws=dev(sa))
         outs.append(host_bf16(c))
-    assert np.array_equal(outs[0], outs[1])
+    for o in outs[1:]:
+        assert np.array_equal(outs[0], o)
     assert np.all(outs[0] == want)
 
 
@@ -200,6 +202,54 @@ def test_reference_granularity_random_cross_kernel():
     ref = O.quant_linear(x, qw, sw, group_k=K, bn=1, bk=K)
     check_close(outs[0], ref, "per-channel skinny")
     check_close(outs[1], ref, "per-channel gemm")
+
+
+@pytest.mark.parametrize("N,K", [(16, 128), (48, 384), (2560, 1152), (2560, 9728)])
+def test_gemv_every_launch_shape(N, K):
+    # The M = 1 kernel at every chunk-slot count, wave count and batch depth,
+    # including step counts that leave a ragged last step (K/128 = 1, 3, 9,
+    # 76 chunks) and grids of a single workgroup: exact-integer inputs stay
+    # bit-exact, fused quantization stays within tolerance of the oracle and
+    # equals the separate quantizer bit for bit, and per-channel weights with
+    # per-token activations match the reference epilogue within tolerance.
+    ia, qa = lattice(1, K, 500 + K)
+    iw, qw = lattice(N, K, 600 + N)
+    sa = np.full(K // 128, 2.0 ** -3, np.float32)
+    sw = np.full((-(-N // 128), K // 128), 2.0 ** -2, np.float32)
+    want = bf16_of(((ia.astype(np.float64) @ iw.astype(np.float64).T) * 2.0 ** -9)
+                   .astype(np.float32))
+    x = O.gen_act_bf16(700 + N + K, 1, K)
+    rw = O.gen_normal(701 + N, N * K, 0.0, 0.02).reshape(N, K)
+    bq, bs = O.quant_weight(rw)
+    cq, cs = O.quant_weight(rw, 1, K)
+    ref_b = O.quant_linear(x, bq, bs)
+    ref_c = O.quant_linear(x, cq, cs, group_k=K, bn=1, bk=K)
+    ref_bc = O.quant_linear(x, cq, cs, group_k=128, bn=1, bk=K)
+    try:
+        for ks in (1, 2, 4, 8):
+            for waves in (4, 8):
+                for u in (1, 2):
+                    HK.set_tuning(L.TUNE_GEMV_KS, ks)
+                    HK.set_tuning(L.TUNE_GEMV_WAVES, waves)
+                    HK.set_tuning(L.TUNE_GEMV_U, u)
+                    cfg = (ks, waves, u)
+                    c, _, _ = run_linear(qw, sw, None, M=1, N=N, K=K, skip_quant=True,
+                                         q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
+                    assert HK.last_kernel() == "fp8_gemv_m1"
+                    got = host_bf16(c)
+                    assert np.array_equal(got, want), (cfg, np.argwhere(got != want)[:5].tolist())
+                    f, _, _ = run_linear(bq, bs, x, M=1, N=N, K=K)
+                    assert HK.last_kernel() == "fp8_gemv_fused_m1"
+                    check_close(host_bf16(f), ref_b, f"fused {cfg}")
+                    nf, _, _ = run_linear(bq, bs, x, M=1, N=N, K=K, flags=L.FLAG_NO_FUSE)
+                    assert np.array_equal(host_bf16(f), host_bf16(nf)), cfg
+                    pc, _, _ = run_linear(cq, cs, x, M=1, N=N, K=K, group_k=K)
+                    check_close(host_bf16(pc), ref_c, f"per-token {cfg}")
+                    pf, _, _ = run_linear(cq, cs, x, M=1, N=N, K=K)
+                    check_close(host_bf16(pf), ref_bc, f"per-channel fused {cfg}")
+    finally:
+        for knob in (L.TUNE_GEMV_KS, L.TUNE_GEMV_WAVES, L.TUNE_GEMV_U):
+            HK.set_tuning(knob, 0)
 
 
 # ----------------------------------------------------- random parity ----
