@@ -48,6 +48,23 @@ Q_PROJ = ("q_proj", 4096, 2560)
 LM_HEAD = ("lm_head", 151936, 2560)
 
 
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "fp8_gemv_m1_pmc_traffic.md")
+
+
+def profiled_traffic():
+    """HBM bytes per step measured by the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated by a copy of known size), or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_step:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def fp8_bytes(M, N, K):
     return N * K + (-(-N // 128)) * (K // 128) * 4 + M * K * 2 + M * N * 2
 
@@ -64,7 +81,36 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="skip the detail sweeps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="only run the M = 1 launches eagerly plus a 256 MiB device "
+                         "copy (for rocprofv3 --pmc traffic counts); prints no JSON")
     return ap.parse_args()
+
+
+def pmc_pass(steps):
+    """Eager M = 1 launches of every shape and one plain copy of known size.
+
+    Under rocprofv3 --pmc FETCH_SIZE (or WRITE_SIZE) the copy kernel's count
+    calibrates the counter: bytes = count * (copy bytes / copy count)."""
+    import torch
+    from hephaestus_amd import kernels as HK
+    torch.cuda.set_device(0)
+    lins = [Linear(n, N, K, 1, seed=100 + i) for i, (n, N, K) in enumerate(SHAPES)]
+    for lin in lins:
+        x = act(1, lin.K, seed=lin.K)
+        c = torch.empty(1, lin.N, dtype=torch.bfloat16, device="cuda")
+        for _ in range(steps):
+            w, s = lin.next()
+            HK.linear_fp8(c, x, w, s, lin.q_ws, lin.s_ws, 1, lin.N, lin.K)
+        torch.cuda.synchronize()
+        print(f"pmc-pass {lin.name} N={lin.N} K={lin.K} kernel={HK.last_kernel()} "
+              f"launches={steps}", flush=True)
+    a = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print("pmc-pass copy 268435456 bytes x3", flush=True)
 
 
 class Linear:
@@ -118,6 +164,9 @@ def main():
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the FP8 linear path has no multi-GPU mode here)", file=sys.stderr)
         sys.exit(2)
+    if args.pmc_pass:
+        pmc_pass(max(1, min(args.steps, 20)))
+        return
     import torch
     from hephaestus_amd import kernels as HK
     from hephaestus_amd.timing import KernelTimer
@@ -213,7 +262,10 @@ def main():
                    "arch": props.gcnArchName},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": kernel_names[-1],
+                     "traffic": profiled_traffic(),
+                     "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE per step, "
+                                       "profiles/fp8_gemv_m1_pmc_traffic.md",
+                     "kernel": kernel_names[-1],
                      "bytes_per_step": step_bytes},
         "cpu_baseline": cpu,
         "detail": detail,
