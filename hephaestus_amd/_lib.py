@@ -1,4 +1,5 @@
-"""ctypes binding of libhephfp8.so (the C ABI declared in include/hephfp8.h).
+"""ctypes binding of libhephfp8.so (the C ABI declared in include/hephfp8.h
+and include/hephdecode.h).
 
 The library is built in-tree by hephaestus_amd/build.py. There is no
 fallback: if the shared object is missing, loading raises.
@@ -10,8 +11,8 @@ import os
 import re
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libhephfp8.so")
-HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
-                      "include", "hephfp8.h")
+_INCLUDE = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
+HEADERS = [os.path.join(_INCLUDE, "hephfp8.h"), os.path.join(_INCLUDE, "hephdecode.h")]
 
 _lib = None
 
@@ -60,7 +61,17 @@ SIGNATURES = {
     "heph_profile_next_launch": (_i, [_vp, _vp]),
     "heph_last_kernel": (ctypes.c_char_p, []),
     "heph_set_tuning": (_i, [_i, _i]),
+    # hephdecode.h
+    "heph_embed_fp8": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i, _i, _vp]),
+    "heph_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, ctypes.c_float, _vp]),
+    "heph_qk_norm_rope_kv": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
+                                  ctypes.c_double, ctypes.c_float, _vp]),
+    "heph_attention_fp8kv": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "heph_silu_mul": (_i, [_vp, _vp, _vp, _i, _vp]),
+    "heph_argmax_bf16": (_i, [_vp, _vp, _i, _vp]),
 }
+
+ATTN_MAX_KEYS = 8192
 
 
 class HephLibraryMissing(ImportError):
@@ -85,10 +96,12 @@ def lib():
 
 
 def header_functions() -> list[str]:
-    """Names of the functions include/hephfp8.h declares."""
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(heph_[a-z0-9_]+)\s*\(", text)))
+    """Names of the functions include/hephfp8.h and hephdecode.h declare."""
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names.update(re.findall(r"\b(heph_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def strerror(status: int) -> str:

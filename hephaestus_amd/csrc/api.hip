@@ -25,22 +25,6 @@ constexpr int kMaxDevices = 64;
 int g_dev_ok[kMaxDevices];  // 0 unknown, 1 gfx950, -1 other
 std::mutex g_dev_mu;
 
-int check_device()
-{
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return HEPH_ERR_DEVICE;
-    if (dev < 0 || dev >= kMaxDevices) return HEPH_ERR_DEVICE;
-    int state = __atomic_load_n(&g_dev_ok[dev], __ATOMIC_ACQUIRE);
-    if (state == 0) {
-        std::lock_guard<std::mutex> lk(g_dev_mu);
-        hipDeviceProp_t p;
-        if (hipGetDeviceProperties(&p, dev) != hipSuccess) return HEPH_ERR_DEVICE;
-        state = strncmp(p.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
-        __atomic_store_n(&g_dev_ok[dev], state, __ATOMIC_RELEASE);
-    }
-    return state == 1 ? HEPH_OK : HEPH_ERR_DEVICE;
-}
-
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 LaunchTiming take_timing()
@@ -63,6 +47,26 @@ int check_quant_args(const void* x, const void* q, const void* s, int M, int K, 
 }
 
 }  // namespace
+
+namespace heph {
+
+int check_device()
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return HEPH_ERR_DEVICE;
+    if (dev < 0 || dev >= kMaxDevices) return HEPH_ERR_DEVICE;
+    int state = __atomic_load_n(&g_dev_ok[dev], __ATOMIC_ACQUIRE);
+    if (state == 0) {
+        std::lock_guard<std::mutex> lk(g_dev_mu);
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, dev) != hipSuccess) return HEPH_ERR_DEVICE;
+        state = strncmp(p.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
+        __atomic_store_n(&g_dev_ok[dev], state, __ATOMIC_RELEASE);
+    }
+    return state == 1 ? HEPH_OK : HEPH_ERR_DEVICE;
+}
+
+}  // namespace heph
 
 extern "C" {
 

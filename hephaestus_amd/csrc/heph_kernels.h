@@ -10,6 +10,10 @@
 
 namespace heph {
 
+// HEPH_OK when the current HIP device is a gfx950, else HEPH_ERR_DEVICE
+// (the answer is cached per device).
+int check_device();
+
 // Optional kernel-boundary timestamps for the main kernel of a call.
 struct LaunchTiming {
     hipEvent_t start = nullptr;

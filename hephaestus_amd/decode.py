@@ -1,0 +1,267 @@
+"""One W8A8 decode step of a Qwen3 model on the FP8 linear path.
+
+The step is the reference's `forward_fp8` (src/hephaestus/forward.mojo:359-615)
+with 128x128 block-scaled weights and an E4M3 KV cache holding one scale
+per (layer, kv head, K|V):
+
+    x = embed(token)                                     heph_embed_fp8
+    per layer:
+        xn  = rmsnorm(x, attn_norm)                      heph_rmsnorm
+        qkv = xn @ Wqkv^T          (fused quant)         heph_fp8_linear
+        q, k, v: per-head q/k norm, RoPE, k/v -> cache   heph_qk_norm_rope_kv
+        att = attention(q, K[:pos+1], V[:pos+1])         heph_attention_fp8kv
+        x  += att @ Wo^T                                 heph_fp8_linear + ADD_RESIDUAL
+        xn  = rmsnorm(x, ffn_norm)
+        gu  = xn @ Wgate_up^T
+        act = silu(gate) * up                            heph_silu_mul
+        x  += act @ Wdown^T
+    logits = rmsnorm(x, norm) @ E^T   (f32, tied FP8 embedding)
+    token  = argmax(bf16(logits)), lowest index on ties  heph_argmax_bf16
+
+Every op is a HIP kernel of libhephfp8.so; torch only holds device memory.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _lib as L
+from . import kernels as HK
+from .loader import Fp8Weight, Qwen3Config, Qwen3Fp8Weights, Qwen3Layer
+from .weights import quantize_weight_fp8
+
+
+def _ptr(t: torch.Tensor) -> int:
+    if not t.is_cuda:
+        raise ValueError("decode ops take device memory")
+    return t.data_ptr()
+
+
+def _call(name: str, *args) -> None:
+    HK._check(getattr(L.lib(), name)(*args), name)
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+# ------------------------------------------------------------- the ops ----
+
+def embed_fp8(x, emb, emb_scale, tokens, block: bool = True) -> None:
+    """x[t] = bf16(scale * e4m3(emb[tokens[t]])) (bf16 [n, hidden])."""
+    _call("heph_embed_fp8", _ptr(x), _ptr(emb), _ptr(emb_scale), int(block), _ptr(tokens),
+          tokens.numel(), emb.shape[0], emb.shape[1], _stream())
+
+
+def rmsnorm(out, x, gamma, eps: float = 1e-6) -> None:
+    rows, cols = (1, x.numel()) if x.dim() == 1 else (x.numel() // x.shape[-1], x.shape[-1])
+    _call("heph_rmsnorm", _ptr(out), _ptr(x), _ptr(gamma), rows, cols, eps, _stream())
+
+
+def qk_norm_rope_kv(qkv, q_gamma, k_gamma, k_slot, v_slot, kv_inv, n_heads: int, n_kv: int,
+                    pos: int, theta: float = 1e6, eps: float = 1e-6) -> None:
+    _call("heph_qk_norm_rope_kv", _ptr(qkv), _ptr(q_gamma), _ptr(k_gamma), _ptr(k_slot),
+          _ptr(v_slot), _ptr(kv_inv), n_heads, n_kv, 128, pos, theta, eps, _stream())
+
+
+def attention_fp8kv(out, q, k_cache, v_cache, kv_scale, n_heads: int, n_kv: int,
+                    n_keys: int) -> None:
+    _call("heph_attention_fp8kv", _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache),
+          _ptr(kv_scale), n_heads, n_kv, 128, n_keys, _stream())
+
+
+def silu_mul(out, gate, up, n: int) -> None:
+    _call("heph_silu_mul", _ptr(out), _ptr(gate), _ptr(up), n, _stream())
+
+
+def argmax_bf16(out_idx, logits) -> None:
+    _call("heph_argmax_bf16", _ptr(out_idx), _ptr(logits), logits.numel(), _stream())
+
+
+# ---------------------------------------------------------------- weights ----
+
+def _rand_fp8(g: torch.Generator, N: int, K: int, device) -> Fp8Weight:
+    w = (torch.randn(N, K, generator=g, device=device) * 0.02).to(torch.bfloat16)
+    q, s = quantize_weight_fp8(w)
+    return Fp8Weight(q, s, True)
+
+
+def _rand_gamma(g: torch.Generator, n: int, device) -> torch.Tensor:
+    return (1.0 + 0.1 * torch.randn(n, generator=g, device=device)).to(torch.bfloat16)
+
+
+def random_init(cfg: Qwen3Config, seed: int = 0, device="cuda") -> Qwen3Fp8Weights:
+    """Random-init Qwen3 weights: every linear ~N(0, 0.02) quantized per
+    128x128 block on the GPU (tied FP8 embedding), norm gammas 1 + 0.1 N(0,1)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    H, I = cfg.hidden, cfg.inter
+    out = Qwen3Fp8Weights(cfg, _rand_fp8(g, cfg.vocab, H, device), _rand_gamma(g, H, device))
+    for _ in range(cfg.n_layers):
+        out.layers.append(Qwen3Layer(
+            attn_norm=_rand_gamma(g, H, device), q_norm=_rand_gamma(g, cfg.head_dim, device),
+            k_norm=_rand_gamma(g, cfg.head_dim, device), ffn_norm=_rand_gamma(g, H, device),
+            qkv=_rand_fp8(g, cfg.q_out + 2 * cfg.kv_out, H, device),
+            o=_rand_fp8(g, H, cfg.q_out, device),
+            gate_up=_rand_fp8(g, 2 * I, H, device),
+            down=_rand_fp8(g, H, I, device)))
+    return out
+
+
+# --------------------------------------------------------------- KV cache ----
+
+class KVCache:
+    """E4M3 codes k, v [n_layers, max_ctx, n_kv, 128] with f32 scales
+    [n_layers, 2*n_kv] (K heads then V heads) and their reciprocals."""
+
+    def __init__(self, cfg: Qwen3Config, max_ctx: int, device="cuda"):
+        if max_ctx > L.ATTN_MAX_KEYS:
+            raise ValueError(f"max_ctx {max_ctx} > {L.ATTN_MAX_KEYS}")
+        shape = (cfg.n_layers, max_ctx, cfg.n_kv_heads, cfg.head_dim)
+        self.cfg, self.max_ctx = cfg, max_ctx
+        self.k = torch.zeros(shape, dtype=torch.uint8, device=device)
+        self.v = torch.zeros(shape, dtype=torch.uint8, device=device)
+        self.scale = torch.ones(cfg.n_layers, 2 * cfg.n_kv_heads, dtype=torch.float32,
+                                device=device)
+        self.inv = torch.ones_like(self.scale)
+
+    def fill_synthetic(self, n_pos: int, seed: int = 1) -> None:
+        """Rows 0..n_pos-1 from bf16 ~N(0,1) values. Each (layer, head, K|V)
+        scale is amax/448 over those rows (1.0 below 1e-12), computed on the
+        host in f32 as the quantizer does; codes = e4m3(x * (1/s))."""
+        g = torch.Generator(device=self.k.device).manual_seed(seed)
+        cfg = self.cfg
+        scale = np.ones((cfg.n_layers, 2 * cfg.n_kv_heads), np.float32)
+        for li in range(cfg.n_layers):
+            for j, dst in enumerate((self.k, self.v)):
+                x = torch.randn(n_pos, cfg.n_kv_heads, cfg.head_dim, generator=g,
+                                device=self.k.device).to(torch.bfloat16).float()
+                amax = x.abs().amax(dim=(0, 2)).cpu().numpy().astype(np.float32)
+                s = amax / np.float32(448.0)
+                s[s < np.float32(1e-12)] = np.float32(1.0)
+                inv = (np.float32(1.0) / s).astype(np.float32)
+                scale[li, j * cfg.n_kv_heads:(j + 1) * cfg.n_kv_heads] = s
+                inv_t = torch.from_numpy(inv).to(x.device).view(1, -1, 1)
+                codes = (x * inv_t).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+                dst[li, :n_pos] = codes.view(torch.uint8)
+        self.scale.copy_(torch.from_numpy(scale))
+        self.inv.copy_(torch.from_numpy((np.float32(1.0) / scale).astype(np.float32)))
+
+
+# ---------------------------------------------------------------- decoder ----
+
+class Qwen3Decoder:
+    """Holds the activations and workspaces of a single-token decode step."""
+
+    def __init__(self, weights: Qwen3Fp8Weights, kv: KVCache):
+        self.w, self.kv, cfg = weights, kv, weights.cfg
+        if not weights.embed.block:
+            raise ValueError("the decode step takes 128x128 block-scaled weights")
+        if cfg.head_dim != 128:
+            raise ValueError("head_dim must be 128")
+        dev = weights.embed.w.device
+        H, I, Q, KV = cfg.hidden, cfg.inter, cfg.q_out, cfg.kv_out
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        self.x = torch.empty(1, H, **bf)
+        self.xn = torch.empty(1, H, **bf)
+        self.qkv = torch.empty(1, Q + 2 * KV, **bf)
+        self.att = torch.empty(1, Q, **bf)
+        self.gu = torch.empty(1, 2 * I, **bf)
+        self.act = torch.empty(1, I, **bf)
+        self.logits = torch.empty(1, cfg.vocab, dtype=torch.float32, device=dev)
+        self.next_token = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.token = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.q_ws, self.s_ws = HK.workspace(1, max(H, Q, I), device=dev)
+
+    def _linear(self, c, a, fw: Fp8Weight, K: int, residual: bool = False):
+        fn = HK.linear_add_residual_fp8 if residual else HK.linear_fp8
+        fn(c, a, fw.w, fw.scale, self.q_ws, self.s_ws, 1, fw.N, K)
+
+    def step(self, token, pos: int, trace: list | None = None) -> torch.Tensor:
+        """Decode `token` (int or int32 device tensor [1]) at position pos;
+        the KV cache row pos is written. Returns the argmax token (int32
+        device tensor [1]); logits stay in self.logits. With `trace`, every
+        op's output is appended as (layer, op, host copy) after a device
+        synchronization (for op-by-op checks; slow)."""
+        cfg, w, kv = self.w.cfg, self.w, self.kv
+        if not 0 <= pos < kv.max_ctx:
+            raise ValueError(f"pos {pos} outside the cache (max_ctx {kv.max_ctx})")
+        if isinstance(token, torch.Tensor):
+            self.token.copy_(token.view(1))
+        else:
+            self.token.fill_(int(token))
+
+        def rec(li, op, t):
+            if trace is not None:
+                torch.cuda.synchronize()
+                t = t.detach()
+                a = (t.view(torch.int16).cpu().numpy().view(np.uint16) if t.dtype == torch.bfloat16
+                     else t.cpu().numpy())
+                trace.append((li, op, a.reshape(-1).copy()))
+
+        H, I, Q = cfg.hidden, cfg.inter, cfg.q_out
+        NH, NKV, eps = cfg.n_heads, cfg.n_kv_heads, cfg.eps
+        embed_fp8(self.x, w.embed.w, w.embed.scale, self.token)
+        rec(-1, "embed", self.x)
+        for li, lw in enumerate(w.layers):
+            rmsnorm(self.xn, self.x, lw.attn_norm, eps)
+            rec(li, "attn_norm", self.xn)
+            self._linear(self.qkv, self.xn, lw.qkv, H)
+            rec(li, "qkv", self.qkv)
+            qk_norm_rope_kv(self.qkv, lw.q_norm, lw.k_norm, kv.k[li, pos], kv.v[li, pos],
+                            kv.inv[li], NH, NKV, pos, cfg.theta, eps)
+            rec(li, "q_rope", self.qkv[:, :Q])
+            rec(li, "k_codes", kv.k[li, pos])
+            rec(li, "v_codes", kv.v[li, pos])
+            attention_fp8kv(self.att, self.qkv, kv.k[li], kv.v[li], kv.scale[li], NH, NKV,
+                            pos + 1)
+            rec(li, "attention", self.att)
+            self._linear(self.x, self.att, lw.o, Q, residual=True)
+            rec(li, "o_residual", self.x)
+            rmsnorm(self.xn, self.x, lw.ffn_norm, eps)
+            rec(li, "ffn_norm", self.xn)
+            self._linear(self.gu, self.xn, lw.gate_up, H)
+            rec(li, "gate_up", self.gu)
+            silu_mul(self.act, self.gu, self.gu[:, I:], I)
+            rec(li, "silu_mul", self.act)
+            self._linear(self.x, self.act, lw.down, I, residual=True)
+            rec(li, "down_residual", self.x)
+        rmsnorm(self.xn, self.x, w.final_norm, eps)
+        rec(-1, "final_norm", self.xn)
+        self._linear(self.logits, self.xn, w.embed, H)
+        rec(-1, "logits", self.logits)
+        argmax_bf16(self.next_token, self.logits)
+        rec(-1, "argmax", self.next_token)
+        return self.next_token
+
+
+def host_model(w: Qwen3Fp8Weights) -> dict:
+    """Host copies of the weights in the form oracle.decode_step takes."""
+    def u16(t):
+        return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+    cfg = w.cfg
+    m = {"cfg": {"hidden": cfg.hidden, "n_heads": cfg.n_heads, "n_kv_heads": cfg.n_kv_heads,
+                 "inter": cfg.inter, "eps": cfg.eps, "theta": cfg.theta},
+         "embed": w.embed.w.cpu().numpy(), "embed_scale": w.embed.scale.cpu().numpy(),
+         "final_norm": u16(w.final_norm), "layers": []}
+    for lw in w.layers:
+        d = {"attn_norm": u16(lw.attn_norm), "q_norm": u16(lw.q_norm), "k_norm": u16(lw.k_norm),
+             "ffn_norm": u16(lw.ffn_norm)}
+        for name in ("qkv", "o", "gate_up", "down"):
+            fw = getattr(lw, name)
+            d[name] = fw.w.cpu().numpy()
+            d[name + "_scale"] = fw.scale.cpu().numpy()
+        m["layers"].append(d)
+    return m
+
+
+def host_kv(kv: KVCache) -> dict:
+    return {"k": kv.k.cpu().numpy(), "v": kv.v.cpu().numpy(),
+            "scale": kv.scale.cpu().numpy(), "inv": kv.inv.cpu().numpy()}
+
+
+def n_params_bytes(cfg: Qwen3Config) -> int:
+    """FP8 weight bytes one decode step streams (linears + tied lm_head)."""
+    per_layer = (cfg.q_out + 2 * cfg.kv_out) * cfg.hidden + cfg.hidden * cfg.q_out + \
+        2 * cfg.inter * cfg.hidden + cfg.hidden * cfg.inter
+    return cfg.n_layers * per_layer + cfg.vocab * cfg.hidden

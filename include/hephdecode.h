@@ -1,0 +1,82 @@
+/*
+ * hephdecode.h - the non-linear ops of one Qwen3 W8A8 decode step
+ * (random-init end-to-end check of the FP8 linear path). Same conventions as
+ * hephfp8.h: device pointers, a hipStream_t as void* (NULL = default
+ * stream), HEPH_* status codes, no allocation, no synchronization.
+ *
+ * bf16 tensors are passed as their 16-bit patterns. Head size is 128.
+ */
+#ifndef HEPHDECODE_H
+#define HEPHDECODE_H
+
+#include <stdint.h>
+
+#include "hephfp8.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Longest context the attention op takes (scores are held in LDS). */
+#define HEPH_ATTN_MAX_KEYS 8192
+
+/*
+ * x[t, :] = bf16(scale * e4m3(emb[tokens[t], :])) for t < n_tok.
+ * block != 0: emb_scale is [ceil(vocab/128), hidden/128] (128x128 blocks);
+ * block == 0: one scale per row, [vocab]. A token id outside [0, vocab)
+ * gives a zero row.
+ * Replaces embed_lookup_fp8 (src/hephaestus/kernels.mojo:530-570).
+ */
+int heph_embed_fp8(void* x_bf16, const uint8_t* emb, const float* emb_scale, int block,
+                   const int32_t* tokens, int n_tok, int vocab, int hidden, void* stream);
+
+/*
+ * out = bf16(gamma * bf16(in * 1/sqrt(mean(in^2) + eps))) per row of cols;
+ * out may alias in. Replaces _rms_norm (src/hephaestus/forward.mojo:45-81).
+ */
+int heph_rmsnorm(void* out_bf16, const void* in_bf16, const void* gamma_bf16, int rows,
+                 int cols, float eps, void* stream);
+
+/*
+ * On the qkv output of one token ([n_heads + 2*n_kv_heads, 128] bf16):
+ * per-head RMSNorm of q (q_gamma) and k (k_gamma), RoPE of both at `pos`
+ * (theta), q written back in place; k and v quantized to E4M3 with
+ * code = e4m3(clamp(x * kv_inv_scale[h], +-448)) into k_slot / v_slot
+ * ([n_kv_heads, 128] codes each). kv_inv_scale: n_kv_heads K entries, then
+ * n_kv_heads V entries. Replaces the q/k _rms_norm calls and
+ * apply_rope_qk_inplace of forward.mojo:474-500 (kernels.mojo:709-796) and
+ * the cache write of k/v (forward.mojo:415-431).
+ */
+int heph_qk_norm_rope_kv(void* qkv_bf16, const void* q_gamma, const void* k_gamma,
+                         uint8_t* k_slot, uint8_t* v_slot, const float* kv_inv_scale,
+                         int n_heads, int n_kv_heads, int head_dim, int pos, double theta,
+                         float eps, void* stream);
+
+/*
+ * One query token over n_keys cached keys: out[h] = sum_j p_j * v_j with
+ * p = bf16(softmax(q.k_j * sk / sqrt(128))), K and V E4M3 codes
+ * [n_keys, n_kv_heads, 128] scaled by kv_scale (K entries, then V).
+ * Replaces attention (src/hephaestus/kernels.mojo:923-1035, :1183-1240).
+ */
+int heph_attention_fp8kv(void* out_bf16, const void* q_bf16, const uint8_t* k_cache,
+                         const uint8_t* v_cache, const float* kv_scale, int n_heads,
+                         int n_kv_heads, int head_dim, int n_keys, void* stream);
+
+/*
+ * out = bf16(bf16(g / (1 + exp(-g))) * up). Replaces silu_mul
+ * (src/hephaestus/kernels.mojo:1243-1278).
+ */
+int heph_silu_mul(void* out_bf16, const void* gate_bf16, const void* up_bf16, int n,
+                  void* stream);
+
+/*
+ * out_idx[0] = argmax_i bf16(logits[i]), lowest index on ties. Replaces
+ * argmax_logits (src/hephaestus/kernels.mojo:1376-1463).
+ */
+int heph_argmax_bf16(int32_t* out_idx, const float* logits, int n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HEPHDECODE_H */

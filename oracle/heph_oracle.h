@@ -23,6 +23,9 @@
  *                     (dequantize, f32 accumulate, C = A @ W^T) with the
  *                     per-block scales of the block-scaled format.
  *   bf16_linear       src/hephaestus/kernels.mojo:89-121 (lm_head, f32 out).
+ *   decode-step ops   heph_decode_oracle.c: embedding, RMSNorm, q/k norm +
+ *                     RoPE + KV-cache quantization, attention over an E4M3
+ *                     KV cache, SwiGLU, argmax (forward.mojo:359-615).
  */
 #ifndef HEPH_ORACLE_H
 #define HEPH_ORACLE_H
@@ -94,6 +97,24 @@ void heph_oracle_gen_uniform(uint64_t seed, uint64_t offset, size_t n,
  * before rounding to bf16. */
 void heph_oracle_gen_act_bf16(uint64_t seed, size_t n, double outlier_p,
                               float outlier_mul, uint16_t* out);
+
+/* ---- one Qwen3 decode step: the non-linear ops (heph_decode_oracle.c) --- */
+/* Same arithmetic and reduction order as hephaestus_amd/csrc/decode.hip;
+ * head size 128. */
+void heph_oracle_embed_fp8(uint16_t* x, const uint8_t* emb, const float* scale, int block,
+                           const int32_t* tokens, int n_tok, int hidden);
+void heph_oracle_rmsnorm(uint16_t* out, const uint16_t* in, const uint16_t* gamma, int rows,
+                         int cols, float eps);
+void heph_oracle_rope_cs(int pos, int p, int D, double theta, float* c, float* s);
+void heph_oracle_qk_norm_rope_kv(uint16_t* qkv, const uint16_t* q_gamma,
+                                 const uint16_t* k_gamma, uint8_t* k_slot, uint8_t* v_slot,
+                                 const float* kv_inv, int n_heads, int n_kv, int pos,
+                                 double theta, float eps);
+int heph_oracle_attention_fp8kv(uint16_t* out, const uint16_t* q, const uint8_t* kc,
+                                const uint8_t* vc, const float* kv_scale, int n_heads,
+                                int n_kv, int n_keys);
+void heph_oracle_silu_mul(uint16_t* out, const uint16_t* gate, const uint16_t* up, size_t n);
+int heph_oracle_argmax_bf16(const float* logits, size_t n);
 
 /* FNV-1a 64 digest, used for committed input/output digests. */
 uint64_t heph_oracle_fnv1a64(const void* data, size_t n);

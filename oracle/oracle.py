@@ -77,6 +77,22 @@ def lib():
         L.heph_oracle_fnv1a64.restype = ctypes.c_uint64
         L.heph_oracle_fnv1a64.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
         L.heph_oracle_num_threads.restype = ctypes.c_int
+        _i32p = ctypes.POINTER(ctypes.c_int32)
+        L.heph_oracle_embed_fp8.argtypes = [_u16p, _u8p, _f32p, ctypes.c_int, _i32p,
+                                            ctypes.c_int, ctypes.c_int]
+        L.heph_oracle_rmsnorm.argtypes = [_u16p, _u16p, _u16p, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_float]
+        L.heph_oracle_rope_cs.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_double, _f32p, _f32p]
+        L.heph_oracle_qk_norm_rope_kv.argtypes = [_u16p, _u16p, _u16p, _u8p, _u8p, _f32p,
+                                                  ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                  ctypes.c_double, ctypes.c_float]
+        L.heph_oracle_attention_fp8kv.argtypes = [_u16p, _u16p, _u8p, _u8p, _f32p,
+                                                  ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.heph_oracle_attention_fp8kv.restype = ctypes.c_int
+        L.heph_oracle_silu_mul.argtypes = [_u16p, _u16p, _u16p, ctypes.c_size_t]
+        L.heph_oracle_argmax_bf16.argtypes = [_f32p, ctypes.c_size_t]
+        L.heph_oracle_argmax_bf16.restype = ctypes.c_int
         for name in ("heph_oracle_quant_act", "heph_oracle_quant_weight",
                      "heph_oracle_linear", "heph_oracle_linear_f64",
                      "heph_oracle_quant_linear", "heph_oracle_bf16_linear"):
@@ -247,3 +263,118 @@ def digest(a: np.ndarray) -> str:
 
 def num_threads() -> int:
     return lib().heph_oracle_num_threads()
+
+
+# ---- one Qwen3 decode step (heph_decode_oracle.c) ---------------------------
+
+_i32p = ctypes.POINTER(ctypes.c_int32)
+
+
+def embed_fp8(emb: np.ndarray, scale: np.ndarray, block: bool, tokens) -> np.ndarray:
+    """bf16 rows bf16(scale * e4m3(emb[token])) (kernels.mojo:530-548)."""
+    tokens = np.ascontiguousarray(tokens, np.int32)
+    emb = np.ascontiguousarray(emb, np.uint8)
+    scale = np.ascontiguousarray(scale, np.float32)
+    H = emb.shape[1]
+    x = np.empty((tokens.size, H), np.uint16)
+    lib().heph_oracle_embed_fp8(_p(x, _u16p), _p(emb, _u8p), _p(scale, _f32p), int(block),
+                                _p(tokens, _i32p), tokens.size, H)
+    return x
+
+
+def rmsnorm(x: np.ndarray, gamma: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    """bf16(gamma * bf16(x / sqrt(mean(x^2) + eps))) per row (bf16 in/out)."""
+    x = np.ascontiguousarray(x, np.uint16)
+    g = np.ascontiguousarray(gamma, np.uint16)
+    rows, cols = (1, x.size) if x.ndim == 1 else x.shape
+    out = np.empty_like(x)
+    lib().heph_oracle_rmsnorm(_p(out, _u16p), _p(x, _u16p), _p(g, _u16p), rows, cols, eps)
+    return out
+
+
+def rope_cs(pos: int, p: int, D: int = 128, theta: float = 1e6):
+    c, s = ctypes.c_float(), ctypes.c_float()
+    lib().heph_oracle_rope_cs(pos, p, D, theta, ctypes.byref(c), ctypes.byref(s))
+    return c.value, s.value
+
+
+def qk_norm_rope_kv(qkv: np.ndarray, q_gamma, k_gamma, kv_inv, n_heads: int, n_kv: int,
+                    pos: int, theta: float = 1e6, eps: float = 1e-6):
+    """(q bf16 [n_heads*128] normalized and rotated, k codes, v codes)."""
+    qkv = np.array(qkv, dtype=np.uint16, copy=True).reshape(-1)
+    qg = np.ascontiguousarray(q_gamma, np.uint16)
+    kg = np.ascontiguousarray(k_gamma, np.uint16)
+    inv = np.ascontiguousarray(kv_inv, np.float32)
+    k = np.empty(n_kv * 128, np.uint8)
+    v = np.empty(n_kv * 128, np.uint8)
+    lib().heph_oracle_qk_norm_rope_kv(_p(qkv, _u16p), _p(qg, _u16p), _p(kg, _u16p),
+                                      _p(k, _u8p), _p(v, _u8p), _p(inv, _f32p), n_heads, n_kv,
+                                      pos, theta, eps)
+    return qkv[:n_heads * 128].copy(), k, v
+
+
+def attention_fp8kv(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, kv_scale, n_heads: int,
+                    n_kv: int, n_keys: int) -> np.ndarray:
+    """bf16 [n_heads*128]; kc / vc: E4M3 codes [>= n_keys, n_kv, 128]."""
+    q = np.ascontiguousarray(q, np.uint16)
+    kc = np.ascontiguousarray(kc, np.uint8)
+    vc = np.ascontiguousarray(vc, np.uint8)
+    sc = np.ascontiguousarray(kv_scale, np.float32)
+    out = np.empty(n_heads * 128, np.uint16)
+    _check(lib().heph_oracle_attention_fp8kv(_p(out, _u16p), _p(q, _u16p), _p(kc, _u8p),
+                                             _p(vc, _u8p), _p(sc, _f32p), n_heads, n_kv,
+                                             n_keys), "attention_fp8kv")
+    return out
+
+
+def silu_mul(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    g = np.ascontiguousarray(gate, np.uint16)
+    u = np.ascontiguousarray(up, np.uint16)
+    out = np.empty_like(g)
+    lib().heph_oracle_silu_mul(_p(out, _u16p), _p(g, _u16p), _p(u, _u16p), g.size)
+    return out
+
+
+def argmax_bf16(logits: np.ndarray) -> int:
+    x = np.ascontiguousarray(logits, np.float32)
+    return int(lib().heph_oracle_argmax_bf16(_p(x, _f32p), x.size))
+
+
+def _linear_bf16(x_bf16, qw, sw, residual=None, nthreads=0):
+    """bf16 output of the FP8 linear (block 128 scales), optionally + residual
+    in f32 before the cast (wmma_gfx12.mojo:712-715)."""
+    acc = quant_linear(np.ascontiguousarray(x_bf16, np.uint16).reshape(1, -1), qw, sw,
+                       nthreads=nthreads)[0]
+    if residual is not None:
+        acc = acc + bf16_to_f32(np.ascontiguousarray(residual, np.uint16))
+    return f32_to_bf16(acc.astype(np.float32))
+
+
+def decode_step(model: dict, kv: dict, token: int, pos: int, nthreads: int = 0):
+    """One W8A8 decode step of a Qwen3 model on the CPU (forward.mojo:359-615
+    with 128x128 block scales and an E4M3 KV cache). model: host arrays
+    (see hephaestus_amd.decode.Qwen3Decoder.host_model); kv: {"k", "v": codes
+    [L, ctx, n_kv, 128], "scale": f32 [L, 2*n_kv], "inv": f32 [L, 2*n_kv]},
+    updated in place at row `pos`. Returns (f32 logits, argmax)."""
+    cfg = model["cfg"]
+    H, NH, NKV, D = cfg["hidden"], cfg["n_heads"], cfg["n_kv_heads"], 128
+    Q, KV, I = NH * D, NKV * D, cfg["inter"]
+    eps, theta = cfg["eps"], cfg["theta"]
+    x = embed_fp8(model["embed"], model["embed_scale"], True, [token])[0]
+    for li, L in enumerate(model["layers"]):
+        xn = rmsnorm(x, L["attn_norm"], eps)
+        qkv = _linear_bf16(xn, L["qkv"], L["qkv_scale"], nthreads=nthreads)
+        q, k, v = qk_norm_rope_kv(qkv, L["q_norm"], L["k_norm"], kv["inv"][li], NH, NKV, pos,
+                                  theta, eps)
+        kv["k"][li, pos] = k.reshape(NKV, D)
+        kv["v"][li, pos] = v.reshape(NKV, D)
+        att = attention_fp8kv(q, kv["k"][li], kv["v"][li], kv["scale"][li], NH, NKV, pos + 1)
+        x = _linear_bf16(att, L["o"], L["o_scale"], residual=x, nthreads=nthreads)
+        xn = rmsnorm(x, L["ffn_norm"], eps)
+        gu = _linear_bf16(xn, L["gate_up"], L["gate_up_scale"], nthreads=nthreads)
+        act = silu_mul(gu[:I], gu[I:])
+        x = _linear_bf16(act, L["down"], L["down_scale"], residual=x, nthreads=nthreads)
+    xn = rmsnorm(x, model["final_norm"], eps)
+    logits = quant_linear(xn.reshape(1, -1), model["embed"], model["embed_scale"],
+                          nthreads=nthreads)[0]
+    return logits, argmax_bf16(logits)

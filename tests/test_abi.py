@@ -149,3 +149,21 @@ def test_python_mirror_rejects_host_tensors():
         K.linear_fp8(c, a, w, s, qws, sws, 1, 256, 2560)
     with pytest.raises(ValueError, match="neither"):
         K.linear_fp8(c, a, w, torch.ones(3, 20), qws, sws, 1, 256, 2560)
+
+
+def test_decode_ops_reject(lib):
+    assert lib.heph_embed_fp8(None, FAKE, FAKE, 1, FAKE, 1, 100, 256, None) == L.HEPH_ERR_NULL
+    assert lib.heph_embed_fp8(FAKE, FAKE, FAKE, 1, FAKE, 1, 100, 200, None) == L.HEPH_ERR_SHAPE
+    assert lib.heph_rmsnorm(FAKE, FAKE, None, 1, 2560, 1e-6, None) == L.HEPH_ERR_NULL
+    assert lib.heph_rmsnorm(FAKE, FAKE, FAKE, 0, 2560, 1e-6, None) == L.HEPH_ERR_SHAPE
+    q = lib.heph_qk_norm_rope_kv
+    assert q(FAKE, FAKE, FAKE, FAKE, None, FAKE, 32, 8, 128, 0, 1e6, 1e-6, None) == L.HEPH_ERR_NULL
+    assert q(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 32, 8, 64, 0, 1e6, 1e-6, None) == L.HEPH_ERR_SHAPE
+    assert q(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 30, 8, 128, 0, 1e6, 1e-6, None) == L.HEPH_ERR_SHAPE
+    a = lib.heph_attention_fp8kv
+    assert a(FAKE, FAKE, FAKE, FAKE, FAKE, 32, 8, 128, L.ATTN_MAX_KEYS + 1, None) == \
+        L.HEPH_ERR_SHAPE
+    assert a(FAKE, FAKE, FAKE, FAKE, FAKE, 32, 8, 128, 0, None) == L.HEPH_ERR_SHAPE
+    assert a(FAKE, FAKE, ODD, FAKE, FAKE, 32, 8, 128, 10, None) == L.HEPH_ERR_ALIGN
+    assert lib.heph_silu_mul(FAKE, FAKE, FAKE, 0, None) == L.HEPH_ERR_SHAPE
+    assert lib.heph_argmax_bf16(None, FAKE, 10, None) == L.HEPH_ERR_NULL

@@ -1,0 +1,324 @@
+"""GPU parity of the decode-step ops and the end-to-end random-init decode
+against the CPU oracle.
+
+Bars: embedding, RMSNorm, q/k norm + RoPE + KV quantization and argmax are
+bit-exact (the kernels repeat the oracle's reduction order and every
+rounding step). Attention and SwiGLU call expf, whose last bit may differ
+between the GPU and host math libraries: at least 99% of outputs
+identical, the rest within one bf16 step. The FP8 linears are within the
+linear path's tolerance (MFMA sums are not fp32-exact). End to end, every
+op of every layer is recomputed by the oracle from the GPU's own inputs
+and held to those bars, and the argmax is compared on identical logits;
+the free-running step is held to the oracle's own sensitivity.
+"""
+import time
+
+import numpy as np
+import pytest
+import torch
+
+from hephaestus_amd import _lib as L
+from hephaestus_amd import decode as DEC
+from hephaestus_amd.kernels import HephError
+from hephaestus_amd.loader import Qwen3Config
+from oracle import oracle as O
+from tests._gpu import dev
+
+pytestmark = pytest.mark.gpu
+
+
+
+def bf16_np(x):
+    return O.f32_to_bf16(np.ascontiguousarray(x, np.float32))
+
+
+def f32(b):
+    return O.bf16_to_f32(np.ascontiguousarray(b, np.uint16)).astype(np.float64)
+
+
+def host(t):
+    t = t.detach()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).cpu().numpy().view(np.uint16)
+    return t.cpu().numpy()
+
+
+def rng_bf16(seed, n, scale=1.0):
+    return bf16_np(np.random.default_rng(seed).standard_normal(n) * scale)
+
+
+def codes(rng, shape):
+    c = rng.integers(0, 0x7E, size=shape, dtype=np.uint8)
+    return c | (rng.integers(0, 2, size=shape, dtype=np.uint8) << 7)
+
+
+def test_embed_bit_exact():
+    V, H = 1000, 2560
+    rng = np.random.default_rng(0)
+    emb = codes(rng, (V, H))
+    sblk = rng.random((-(-V // 128), H // 128), dtype=np.float32)
+    toks = np.array([0, 127, 128, 999, 500], np.int32)
+    x = torch.empty(len(toks), H, dtype=torch.bfloat16, device="cuda")
+    DEC.embed_fp8(x, dev(emb), dev(sblk), dev(toks))
+    torch.cuda.synchronize()
+    assert np.array_equal(host(x), O.embed_fp8(emb, sblk, True, toks))
+
+
+@pytest.mark.parametrize("rows,cols,scale", [(3, 2560, 1.0), (1, 9728, 40.0), (2, 2560, 1e-4),
+                                             (32, 128, 1.0)])
+def test_rmsnorm_bit_exact(rows, cols, scale):
+    x = rng_bf16(cols + rows, rows * cols, scale).reshape(rows, cols)
+    g = rng_bf16(7, cols)
+    out = torch.empty(rows, cols, dtype=torch.bfloat16, device="cuda")
+    xd = dev(x)
+    DEC.rmsnorm(out, xd, dev(g))
+    DEC.rmsnorm(xd, xd, dev(g))                 # in place gives the same
+    torch.cuda.synchronize()
+    want = O.rmsnorm(x, g)
+    assert np.array_equal(host(out), want)
+    assert np.array_equal(host(xd), want)
+
+
+@pytest.mark.parametrize("pos", [0, 5, 4096, 123457])
+def test_qk_norm_rope_kv_bit_exact(pos):
+    NH, NKV = 32, 8
+    qkv = rng_bf16(pos + 1, (NH + 2 * NKV) * 128, 2.0)
+    qg, kg = rng_bf16(2, 128), rng_bf16(3, 128)
+    inv = (np.random.default_rng(4).random(2 * NKV, dtype=np.float32) * 100 + 1).astype(np.float32)
+    d = dev(qkv)
+    k = torch.zeros(NKV * 128, dtype=torch.uint8, device="cuda")
+    v = torch.zeros_like(k)
+    DEC.qk_norm_rope_kv(d, dev(qg), dev(kg), k, v, dev(inv), NH, NKV, pos, 1e6, 1e-6)
+    torch.cuda.synchronize()
+    q_o, k_o, v_o = O.qk_norm_rope_kv(qkv, qg, kg, inv, NH, NKV, pos)
+    got = host(d)
+    assert np.array_equal(got[:NH * 128], q_o)
+    assert np.array_equal(got[NH * 128:], qkv[NH * 128:])       # k, v rows untouched
+    assert np.array_equal(host(k), k_o)
+    assert np.array_equal(host(v), v_o)
+
+
+# Two bf16-rounded results of nearly equal values differ by at most one bf16
+# step of their magnitude, which is up to 2^-7 of the value (8 significant
+# bits: the step in [0.5, 1) is 2^-8).
+STEP = 2.0 ** -7
+
+
+def mostly_equal(got, want, what):
+    """>= 99% identical; the rest within one bf16 step, plus 4e-3 of the
+    largest output for sums that cancel (one probability or SiLU value that
+    rounded the other way moves an output by its own bf16 step times v)."""
+    g, w = f32(got), f32(want)
+    same = np.mean(g == w)
+    err = np.abs(g - w).max() / max(np.abs(w).max(), 1e-30)
+    assert same >= 0.99, f"{what}: only {same:.4f} identical"
+    assert np.all(np.abs(g - w) <= STEP * np.abs(w) + 4e-3 * np.abs(w).max()), \
+        f"{what}: max rel {err:.2e}"
+
+
+@pytest.mark.parametrize("n", [1, 2, 300, 4097, 8192])
+def test_attention_vs_oracle(n):
+    NH, NKV = 32, 8
+    rng = np.random.default_rng(n)
+    q = rng_bf16(n, NH * 128, 3.0)
+    kc, vc = codes(rng, (n, NKV, 128)), codes(rng, (n, NKV, 128))
+    sc = (rng.random(2 * NKV, dtype=np.float32) * 0.02 + 0.005).astype(np.float32)
+    out = torch.empty(NH * 128, dtype=torch.bfloat16, device="cuda")
+    DEC.attention_fp8kv(out, dev(q), dev(kc), dev(vc), dev(sc), NH, NKV, n)
+    torch.cuda.synchronize()
+    mostly_equal(host(out), O.attention_fp8kv(q, kc, vc, sc, NH, NKV, n), f"attention n={n}")
+
+
+def test_attention_rejects_long_context():
+    z = torch.zeros(16, dtype=torch.uint8, device="cuda")
+    with pytest.raises(HephError):
+        DEC.attention_fp8kv(z, z, z, z, z, 32, 8, L.ATTN_MAX_KEYS + 1)
+
+
+def test_silu_mul_vs_oracle():
+    g, u = rng_bf16(5, 9728, 4.0), rng_bf16(6, 9728)
+    out = torch.empty(9728, dtype=torch.bfloat16, device="cuda")
+    DEC.silu_mul(out, dev(g), dev(u), 9728)
+    torch.cuda.synchronize()
+    mostly_equal(host(out), O.silu_mul(g, u), "silu_mul")
+
+
+def test_argmax_bit_exact_and_ties():
+    idx = torch.zeros(1, dtype=torch.int32, device="cuda")
+    rng = np.random.default_rng(8)
+    for trial in range(4):
+        x = rng.standard_normal(151936).astype(np.float32)
+        if trial:
+            top = x.max()
+            x[[77 + trial, 150000]] = top + 1.0                    # exact tie
+            x[5000 * trial] = np.float32(top + 1.0 + 2.0 ** -12)   # same bf16
+        DEC.argmax_bf16(idx, dev(x))
+        torch.cuda.synchronize()
+        assert int(idx.item()) == O.argmax_bf16(x), trial
+
+
+# ------------------------------------------------------------- end to end ----
+#
+# A random-init W8A8 stack is chaotic: one bf16 ulp added to three embedding
+# elements moves the oracle's own logits by ~8% of their range (E4M3 codes
+# flip at rounding boundaries and the layers amplify it). So the strong
+# check is op by op: every op of every layer is recomputed by the oracle
+# from the GPU's own inputs and must match to that op's bar; the final
+# argmax is then compared on identical logits. The free-running step is
+# checked against the oracle's measured sensitivity.
+
+EXACT = {"embed", "attn_norm", "q_rope", "k_codes", "v_codes", "ffn_norm", "final_norm",
+         "argmax"}
+LINEAR = {"qkv", "o_residual", "gate_up", "down_residual"}
+
+
+def setup_model(cfg, ctx, seed):
+    w = DEC.random_init(cfg, seed=seed)
+    kv = DEC.KVCache(cfg, ctx + 1)
+    kv.fill_synthetic(ctx, seed=seed + 1)
+    return w, kv
+
+
+def replay(model, kvh, token, pos, trace):
+    """Oracle output of every traced op, computed from the GPU's inputs."""
+    cfg = model["cfg"]
+    NH, NKV, I, Q = cfg["n_heads"], cfg["n_kv_heads"], cfg["inter"], cfg["n_heads"] * 128
+    eps, theta = cfg["eps"], cfg["theta"]
+    got = {(li, op): a for li, op, a in trace}
+    out = []
+    x = None
+    for li, op, g in trace:
+        L = model["layers"][li] if li >= 0 else None
+        if op == "embed":
+            want = O.embed_fp8(model["embed"], model["embed_scale"], True, [token])[0]
+        elif op == "attn_norm":
+            want = O.rmsnorm(x, L["attn_norm"], eps)
+        elif op == "qkv":
+            want = O._linear_bf16(got[(li, "attn_norm")], L["qkv"], L["qkv_scale"])
+        elif op in ("q_rope", "k_codes", "v_codes"):
+            q, k, v = O.qk_norm_rope_kv(got[(li, "qkv")], L["q_norm"], L["k_norm"],
+                                        kvh["inv"][li], NH, NKV, pos, theta, eps)
+            want = {"q_rope": q, "k_codes": k, "v_codes": v}[op]
+        elif op == "attention":
+            kc, vc = kvh["k"][li].copy(), kvh["v"][li].copy()
+            kc[pos] = got[(li, "k_codes")].reshape(NKV, 128)
+            vc[pos] = got[(li, "v_codes")].reshape(NKV, 128)
+            want = O.attention_fp8kv(got[(li, "q_rope")], kc, vc, kvh["scale"][li], NH, NKV,
+                                     pos + 1)
+        elif op == "o_residual":
+            want = O._linear_bf16(got[(li, "attention")], L["o"], L["o_scale"], residual=x)
+        elif op == "ffn_norm":
+            want = O.rmsnorm(got[(li, "o_residual")], L["ffn_norm"], eps)
+        elif op == "gate_up":
+            want = O._linear_bf16(got[(li, "ffn_norm")], L["gate_up"], L["gate_up_scale"])
+        elif op == "silu_mul":
+            gu = got[(li, "gate_up")]
+            want = O.silu_mul(gu[:I], gu[I:])
+        elif op == "down_residual":
+            want = O._linear_bf16(got[(li, "silu_mul")], L["down"], L["down_scale"],
+                                  residual=got[(li, "o_residual")])
+        elif op == "final_norm":
+            want = O.rmsnorm(x, model["final_norm"], eps)
+        elif op == "logits":
+            want = O.quant_linear(got[(-1, "final_norm")].reshape(1, -1), model["embed"],
+                                  model["embed_scale"])[0]
+        elif op == "argmax":
+            want = np.array([O.argmax_bf16(got[(-1, "logits")])], np.int32)
+        else:
+            raise AssertionError(op)
+        if op in ("embed", "o_residual", "down_residual"):
+            x = g                      # the residual stream the next op reads
+        out.append((li, op, g, want))
+    return out
+
+
+def check_ops(results):
+    worst = {}
+    for li, op, g, want in results:
+        what = f"layer {li} {op}"
+        if op in EXACT:
+            assert np.array_equal(g, want), (what, np.flatnonzero(g != want)[:8])
+            continue
+        if op == "logits":
+            r = np.abs(g - want).max() / np.abs(want).max()
+            assert r <= 1e-3, (what, r)
+        elif op in ("attention", "silu_mul"):
+            mostly_equal(g, want, what)
+            r = np.abs(f32(g) - f32(want)).max() / np.abs(f32(want)).max()
+        else:
+            assert op in LINEAR
+            gg, ww = f32(g), f32(want)
+            r = np.abs(gg - ww).max() / np.abs(ww).max()
+            assert r <= 1e-2, (what, r)
+            bound = STEP * np.abs(ww) + 1e-3 * np.abs(ww).max()
+            assert np.all(np.abs(gg - ww) <= bound), (what, np.abs(gg - ww).max())
+        worst[op] = max(worst.get(op, 0.0), r)
+    print("op-by-op worst max-abs-rel: " + ", ".join(f"{k} {v:.1e}" for k, v in worst.items()),
+          flush=True)
+
+
+def op_by_op(cfg, ctx, token, seed):
+    t0 = time.time()
+    w, kv = setup_model(cfg, ctx, seed)
+    kvh = DEC.host_kv(kv)
+    trace = []
+    DEC.Qwen3Decoder(w, kv).step(token, ctx, trace=trace)
+    print(f"traced step {time.time() - t0:.1f}s, {len(trace)} ops", flush=True)
+    check_ops(replay(DEC.host_model(w), kvh, token, ctx, trace))
+    print(f"op-by-op replay done {time.time() - t0:.1f}s", flush=True)
+
+
+def free_running(cfg, ctx, token, seed):
+    w, kv = setup_model(cfg, ctx, seed)
+    kvh = DEC.host_kv(kv)
+    dec_ = DEC.Qwen3Decoder(w, kv)
+    g_idx = int(dec_.step(token, ctx).item())
+    g = dec_.logits[0].cpu().numpy().astype(np.float64)
+    model = DEC.host_model(w)
+    c, c_idx = O.decode_step(model, {k: v.copy() for k, v in kvh.items()}, token, ctx)
+    # the oracle's own sensitivity: the same step with one embedding block
+    # scale raised by a bf16 step (2^-8): the token's first 128 embedding
+    # values move by at most one bf16 step each
+    m2 = dict(model)
+    m2["embed_scale"] = model["embed_scale"].copy()
+    m2["embed_scale"][token // 128, 0] *= np.float32(1 + 2.0 ** -8)
+    p, _ = O.decode_step(m2, {k: v.copy() for k, v in kvh.items()}, token, ctx)
+    c = c.astype(np.float64)
+    err, sens = np.abs(g - c).max(), np.abs(p.astype(np.float64) - c).max()
+    cb = f32(bf16_np(c))
+    order = np.argsort(-cb, kind="stable")
+    gap = cb[order[0]] - cb[order[1]]
+    print(f"free-running: argmax gpu {g_idx} oracle {c_idx}; |gpu - oracle| {err:.3e}, "
+          f"oracle sensitivity {sens:.3e}, max|logit| {np.abs(c).max():.3e}, "
+          f"oracle top-2 gap {gap:.3e}", flush=True)
+    assert err <= 4 * max(sens, 1e-3 * np.abs(c).max()), (err, sens)
+    if gap > 2 * err:
+        assert g_idx == c_idx
+    else:
+        # a near-tie within the chaotic envelope: the GPU's pick must be one
+        # of the oracle's candidates inside it
+        assert cb[c_idx] - cb[g_idx] <= 2 * err, (g_idx, c_idx, gap, err)
+
+
+SMALL = Qwen3Config(vocab=4096, hidden=512, n_layers=3, n_heads=4, n_kv_heads=2, head_dim=128,
+                    inter=1024)
+
+
+def test_decode_small_model_op_by_op():
+    op_by_op(SMALL, ctx=300, token=1234, seed=11)
+
+
+def test_decode_small_model_free_running():
+    free_running(SMALL, ctx=300, token=1234, seed=11)
+
+
+def test_decode_qwen3_4b_config4_op_by_op():
+    # 36 layers, hidden 2560, 32/8 heads, head_dim 128, inter
+    # 9728, vocab 151936, eps 1e-6, theta 1e6; FP8 block-128 linears and
+    # tied lm_head; FP8 KV cache, per-(layer, head) scales, 4096 tokens of
+    # context from bf16 ~N(0,1); greedy argmax at position 4096.
+    op_by_op(Qwen3Config(), ctx=4096, token=12345, seed=4)
+
+
+def test_decode_qwen3_4b_config4_free_running():
+    free_running(Qwen3Config(), ctx=4096, token=12345, seed=4)
