@@ -351,12 +351,49 @@ def detail_sweeps(lins):
                              "frac": round(tf / FP8_PEAK_TFLOPS, 4)}
         pre[f"M={M}"] = row
     out["prefill"] = pre
+    out["decode_step_config4"] = decode_step_timing()
     t4096 = sum(2.0 * 4096 * l.N * l.K for l in lins)
     us4096 = sum(v["us"] for v in pre["M=4096"].values())
     out["prefill_m4096_TFLOPs"] = round(t4096 / (us4096 * 1e-6) / 1e12, 1)
     out["prefill_m4096_frac"] = round(out["prefill_m4096_TFLOPs"] / FP8_PEAK_TFLOPS, 4)
     timer.close()
     return out
+
+
+def decode_step_timing(steps=20):
+    """one random-init Qwen3-4B W8A8 decode step at position 4096
+    (36 layers, FP8 KV cache of 4096 synthetic tokens), replayed from a HIP
+    graph; ms per token and the FP8 weight bytes streamed per ms."""
+    import torch
+    from hephaestus_amd import decode as DEC
+    from hephaestus_amd.loader import Qwen3Config
+    cfg = Qwen3Config()
+    w = DEC.random_init(cfg, seed=4)
+    kv = DEC.KVCache(cfg, 4097)
+    kv.fill_synthetic(4096, seed=5)
+    dec = DEC.Qwen3Decoder(w, kv)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        dec.step(12345, 4096)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            dec.step(12345, 4096)
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    wbytes = DEC.n_params_bytes(cfg)
+    kv_bytes = cfg.n_layers * 4097 * cfg.n_kv_heads * cfg.head_dim * 2
+    return {"ms_per_token": round(ms, 4), "tokens_per_s": round(1e3 / ms, 1),
+            "fp8_weight_bytes": wbytes, "kv_bytes": kv_bytes,
+            "GBs_weights_plus_kv": round((wbytes + kv_bytes) / (ms * 1e-3) / 1e9, 1),
+            "argmax": int(dec.next_token.item())}
 
 
 def cpu_baseline(lins, xs, seconds):

@@ -66,12 +66,13 @@ SIGNATURES = {
     "heph_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, ctypes.c_float, _vp]),
     "heph_qk_norm_rope_kv": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
                                   ctypes.c_double, ctypes.c_float, _vp]),
-    "heph_attention_fp8kv": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "heph_attention_ws_bytes": (_sz, [_i, _i]),
+    "heph_attention_fp8kv": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "heph_silu_mul": (_i, [_vp, _vp, _vp, _i, _vp]),
     "heph_argmax_bf16": (_i, [_vp, _vp, _i, _vp]),
 }
 
-ATTN_MAX_KEYS = 8192
+ATTN_MAX_KEYS = 262144
 
 
 class HephLibraryMissing(ImportError):

@@ -84,24 +84,50 @@ __global__ __launch_bounds__(256) void embed_fp8_kernel(uint16_t* x, const uint8
     x[(size_t)t * hidden + d] = f32_to_bf16(s * e4m3_value(emb[id * hidden + d]));
 }
 
-// One workgroup of 256 threads per row.
+// One workgroup of 256 threads per row; thread t owns elements t, t + 256,
+// ... Rows up to kNormMax elements are loaded into registers, x and gamma
+// together, every load issued before the first use (one memory round
+// trip); longer rows loop.
+constexpr int kNormPer = 40;
+constexpr int kNormMax = 256 * kNormPer;
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* out, const uint16_t* in,
                                                       const uint16_t* gamma, int cols, float eps)
 {
     __shared__ float red[256];
     const uint16_t* x = in + (size_t)blockIdx.x * cols;
     uint16_t* y = out + (size_t)blockIdx.x * cols;
+    const int t = threadIdx.x;
+    if (cols <= kNormMax) {
+        float v[kNormPer], g[kNormPer];
+#pragma unroll
+        for (int e = 0; e < kNormPer; ++e) {
+            const int i = t + e * 256;
+            v[e] = i < cols ? f32_of_bf16(x[i]) : 0.0f;
+            g[e] = i < cols ? f32_of_bf16(gamma[i]) : 0.0f;
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < kNormPer; ++e)
+            if (t + e * 256 < cols) ss = __builtin_fmaf(v[e], v[e], ss);
+        ss = block_sum256(ss, red);
+        const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)cols) + eps));
+#pragma unroll
+        for (int e = 0; e < kNormPer; ++e) {
+            const int i = t + e * 256;
+            if (i < cols) y[i] = f32_to_bf16(g[e] * round_bf16(v[e] * r));
+        }
+        return;
+    }
     float ss = 0.0f;
-    for (int i = threadIdx.x; i < cols; i += 256) {
+    for (int i = t; i < cols; i += 256) {
         const float v = f32_of_bf16(x[i]);
         ss = __builtin_fmaf(v, v, ss);
     }
     ss = block_sum256(ss, red);
     const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)cols) + eps));
-    for (int i = threadIdx.x; i < cols; i += 256) {
-        const float v = round_bf16(f32_of_bf16(x[i]) * r);
-        y[i] = f32_to_bf16(f32_of_bf16(gamma[i]) * v);
-    }
+    for (int i = t; i < cols; i += 256)
+        y[i] = f32_to_bf16(f32_of_bf16(gamma[i]) * round_bf16(f32_of_bf16(x[i]) * r));
 }
 
 // RoPE angle for pair p of a D-wide head at position pos, and its bf16 cos
@@ -157,69 +183,165 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
     }
 }
 
-// One workgroup (256 threads) per query head; scores live in LDS.
-__global__ __launch_bounds__(256) void attention_fp8kv_kernel(
-    uint16_t* out, const uint16_t* q, const uint8_t* kc, const uint8_t* vc, const float* kv_scale,
-    int n_heads, int n_kv, int n_keys)
+// 16 E4M3 codes -> 16 floats with the hardware converter (OCP E4M3FN on
+// gfx950, exact).
+__device__ __forceinline__ void decode16(const uint4& w, float* f)
+{
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)wd[k], false);
+        const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)wd[k], true);
+        f[4 * k] = lo[0];
+        f[4 * k + 1] = lo[1];
+        f[4 * k + 2] = hi[0];
+        f[4 * k + 3] = hi[1];
+    }
+}
+
+// Attention over the E4M3 cache runs as three kernels over splits of
+// kAttnSplit keys, with scores and per-split sums in a caller workspace:
+//   A  scores:  s_j = (sum_d q_d * k_jd, d in order) * sk / sqrt(128)
+//   B  softmax: m = max s; sum of e_j = exp(s_j - m) as per-thread sums over
+//      j = t, t + 256, ... in order folded across the 256 threads; p_j =
+//      bf16(e_j * (1/sum)); then this split's PV: per-thread sums over its
+//      keys j = t, t + 256 (in order) folded across threads -> r_split[d]
+//   C  out_d = bf16((sum over splits of r_split[d], in split order) * sv)
+// The order is fixed by kAttnSplit, not by the launch, and the CPU
+// restatement repeats it. Workgroups are numbered so that the query heads
+// sharing a kv head and a split land on the same XCD (shared L2).
+constexpr int kAttnSplit = 512;
+
+struct AttnMap {
+    int h, split;
+};
+
+__device__ __forceinline__ AttnMap attn_map(int b, int n_heads, int n_kv, int n_splits)
+{
+    const int F = n_kv * n_splits;      // (kv head, split) pairs
+    const int qi = b / F, f = b % F;
+    return {(f / n_splits) * (n_heads / n_kv) + qi, f % n_splits};
+}
+
+__global__ __launch_bounds__(256) void attn_scores_kernel(
+    float* scores, const uint16_t* q, const uint8_t* kc, const float* kv_scale, int n_heads,
+    int n_kv, int n_keys, int n_splits)
 {
     constexpr int D = 128;
-    __shared__ float qs[D];
-    __shared__ float p[HEPH_ATTN_MAX_KEYS];
-    __shared__ float red[256];
-    __shared__ float part[2][D];
-    const int h = blockIdx.x, t = threadIdx.x;
-    const int kh = h / (n_heads / n_kv);
-    if (t < D) qs[t] = f32_of_bf16(q[(size_t)h * D + t]);
-    __syncthreads();
+    const AttnMap m = attn_map(blockIdx.x, n_heads, n_kv, n_splits);
+    const int t = threadIdx.x, kh = m.h / (n_heads / n_kv);
     const size_t row = (size_t)n_kv * D;
+    float qv[D];
+#pragma unroll
+    for (int c = 0; c < D / 8; ++c) {
+        const uint4 w = ldg16u(q + (size_t)m.h * D + c * 8);
+        qv[8 * c] = bf16lo(w.x); qv[8 * c + 1] = bf16hi(w.x);
+        qv[8 * c + 2] = bf16lo(w.y); qv[8 * c + 3] = bf16hi(w.y);
+        qv[8 * c + 4] = bf16lo(w.z); qv[8 * c + 5] = bf16hi(w.z);
+        qv[8 * c + 6] = bf16lo(w.w); qv[8 * c + 7] = bf16hi(w.w);
+    }
     const float qk_scale = kv_scale[kh] * 0.08838834764831845f;   // sk * f32(1/sqrt(128))
-
-    // scores: key j = t, t + 256, ...; dot over d = 0..127 in order
-    float mx = -3.4e38f;
-    for (int j = t; j < n_keys; j += 256) {
+    const int j0 = m.split * kAttnSplit + t;
+    uint4 w[2][8];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int j = min(j0 + u * 256, n_keys - 1);
         const uint4* kp = reinterpret_cast<const uint4*>(kc + j * row + kh * D);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) w[u][c] = kp[c];
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int j = j0 + u * 256;
         float dot = 0.0f;
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-            const uint4 w = kp[c];
-            const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+            float k16[16];
+            decode16(w[u][c], k16);
 #pragma unroll
-            for (int k = 0; k < 16; ++k)
-                dot = __builtin_fmaf(qs[c * 16 + k], e4m3_value((wd[k >> 2] >> (8 * (k & 3))) & 0xFFu), dot);
+            for (int k = 0; k < 16; ++k) dot = __builtin_fmaf(qv[16 * c + k], k16[k], dot);
         }
-        const float sc = dot * qk_scale;
-        p[j] = sc;
-        mx = fmaxf(mx, sc);
+        if (j < n_keys) scores[(size_t)m.h * n_keys + j] = dot * qk_scale;
     }
+}
+
+__global__ __launch_bounds__(256) void attn_pv_kernel(
+    float* partial, const float* scores, const uint8_t* vc, int n_heads, int n_kv, int n_keys,
+    int n_splits)
+{
+    constexpr int D = 128, FOLD = 32, PAD = FOLD + 1;
+    __shared__ float red[256 * PAD];
+    const AttnMap m = attn_map(blockIdx.x, n_heads, n_kv, n_splits);
+    const int t = threadIdx.x, kh = m.h / (n_heads / n_kv);
+    const size_t row = (size_t)n_kv * D;
+    const float* sc = scores + (size_t)m.h * n_keys;
+
+    // V rows of this thread's two keys go out first
+    const int j0 = m.split * kAttnSplit + t;
+    uint4 w[2][8];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int j = min(j0 + u * 256, n_keys - 1);
+        const uint4* vp = reinterpret_cast<const uint4*>(vc + j * row + kh * D);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) w[u][c] = vp[c];
+    }
+    float mx = -3.4e38f;
+    for (int j = t; j < n_keys; j += 256) mx = fmaxf(mx, sc[j]);
     red[t] = mx;
     __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if (t < w) red[t] = fmaxf(red[t], red[t + w]);
+    for (int s = 128; s > 0; s >>= 1) {
+        if (t < s) red[t] = fmaxf(red[t], red[t + s]);
         __syncthreads();
     }
     mx = red[0];
     __syncthreads();
     float se = 0.0f;
-    for (int j = t; j < n_keys; j += 256) {
-        const float e = expf(p[j] - mx);
-        p[j] = e;
-        se += e;
-    }
+    for (int j = t; j < n_keys; j += 256) se += expf(sc[j] - mx);
     se = block_sum256(se, red);
     const float inv = __fdiv_rn(1.0f, se);
-    for (int j = t; j < n_keys; j += 256) p[j] = round_bf16(p[j] * inv);
-    __syncthreads();
 
-    // PV: thread (d, half) sums keys [half * n/2 ... ) in order
-    const int d = t & (D - 1), hf = t >> 7;
-    const int mid = (n_keys + 1) >> 1;
-    const int j0 = hf ? mid : 0, j1 = hf ? n_keys : mid;
-    float acc = 0.0f;
-    for (int j = j0; j < j1; ++j)
-        acc = __builtin_fmaf(p[j], e4m3_value(vc[j * row + kh * D + d]), acc);
-    part[hf][d] = acc;
-    __syncthreads();
-    if (t < D) out[(size_t)h * D + t] = f32_to_bf16((part[0][t] + part[1][t]) * kv_scale[n_kv + kh]);
+    float acc[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int j = j0 + u * 256;
+        const float pj = j < n_keys ? round_bf16(expf(sc[j] - mx) * inv) : 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            float v16[16];
+            decode16(w[u][c], v16);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) acc[16 * c + k] = __builtin_fmaf(pj, v16[k], acc[16 * c + k]);
+        }
+    }
+    float* dst = partial + ((size_t)m.h * n_splits + m.split) * D;
+#pragma unroll
+    for (int d0 = 0; d0 < D; d0 += FOLD) {
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < FOLD; ++i) red[t * PAD + i] = acc[d0 + i];
+        __syncthreads();
+        for (int s = 128; s > 0; s >>= 1) {
+            for (int k = t; k < s * FOLD; k += 256) {
+                const int r = k / FOLD, i = k % FOLD;
+                red[r * PAD + i] += red[(r + s) * PAD + i];
+            }
+            __syncthreads();
+        }
+        if (t < FOLD) dst[d0 + t] = red[t];
+    }
+}
+
+__global__ __launch_bounds__(128) void attn_combine_kernel(
+    uint16_t* out, const float* partial, const float* kv_scale, int n_heads, int n_kv, int n_splits)
+{
+    const int h = blockIdx.x, d = threadIdx.x;
+    const float* p = partial + (size_t)h * n_splits * 128 + d;
+    float v = 0.0f;
+    for (int s = 0; s < n_splits; ++s) v += p[s * 128];
+    out[(size_t)h * 128 + d] = f32_to_bf16(v * kv_scale[n_kv + h / (n_heads / n_kv)]);
 }
 
 __global__ __launch_bounds__(256) void silu_mul_kernel(uint16_t* out, const uint16_t* gate,
@@ -314,19 +436,39 @@ int heph_qk_norm_rope_kv(void* qkv_bf16, const void* q_gamma, const void* k_gamm
     return status_of(hipGetLastError());
 }
 
+size_t heph_attention_ws_bytes(int n_heads, int n_keys)
+{
+    if (n_heads < 1 || n_keys < 1) return 0;
+    const size_t splits = (size_t)(n_keys + kAttnSplit - 1) / kAttnSplit;
+    return 4 * (size_t)n_heads * ((size_t)n_keys + splits * 128);
+}
+
 int heph_attention_fp8kv(void* out_bf16, const void* q_bf16, const uint8_t* k_cache,
                          const uint8_t* v_cache, const float* kv_scale, int n_heads,
-                         int n_kv_heads, int head_dim, int n_keys, void* stream)
+                         int n_kv_heads, int head_dim, int n_keys, void* ws, size_t ws_bytes,
+                         void* stream)
 {
-    if (!out_bf16 || !q_bf16 || !k_cache || !v_cache || !kv_scale) return HEPH_ERR_NULL;
+    if (!out_bf16 || !q_bf16 || !k_cache || !v_cache || !kv_scale || !ws) return HEPH_ERR_NULL;
     if (head_dim != 128 || n_kv_heads < 1 || n_heads < n_kv_heads || n_heads % n_kv_heads ||
         n_keys < 1 || n_keys > HEPH_ATTN_MAX_KEYS)
         return HEPH_ERR_SHAPE;
-    if (reinterpret_cast<uintptr_t>(k_cache) % 16) return HEPH_ERR_ALIGN;
+    if (ws_bytes < heph_attention_ws_bytes(n_heads, n_keys)) return HEPH_ERR_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(k_cache) % 16 || reinterpret_cast<uintptr_t>(v_cache) % 16 ||
+        reinterpret_cast<uintptr_t>(q_bf16) % 16 || reinterpret_cast<uintptr_t>(ws) % 16)
+        return HEPH_ERR_ALIGN;
     if (int st = check_device()) return st;
-    attention_fp8kv_kernel<<<n_heads, 256, 0, static_cast<hipStream_t>(stream)>>>(
-        static_cast<uint16_t*>(out_bf16), static_cast<const uint16_t*>(q_bf16), k_cache, v_cache,
-        kv_scale, n_heads, n_kv_heads, n_keys);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int splits = (n_keys + kAttnSplit - 1) / kAttnSplit;
+    float* scores = static_cast<float*>(ws);
+    float* partial = scores + (size_t)n_heads * n_keys;
+    const int blocks = n_heads * splits;
+    attn_scores_kernel<<<blocks, 256, 0, s>>>(scores, static_cast<const uint16_t*>(q_bf16),
+                                              k_cache, kv_scale, n_heads, n_kv_heads, n_keys,
+                                              splits);
+    attn_pv_kernel<<<blocks, 256, 0, s>>>(partial, scores, v_cache, n_heads, n_kv_heads, n_keys,
+                                          splits);
+    attn_combine_kernel<<<n_heads, 128, 0, s>>>(static_cast<uint16_t*>(out_bf16), partial,
+                                                kv_scale, n_heads, n_kv_heads, splits);
     return status_of(hipGetLastError());
 }
 

@@ -64,10 +64,18 @@ def qk_norm_rope_kv(qkv, q_gamma, k_gamma, k_slot, v_slot, kv_inv, n_heads: int,
           _ptr(v_slot), _ptr(kv_inv), n_heads, n_kv, 128, pos, theta, eps, _stream())
 
 
+def attention_ws(n_heads: int, n_keys: int, device="cuda") -> torch.Tensor:
+    """Scratch for attention_fp8kv with up to n_keys keys."""
+    n = L.lib().heph_attention_ws_bytes(n_heads, n_keys)
+    return torch.empty(max(n, 16), dtype=torch.uint8, device=device)
+
+
 def attention_fp8kv(out, q, k_cache, v_cache, kv_scale, n_heads: int, n_kv: int,
-                    n_keys: int) -> None:
+                    n_keys: int, ws: torch.Tensor | None = None) -> None:
+    if ws is None:
+        ws = attention_ws(n_heads, n_keys, device=out.device)
     _call("heph_attention_fp8kv", _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache),
-          _ptr(kv_scale), n_heads, n_kv, 128, n_keys, _stream())
+          _ptr(kv_scale), n_heads, n_kv, 128, n_keys, _ptr(ws), ws.numel(), _stream())
 
 
 def silu_mul(out, gate, up, n: int) -> None:
@@ -171,6 +179,7 @@ class Qwen3Decoder:
         self.next_token = torch.zeros(1, dtype=torch.int32, device=dev)
         self.token = torch.zeros(1, dtype=torch.int32, device=dev)
         self.q_ws, self.s_ws = HK.workspace(1, max(H, Q, I), device=dev)
+        self.attn_ws = attention_ws(cfg.n_heads, kv.max_ctx, device=dev)
 
     def _linear(self, c, a, fw: Fp8Weight, K: int, residual: bool = False):
         fn = HK.linear_add_residual_fp8 if residual else HK.linear_fp8
@@ -213,7 +222,7 @@ class Qwen3Decoder:
             rec(li, "k_codes", kv.k[li, pos])
             rec(li, "v_codes", kv.v[li, pos])
             attention_fp8kv(self.att, self.qkv, kv.k[li], kv.v[li], kv.scale[li], NH, NKV,
-                            pos + 1)
+                            pos + 1, self.attn_ws)
             rec(li, "attention", self.att)
             self._linear(self.x, self.att, lw.o, Q, residual=True)
             rec(li, "o_residual", self.x)

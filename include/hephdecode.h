@@ -9,6 +9,7 @@
 #ifndef HEPHDECODE_H
 #define HEPHDECODE_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #include "hephfp8.h"
@@ -17,8 +18,8 @@
 extern "C" {
 #endif
 
-/* Longest context the attention op takes (scores are held in LDS). */
-#define HEPH_ATTN_MAX_KEYS 8192
+/* Longest context the attention op takes. */
+#define HEPH_ATTN_MAX_KEYS 262144
 
 /*
  * x[t, :] = bf16(scale * e4m3(emb[tokens[t], :])) for t < n_tok.
@@ -56,11 +57,15 @@ int heph_qk_norm_rope_kv(void* qkv_bf16, const void* q_gamma, const void* k_gamm
  * One query token over n_keys cached keys: out[h] = sum_j p_j * v_j with
  * p = bf16(softmax(q.k_j * sk / sqrt(128))), K and V E4M3 codes
  * [n_keys, n_kv_heads, 128] scaled by kv_scale (K entries, then V).
- * Replaces attention (src/hephaestus/kernels.mojo:923-1035, :1183-1240).
+ * ws: device scratch of heph_attention_ws_bytes(n_heads, n_keys) bytes
+ * (scores and per-split sums), 16-byte aligned. Replaces attention
+ * (src/hephaestus/kernels.mojo:923-1035, :1183-1240).
  */
+size_t heph_attention_ws_bytes(int n_heads, int n_keys);
 int heph_attention_fp8kv(void* out_bf16, const void* q_bf16, const uint8_t* k_cache,
                          const uint8_t* v_cache, const float* kv_scale, int n_heads,
-                         int n_kv_heads, int head_dim, int n_keys, void* stream);
+                         int n_kv_heads, int head_dim, int n_keys, void* ws, size_t ws_bytes,
+                         void* stream);
 
 /*
  * out = bf16(bf16(g / (1 + exp(-g))) * up). Replaces silu_mul

@@ -11,7 +11,8 @@
  *   embed          src/hephaestus/kernels.mojo:530-548
  *   rmsnorm        HF Qwen3RMSNorm as the engine calls it, forward.mojo:45-81
  *   qk_norm_rope   forward.mojo:474-500, rope kernels.mojo:709-762
- *   attention      kernels.mojo:923-1035 (fp32 scores, bf16 probabilities)
+ *   attention      kernels.mojo:923-1035 (fp32 scores, bf16 probabilities),
+ *                  value sums in splits of 512 keys as decode.hip runs them
  *   silu_mul       kernels.mojo:1243-1255
  *   argmax         kernels.mojo:1376-1433 (bf16 logits, lowest index on ties)
  */
@@ -134,7 +135,12 @@ int heph_oracle_attention_fp8kv(uint16_t* out, const uint16_t* q, const uint8_t*
 {
     enum { D = 128 };
     float* p = malloc(sizeof(float) * (size_t)n_keys);
-    if (!p) return -1;
+    float* pv = malloc(sizeof(float) * 256 * D);
+    if (!p || !pv) {
+        free(p);
+        free(pv);
+        return -1;
+    }
     float dec[256];
     for (int c = 0; c < 256; ++c) dec[c] = heph_oracle_e4m3_decode((uint8_t)c);
     const size_t row = (size_t)n_kv * D;
@@ -159,15 +165,27 @@ int heph_oracle_attention_fp8kv(uint16_t* out, const uint16_t* q, const uint8_t*
         }
         const float inv = 1.0f / fold(part, 256);
         for (int j = 0; j < n_keys; ++j) p[j] = rb(p[j] * inv);
-        const int mid = (n_keys + 1) >> 1;
-        for (int d = 0; d < D; ++d) {
-            float a0 = 0.0f, a1 = 0.0f;
-            for (int j = 0; j < mid; ++j) a0 = fmaf(p[j], dec[vc[j * row + kh * D + d]], a0);
-            for (int j = mid; j < n_keys; ++j) a1 = fmaf(p[j], dec[vc[j * row + kh * D + d]], a1);
-            out[(size_t)h * D + d] = tob((a0 + a1) * kv_scale[n_kv + kh]);
+        /* PV over splits of 512 keys: per split, per-thread sums over the
+         * split's keys j = t, t + 256 (in order) folded across the 256
+         * threads; then the split results summed in split order */
+        float tot[D];
+        for (int d = 0; d < D; ++d) tot[d] = 0.0f;
+        for (int j0 = 0; j0 < n_keys; j0 += 512) {
+            memset(pv, 0, sizeof(float) * 256 * D);
+            for (int j = j0; j < n_keys && j < j0 + 512; ++j) {
+                const uint8_t* v = vc + j * row + kh * D;
+                float* acc = pv + (size_t)((j - j0) & 255) * D;
+                for (int d = 0; d < D; ++d) acc[d] = fmaf(p[j], dec[v[d]], acc[d]);
+            }
+            for (int d = 0; d < D; ++d) {
+                for (int t = 0; t < 256; ++t) part[t] = pv[(size_t)t * D + d];
+                tot[d] += fold(part, 256);
+            }
         }
+        for (int d = 0; d < D; ++d) out[(size_t)h * D + d] = tob(tot[d] * kv_scale[n_kv + kh]);
     }
     free(p);
+    free(pv);
     return 0;
 }
 

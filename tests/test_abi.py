@@ -161,9 +161,14 @@ def test_decode_ops_reject(lib):
     assert q(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 32, 8, 64, 0, 1e6, 1e-6, None) == L.HEPH_ERR_SHAPE
     assert q(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 30, 8, 128, 0, 1e6, 1e-6, None) == L.HEPH_ERR_SHAPE
     a = lib.heph_attention_fp8kv
-    assert a(FAKE, FAKE, FAKE, FAKE, FAKE, 32, 8, 128, L.ATTN_MAX_KEYS + 1, None) == \
-        L.HEPH_ERR_SHAPE
-    assert a(FAKE, FAKE, FAKE, FAKE, FAKE, 32, 8, 128, 0, None) == L.HEPH_ERR_SHAPE
-    assert a(FAKE, FAKE, ODD, FAKE, FAKE, 32, 8, 128, 10, None) == L.HEPH_ERR_ALIGN
+    ws = lib.heph_attention_ws_bytes(32, 4097)
+    assert ws == 4 * 32 * (4097 + 9 * 128)
+    assert a(FAKE, FAKE, FAKE, FAKE, FAKE, 32, 8, 128, L.ATTN_MAX_KEYS + 1, FAKE, 1 << 40,
+             None) == L.HEPH_ERR_SHAPE
+    assert a(FAKE, FAKE, FAKE, FAKE, FAKE, 32, 8, 128, 0, FAKE, ws, None) == L.HEPH_ERR_SHAPE
+    assert a(FAKE, FAKE, FAKE, FAKE, FAKE, 32, 8, 128, 4097, None, ws, None) == L.HEPH_ERR_NULL
+    assert a(FAKE, FAKE, FAKE, FAKE, FAKE, 32, 8, 128, 4097, FAKE, ws - 4, None) == \
+        L.HEPH_ERR_WORKSPACE
+    assert a(FAKE, FAKE, ODD, FAKE, FAKE, 32, 8, 128, 10, FAKE, ws, None) == L.HEPH_ERR_ALIGN
     assert lib.heph_silu_mul(FAKE, FAKE, FAKE, 0, None) == L.HEPH_ERR_SHAPE
     assert lib.heph_argmax_bf16(None, FAKE, 10, None) == L.HEPH_ERR_NULL

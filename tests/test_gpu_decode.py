@@ -65,7 +65,7 @@ def test_embed_bit_exact():
 
 
 @pytest.mark.parametrize("rows,cols,scale", [(3, 2560, 1.0), (1, 9728, 40.0), (2, 2560, 1e-4),
-                                             (32, 128, 1.0)])
+                                             (32, 128, 1.0), (2, 12288, 1.0)])
 def test_rmsnorm_bit_exact(rows, cols, scale):
     x = rng_bf16(cols + rows, rows * cols, scale).reshape(rows, cols)
     g = rng_bf16(7, cols)
@@ -116,7 +116,7 @@ def mostly_equal(got, want, what):
         f"{what}: max rel {err:.2e}"
 
 
-@pytest.mark.parametrize("n", [1, 2, 300, 4097, 8192])
+@pytest.mark.parametrize("n", [1, 2, 300, 511, 512, 513, 4097, 20000])
 def test_attention_vs_oracle(n):
     NH, NKV = 32, 8
     rng = np.random.default_rng(n)
@@ -129,10 +129,29 @@ def test_attention_vs_oracle(n):
     mostly_equal(host(out), O.attention_fp8kv(q, kc, vc, sc, NH, NKV, n), f"attention n={n}")
 
 
-def test_attention_rejects_long_context():
+def test_attention_decodes_every_e4m3_code():
+    # one key: p = 1 and out = bf16(e4m3(v) * 1), so the hardware converter
+    # must reproduce the E4M3FN table for all 256 codes (NaN for 0x7F/0xFF)
+    NH = NKV = 2
+    vc = np.arange(256, dtype=np.uint8).reshape(1, NKV, 128)
+    kc = np.full((1, NKV, 128), 0x30, np.uint8)
+    q = rng_bf16(9, NH * 128)
+    out = torch.empty(NH * 128, dtype=torch.bfloat16, device="cuda")
+    DEC.attention_fp8kv(out, dev(q), dev(kc), dev(vc), dev(np.ones(4, np.float32)), NH, NKV, 1)
+    torch.cuda.synchronize()
+    got = f32(host(out))
+    table = O.e4m3_decode_table().astype(np.float64)
+    nan = np.isnan(table)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan], table[~nan])
+
+
+def test_attention_rejects_long_context_and_small_workspace():
     z = torch.zeros(16, dtype=torch.uint8, device="cuda")
     with pytest.raises(HephError):
-        DEC.attention_fp8kv(z, z, z, z, z, 32, 8, L.ATTN_MAX_KEYS + 1)
+        DEC.attention_fp8kv(z, z, z, z, z, 32, 8, L.ATTN_MAX_KEYS + 1, ws=z)
+    with pytest.raises(HephError):
+        DEC.attention_fp8kv(z, z, z, z, z, 32, 8, 100, ws=z)
 
 
 def test_silu_mul_vs_oracle():
