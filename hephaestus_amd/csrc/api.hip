@@ -250,6 +250,10 @@ int heph_set_tuning(int knob, int value)
         if (value != 0 && value != 1 && value != 2) return HEPH_ERR_FLAGS;
         gu = value;
         break;
+    case HEPH_TUNE_GEMM_BM:
+        if (value != 0 && value != 128 && value != 192 && value != 256) return HEPH_ERR_FLAGS;
+        gemm_tune(value);
+        return HEPH_OK;
     default: return HEPH_ERR_FLAGS;
     }
     skinny_tune(waves, u);

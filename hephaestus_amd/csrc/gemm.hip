@@ -20,6 +20,8 @@
 //   * the block -> tile order gives each XCD a contiguous run of tiles in
 //     a grouped (8 tile-rows) order, so A and B tiles are reused from that
 //     XCD's L2.
+#include <atomic>
+
 #include "heph_kernels.h"
 
 namespace heph {
@@ -225,11 +227,20 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8Operands op)
 // full 128-byte lines per store, which measured far cheaper than storing
 // the MFMA layout from registers.
 namespace {
-constexpr int L_BM = 256, L_BN = 256;
-constexpr int L_WM = 128, L_WN = 64;
-constexpr int L_MT = L_WM / 16, L_NT = L_WN / 16;
-constexpr int L_STAGE_A = L_BM * kChunk, L_STAGE_B = L_BN * kChunk, L_STAGE_S = L_BM * 4;
-constexpr int L_STAGE = L_STAGE_A + L_STAGE_B + L_STAGE_S;
+constexpr int L_BN = 256, L_WN = 64, L_NT = L_WN / 16;
+constexpr int L_STAGE_B = L_BN * kChunk;
+
+// Tile height BM in {128, 192, 256}: the 8 waves form a 2 x 4 grid of
+// (BM/2) x 64 wave tiles. A smaller BM trades MFMA work per chunk for a
+// tile count that fills the CUs (e.g. 220 tiles of 192 x 256 instead of
+// 160 of 256 x 256 at M = 4096, N = 2560).
+template <int BM>
+struct BigTile {
+    static_assert(BM == 128 || BM == 192 || BM == 256, "tile height");
+    static constexpr int WM = BM / 2, MT = WM / 16;
+    static constexpr int STAGE_A = BM * kChunk, STAGE_S = BM * 4;
+    static constexpr int STAGE = STAGE_A + L_STAGE_B + STAGE_S;
+};
 
 __device__ __forceinline__ void dma16(const void* g, void* lds)
 {
@@ -247,9 +258,12 @@ __device__ __forceinline__ void wait_dma()
 }
 }  // namespace
 
-template <int SM>
+template <int SM, int BM>
 __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
 {
+    using T = BigTile<BM>;
+    constexpr int L_BM = BM, L_WM = T::WM, L_MT = T::MT;
+    constexpr int L_STAGE_A = T::STAGE_A, L_STAGE = T::STAGE;
     __shared__ __attribute__((aligned(16))) uint8_t smem[2 * L_STAGE];
 
     const int tid = threadIdx.x;
@@ -283,12 +297,14 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
         uint8_t* st = smem + buf * L_STAGE;
         const uint8_t* qa = op.q + (size_t)j * kChunk;
         const uint8_t* wb = op.w + (size_t)j * kChunk;
+        if (wave * 32 < L_BM) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            dma16(qa + aoff[q], st + (wave * 32 + q * 8) * kChunk);
-            dma16(wb + boff[q], st + L_STAGE_A + (wave * 32 + q * 8) * kChunk);
+            for (int q = 0; q < 4; ++q) dma16(qa + aoff[q], st + (wave * 32 + q * 8) * kChunk);
         }
-        if (SM != 2 && wave < 4)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            dma16(wb + boff[q], st + L_STAGE_A + (wave * 32 + q * 8) * kChunk);
+        if (SM != 2 && wave * 64 < L_BM)
             dma4(ssrc + j * op.s_step, st + L_STAGE_A + L_STAGE_B + wave * 256);
     };
 
@@ -378,11 +394,11 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
         }
     }
 
-    // ---- epilogue: two passes of 128 rows through LDS (f32) ----
+    // ---- epilogue: two passes of L_WM rows through LDS (f32) ----
     // Rows are padded to 260 floats (4 banks of skew per row), so every
     // lane's address is one base plus immediate offsets.
     constexpr int CST = L_BN + 4;
-    static_assert(128 * CST * 4 <= 2 * L_STAGE, "epilogue tile must fit the stage buffers");
+    static_assert(L_WM * CST * 4 <= 2 * L_STAGE, "epilogue tile must fit the stage buffers");
     float* Cs = reinterpret_cast<float*>(smem);
     float* cw = Cs + (slice * 4) * CST + wn * L_WN + r16;
     for (int pass = 0; pass < 2; ++pass) {
@@ -397,11 +413,11 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
                         cw[(mi * 16 + i) * CST + ni * 16] = acc[mi][ni][i];
         }
         __syncthreads();
-        // 128 rows x 256 cols: each thread writes 8 consecutive outputs
-        for (int e = tid; e < 128 * (L_BN / 8); e += 512) {
+        // L_WM rows x 256 cols: each thread writes 8 consecutive outputs
+        for (int e = tid; e < L_WM * (L_BN / 8); e += 512) {
             const int r = e / (L_BN / 8);
             const int c8 = (e % (L_BN / 8)) * 8;
-            const int grow = m0 + pass * 128 + r;
+            const int grow = m0 + pass * L_WM + r;
             const int gcol = n0 + c8;
             if (grow >= M || gcol >= N) continue;
             const f32x4 lo = *reinterpret_cast<const f32x4*>(&Cs[r * CST + c8]);
@@ -444,21 +460,75 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     }
 }
 
+namespace {
+
+std::atomic<int> g_tune_bm{0};
+int g_cu_count[64];
+
+int cu_count()
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = __atomic_load_n(&g_cu_count[dev], __ATOMIC_RELAXED);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        __atomic_store_n(&g_cu_count[dev], n, __ATOMIC_RELAXED);
+    }
+    return n;
+}
+
+template <int BM>
+hipError_t launch_big(const Fp8Operands& op, hipStream_t stream, const LaunchTiming& t)
+{
+    const int tiles = ((op.M + BM - 1) / BM) * ((op.N + L_BN - 1) / L_BN);
+    if (op.w_block)
+        return launch(fp8_gemm256_kernel<0, BM>, dim3(tiles), dim3(512), 0, stream, t, op);
+    if (op.s_step == 0)
+        return launch(fp8_gemm256_kernel<2, BM>, dim3(tiles), dim3(512), 0, stream, t, op);
+    return launch(fp8_gemm256_kernel<1, BM>, dim3(tiles), dim3(512), 0, stream, t, op);
+}
+
+}  // namespace
+
+// Tile height of the large-M kernel: the one whose tile count fills the
+// CUs best (one 512-thread workgroup per CU; fraction of the last round's
+// slots used), the taller tile on a tie.
+int gemm_tile_m(int M, int N)
+{
+    const int forced = g_tune_bm.load(std::memory_order_relaxed);
+    if (forced) return forced;
+    const int cus = cu_count();
+    int best = 256;
+    double best_fill = -1.0;
+    for (int bm : {256, 192, 128}) {
+        const long tiles = (long)((M + bm - 1) / bm) * ((N + L_BN - 1) / L_BN);
+        const long rounds = (tiles + cus - 1) / cus;
+        const double fill = (double)tiles / (double)(rounds * cus);
+        if (fill > best_fill + 0.01) {
+            best_fill = fill;
+            best = bm;
+        }
+    }
+    return best;
+}
+
+void gemm_tune(int bm) { g_tune_bm.store(bm, std::memory_order_relaxed); }
+
 hipError_t launch_fp8_gemm(const Fp8Operands& op, hipStream_t stream,
                            const LaunchTiming& t, const char** name)
 {
-    // Large M: the 256x256 DMA kernel (N % 16 == 0 keeps every 8-wide
+    // Large M: the 256-column DMA kernel (N % 16 == 0 keeps every 8-wide
     // output group inside the row; its 32-bit operand offsets need
     // M*K and N*K below 2^31). Otherwise the 128x128 kernel.
     const bool small_offsets = (long)op.M * op.K < (1L << 31) && (long)op.N * op.K < (1L << 31);
     if (op.M >= 1024 && small_offsets) {
-        const int tiles = ((op.M + L_BM - 1) / L_BM) * ((op.N + L_BN - 1) / L_BN);
-        *name = "fp8_gemm_256x256";
-        if (op.w_block)
-            return launch(fp8_gemm256_kernel<0>, dim3(tiles), dim3(512), 0, stream, t, op);
-        if (op.s_step == 0)
-            return launch(fp8_gemm256_kernel<2>, dim3(tiles), dim3(512), 0, stream, t, op);
-        return launch(fp8_gemm256_kernel<1>, dim3(tiles), dim3(512), 0, stream, t, op);
+        switch (gemm_tile_m(op.M, op.N)) {
+        case 128: *name = "fp8_gemm_128x256"; return launch_big<128>(op, stream, t);
+        case 192: *name = "fp8_gemm_192x256"; return launch_big<192>(op, stream, t);
+        default: *name = "fp8_gemm_256x256"; return launch_big<256>(op, stream, t);
+        }
     }
     const int tiles = ((op.M + BM - 1) / BM) * ((op.N + BN - 1) / BN);
     *name = "fp8_gemm_128x128";

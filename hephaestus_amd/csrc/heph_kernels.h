@@ -84,6 +84,11 @@ void gemv_tune(int ks, int waves, int u);
 hipError_t launch_fp8_gemm(const Fp8Operands& op, hipStream_t stream,
                            const LaunchTiming& t, const char** name);
 
+// Tile height (128, 192 or 256) the large-M GEMM uses for M x N, and its
+// override (0 = automatic).
+int gemm_tile_m(int M, int N);
+void gemm_tune(int bm);
+
 // bf16 x [M,K] @ w [N,K]^T, f32 accumulation, M <= 32.
 hipError_t launch_bf16_skinny(void* c, bool c_f32, bool residual, const uint16_t* x,
                               const uint16_t* w, int M, int N, int K,

@@ -154,12 +154,14 @@ const char* heph_last_kernel(void);
  *                           0, 1, 2, 4 or 8
  *   HEPH_TUNE_GEMV_WAVES    waves per workgroup of the M = 1 kernel: 0, 4, 8
  *   HEPH_TUNE_GEMV_U        steps per load batch of the M = 1 kernel: 0, 1, 2
+ *   HEPH_TUNE_GEMM_BM       tile height of the M >= 1024 GEMM: 0, 128, 192, 256
  */
 #define HEPH_TUNE_SKINNY_WAVES 1
 #define HEPH_TUNE_SKINNY_U     2
 #define HEPH_TUNE_GEMV_KS      3
 #define HEPH_TUNE_GEMV_WAVES   4
 #define HEPH_TUNE_GEMV_U       5
+#define HEPH_TUNE_GEMM_BM      6
 int heph_set_tuning(int knob, int value);
 
 #ifdef __cplusplus

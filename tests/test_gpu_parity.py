@@ -463,11 +463,20 @@ def test_graph_capture_replays_match_eager():
 
 # ------------------------------------------------ large-M GEMM variants ----
 
+@pytest.fixture(params=[128, 192, 256])
+def tile_m(request):
+    """Force the large-M kernel's tile height for one test."""
+    HK.set_tuning(L.TUNE_GEMM_BM, request.param)
+    yield request.param
+    HK.set_tuning(L.TUNE_GEMM_BM, 0)
+
+
 @pytest.mark.parametrize("mode", ["block", "channel_token", "channel_g128"])
 @pytest.mark.parametrize("out,resid", [("bf16", False), ("bf16", True), ("f32", False), ("f32", True)])
-def test_large_m_gemm_modes(mode, out, resid):
-    # M >= 1024 takes the 256x256 kernel; ragged M and N, every scale mode,
-    # both output types, with and without the fused residual.
+def test_large_m_gemm_modes(mode, out, resid, tile_m):
+    # M >= 1024 takes the 256-column kernel at every tile height; ragged M
+    # and N, every scale mode, both output types, with and without the
+    # fused residual.
     M, N, K = 1300, 400, 1024
     x = O.gen_act_bf16(60, M, K, outlier_p=1e-3)
     if mode == "block":
@@ -480,7 +489,7 @@ def test_large_m_gemm_modes(mode, out, resid):
     r = O.gen_normal(62, M * N).reshape(M, N).astype(np.float32)
     res_t = (dev(bf16_of(r)) if out == "bf16" else dev(r)) if resid else None
     c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K, group_k=g, out=dt, residual=res_t)
-    assert HK.last_kernel() == "fp8_gemm_256x256"
+    assert HK.last_kernel() == f"fp8_gemm_{tile_m}x256"
     ref = O.quant_linear(x, qw, sw, group_k=g, bn=bn, bk=bk)
     if resid:
         ref = ref + (f32_of_bf16(bf16_of(r)) if out == "bf16" else r)
@@ -491,7 +500,7 @@ def test_large_m_gemm_modes(mode, out, resid):
 
 
 @pytest.mark.parametrize("M", [1024, 1100])
-def test_large_m_exact_integer(M):
+def test_large_m_exact_integer(M, tile_m):
     N, K = 272, 2560
     ia, qa = lattice(M, K, 3000 + M)
     iw, qw = lattice(N, K, 4000)
@@ -500,5 +509,18 @@ def test_large_m_exact_integer(M):
     ref = (ia.astype(np.float64) @ iw.astype(np.float64).T) * 0.0625 * 2.0 ** -5
     c, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, skip_quant=True,
                          q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
-    assert HK.last_kernel() == "fp8_gemm_256x256"
+    assert HK.last_kernel() == f"fp8_gemm_{tile_m}x256"
     assert np.array_equal(host_bf16(c), bf16_of(ref.astype(np.float32)))
+
+
+def test_large_m_tile_choice_fills_the_cus():
+    # At M = 4096 the automatic tile height is the one whose tile count
+    # best fills 256 CUs: 128 for N = 6144 (768 tiles), 192 for N = 2560
+    # (220 tiles), 256 for N = 19456 (1216 tiles).
+    x = O.gen_act_bf16(70, 4096, 256)
+    for N, want in ((6144, 128), (2560, 192), (19456, 256)):
+        if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+            pytest.skip("expectations are for a 256-CU MI355X")
+        qw, sw = O.gen_weight(71, N, 256)
+        run_linear(qw, sw, x, M=4096, N=N, K=256)
+        assert HK.last_kernel() == f"fp8_gemm_{want}x256", N
