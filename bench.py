@@ -81,10 +81,32 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="skip the detail sweeps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--prefill-pass", action="store_true",
+                    help="only run the configs[3] M = 4096 prefill launches eagerly (quant + "
+                         "GEMM, 10 per shape, for rocprofv3 traces); prints no JSON")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="only run the M = 1 launches eagerly plus a 256 MiB device "
                          "copy (for rocprofv3 --pmc traffic counts); prints no JSON")
     return ap.parse_args()
+
+
+def prefill_pass(steps):
+    """configs[3] at M = 4096: quantize + GEMM for each shape, eagerly."""
+    import torch
+    from hephaestus_amd import kernels as HK
+    torch.cuda.set_device(0)
+    M = 4096
+    for i, (name, N, K) in enumerate(SHAPES):
+        lin = Linear(name, N, K, M, seed=100 + i, rotate=False)
+        x = act(M, K, seed=M + 1, outliers=True)
+        c = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        w, s = lin.next()
+        for _ in range(steps):
+            HK.linear_fp8(c, x, w, s, lin.q_ws, lin.s_ws, M, N, K)
+        torch.cuda.synchronize()
+        print(f"prefill-pass {name} M={M} N={N} K={K} kernel={HK.last_kernel()} "
+              f"launches={steps}", flush=True)
+        del lin
 
 
 def pmc_pass(steps):
@@ -166,6 +188,9 @@ def main():
         sys.exit(2)
     if args.pmc_pass:
         pmc_pass(max(1, min(args.steps, 20)))
+        return
+    if args.prefill_pass:
+        prefill_pass(max(1, min(args.steps, 20)))
         return
     import torch
     from hephaestus_amd import kernels as HK
