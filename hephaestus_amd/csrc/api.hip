@@ -153,12 +153,12 @@ int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
     op.N = N;
     op.K = K;
 
-    const bool skinny = (flags & HEPH_FLAG_FORCE_SKINNY) ||
-                        (!(flags & HEPH_FLAG_FORCE_GEMM) && M <= HEPH_SKINNY_MAX_M);
-    // M = 1 takes the chunk-slot GEMV unless a kernel is forced.
-    const bool gemv = M == 1 && !(flags & (HEPH_FLAG_FORCE_SKINNY | HEPH_FLAG_FORCE_GEMM));
-    const bool fused = (skinny || gemv) && !skip_quant && !(flags & HEPH_FLAG_NO_FUSE) &&
-                       group_k == kChunk && M <= kFusedMaxM;
+    // M <= 32 takes the chunk-slot GEMV unless a kernel is forced; the
+    // skinny kernel serves FORCE_SKINNY (cross-kernel checks) only.
+    const bool skinny = flags & HEPH_FLAG_FORCE_SKINNY;
+    const bool gemv = !skinny && !(flags & HEPH_FLAG_FORCE_GEMM) && M <= HEPH_SKINNY_MAX_M;
+    const bool fuse_ok = !skip_quant && !(flags & HEPH_FLAG_NO_FUSE) && group_k == kChunk;
+    const bool fused = fuse_ok && ((gemv && gemv_fuses(M, N, K)) || (skinny && M <= kFusedMaxM));
     LaunchTiming t = take_timing();
     if (!skip_quant && !fused) {
         // A timed call spans both kernels: the quantizer carries the start
@@ -243,7 +243,7 @@ int heph_set_tuning(int knob, int value)
         gks = value;
         break;
     case HEPH_TUNE_GEMV_WAVES:
-        if (value != 0 && value != 4 && value != 8) return HEPH_ERR_FLAGS;
+        if (value != 0 && value != 4 && value != 8 && value != 16) return HEPH_ERR_FLAGS;
         gwaves = value;
         break;
     case HEPH_TUNE_GEMV_U:

@@ -1,35 +1,45 @@
-// gemv.hip - W8A8 FP8 linear at M = 1 (the decode GEMV).
+// gemv.hip - W8A8 FP8 linear for 1 <= M <= 32 (decode GEMV and batched decode).
 //
-// Replaces the reference's decode GEMV (src/hephaestus/wmma_gfx12.mojo:650-744,
-// reached through gemv_fp8 / linear_fp8, src/hephaestus/kernels.mojo:372-470),
-// which gives one 32-lane wave a 16-column tile over all of K.
+// Replaces the reference's decode GEMV and small-M kernels
+// (src/hephaestus/wmma_gfx12.mojo:650-744 and :906-1019, reached through
+// gemv_fp8 / linear_fp8, src/hephaestus/kernels.mojo:372-470). Those give
+// one 32-lane wave a 16-column tile over all of K.
 //
-// At M = 1 only one row of the 16x16 MFMA tile carries data. This kernel
-// fills the other rows with further K-chunks instead ("chunk slots"): with
-// KS slots, MFMA column c holds output column n0 + c % TW (TW = 16 / KS) at
-// K-chunk step*KS + c / TW, and A row t holds the activation chunk of slot
-// t. The wanted product of column c is then C[c / TW][c]; every other C
-// element is unused. One v_mfma_f32_16x16x128_f8f6f4 covers KS chunks of
-// TW columns, so a workgroup owns only TW output columns and the grid has
-// N*KS/16 workgroups: enough to cover all 256 CUs even at N = 2560, with
-// no reduction across workgroups.
+// At M <= 32 the work is bound by streaming the E4M3 weights from HBM, and
+// with M rows only M of the 16 rows of a 16x16 MFMA tile carry data. This
+// kernel fills the other rows with further K-chunks instead ("chunk
+// slots"): with KS slots of MR rows each (KS * MR <= 16; MR = M rounded up
+// to a power of two), A row t*MR + m holds row m of the activations at the
+// chunk of slot t, and MFMA column c holds output column n0 + c % TW
+// (TW = 16 / KS) at K-chunk step*KS + c / TW. The wanted products of
+// column c are then C[(c / TW)*MR + m][c]; every other C element is unused.
+// One v_mfma_f32_16x16x128_f8f6f4 covers KS chunks of TW columns, so a
+// workgroup owns only TW output columns and the grid has N*KS/16
+// workgroups: enough to cover the 256 CUs even at N = 2560 for M <= 4,
+// with no reduction across workgroups. M = 17..32 runs two 16-row tiles
+// with one slot.
 //   * workgroup = TW output columns; its WAVES waves split the KC/KS steps
 //     into contiguous runs; loads go out in batches of U steps, two batches
 //     in flight, each lane issuing two 16-byte weight loads per step;
-//   * fused mode (1x128 groups) quantizes x inside the kernel: 64/KS lanes
-//     share a slot's 128-element group, its max is reduced with DPP, the
-//     scale is the reference's own division (amax/448, 1/s, both rounded to
-//     nearest even), and the codes reach the MFMA A layout through a
-//     per-wave LDS tile. Workgroup 0 also writes q/s to the workspace so
-//     later SKIP_QUANT calls can reuse them;
-//   * each lane rescales its own C element by sa[chunk] * sw[block, chunk]
-//     in registers; per-channel/per-token scales (the reference's own
-//     granularity) accumulate unscaled and apply acc*(sa*sw) at the end
-//     (wmma_gfx12.mojo:711-712);
+//   * fused mode (1x128 groups) quantizes x inside the kernel:
+//     64/(KS*MR) lanes share an A row's 128-element group, its max (on the
+//     bf16 magnitude bits, two per packed 16-bit max, NaN skipped) is
+//     reduced with DPP, the scale is the reference's own division
+//     (amax/448, 1/s, both rounded to nearest even), and the codes reach
+//     the MFMA A layout through a per-wave LDS tile. Workgroup 0 also
+//     writes q/s to the workspace so later SKIP_QUANT calls can reuse them;
+//   * each lane rescales its candidate C elements by sa[row, chunk] *
+//     sw[block, chunk] in registers, the row scales passed between lanes
+//     by ds_bpermute from the lane that quantized (or loaded) that A row;
+//     per-channel/per-token scales (the
+//     reference's own granularity) accumulate unscaled and apply the
+//     reference association at the end: acc*(sa*sw) at M = 1
+//     (wmma_gfx12.mojo:711-712), (acc*sa)*sw otherwise (:973, :848);
 //   * the last wave of a workgroup to finish sums the waves' slot partials
 //     in a fixed order (deterministic) and stores bf16 or f32, optionally
 //     adding the residual first (wmma_gfx12.mojo:712-715).
 #include <atomic>
+#include <type_traits>
 
 #include "heph_kernels.h"
 
@@ -44,30 +54,6 @@ enum GemvScale { kGemvBlock = 0, kGemvChannel = 1, kGemvConst = 2 };
 
 namespace {
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float x)
-{
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
-}
-
-__device__ __forceinline__ float readlane_f(float v, int l)
-{
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
-}
-
-// Max over each aligned run of LPR lanes (LPR = 8, 16, 32 or 64).
-template <int LPR>
-__device__ __forceinline__ float lanes_max(float m)
-{
-    m = fmaxf(m, dpp_f<0xB1>(m));    // quad_perm [1,0,3,2]
-    m = fmaxf(m, dpp_f<0x4E>(m));    // quad_perm [2,3,0,1]
-    m = fmaxf(m, dpp_f<0x141>(m));   // row_half_mirror: runs of 8
-    if constexpr (LPR >= 16) m = fmaxf(m, dpp_f<0x140>(m));   // row_mirror: 16
-    if constexpr (LPR >= 32) m = fmaxf(m, __shfl_xor(m, 16));
-    if constexpr (LPR == 64) m = fmaxf(readlane_f(m, 0), readlane_f(m, 32));
-    return m;
-}
-
 // The reference group scale (kernels.mojo:173-181): s = amax / 448, 1.0
 // below 1e-12, inv = 1 / s; both divisions IEEE round-to-nearest-even.
 __device__ __forceinline__ void group_scale_div(float amax, float& s, float& inv)
@@ -77,7 +63,7 @@ __device__ __forceinline__ void group_scale_div(float amax, float& s, float& inv
     inv = __frcp_rn(s);
 }
 
-// E consecutive bf16 activations (E = 2, 4, 8 or 16) as E/2 dwords.
+// E consecutive bf16 activations (E = 2, 4, 8, 16 or 32) as E/2 dwords.
 template <int E>
 struct XVec {
     uint32_t d[E / 2];
@@ -112,38 +98,89 @@ __device__ __forceinline__ void store_codes(uint8_t* p, const uint32_t* cd)
     if constexpr (E == 2) *reinterpret_cast<uint16_t*>(p) = (uint16_t)cd[0];
     else if constexpr (E == 4) *reinterpret_cast<uint32_t*>(p) = cd[0];
     else if constexpr (E == 8) *reinterpret_cast<uint2*>(p) = make_uint2(cd[0], cd[1]);
-    else *reinterpret_cast<uint4*>(p) = make_uint4(cd[0], cd[1], cd[2], cd[3]);
+    else {
+#pragma unroll
+        for (int h = 0; h < E / 16; ++h)
+            reinterpret_cast<uint4*>(p)[h] =
+                make_uint4(cd[4 * h], cd[4 * h + 1], cd[4 * h + 2], cd[4 * h + 3]);
+    }
+}
+
+// Max over each aligned run of LPR lanes, unsigned integers.
+template <int LPR>
+__device__ __forceinline__ uint32_t lanes_max_u(uint32_t m)
+{
+    auto dpp = [](uint32_t x, auto ctrl) {
+        return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, decltype(ctrl)::value, 0xf, 0xf, false);
+    };
+    m = max(m, dpp(m, std::integral_constant<int, 0xB1>{}));
+    m = max(m, dpp(m, std::integral_constant<int, 0x4E>{}));
+    if constexpr (LPR >= 8) m = max(m, dpp(m, std::integral_constant<int, 0x141>{}));
+    if constexpr (LPR >= 16) m = max(m, dpp(m, std::integral_constant<int, 0x140>{}));
+    if constexpr (LPR >= 32) m = max(m, (uint32_t)__shfl_xor((int)m, 16));
+    if constexpr (LPR == 64)
+        m = max((uint32_t)__builtin_amdgcn_readlane((int)m, 0),
+                (uint32_t)__builtin_amdgcn_readlane((int)m, 32));
+    return m;
+}
+
+// Four floats -> four E4M3FN codes (byte i = code of value i), RNE. The
+// first conversion writes the low half of a register whose other half the
+// second one overwrites, so its previous contents do not matter.
+__device__ __forceinline__ uint32_t pack4_any(float a, float b, float c, float d, uint32_t junk)
+{
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, (int)junk, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+    return (uint32_t)w;
+}
+
+__device__ __forceinline__ float pick(const f32x4& p, int e)
+{
+    return e == 0 ? p[0] : e == 1 ? p[1] : e == 2 ? p[2] : p[3];
 }
 
 }  // namespace
 
-template <int WAVES, int KS, int U, bool FUSED, int SM>
+template <int WAVES, int KS, int MR, int MT, int U, bool FUSED, int SM>
 __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
 {
     static_assert(KS == 1 || KS == 2 || KS == 4 || KS == 8, "chunk slots");
-    static_assert(!(FUSED && SM == kGemvConst), "per-token quantization is not fused");
+    static_assert(MR == 1 || MR == 2 || MR == 4 || MR == 8 || MR == 16, "rows per slot");
+    static_assert(KS * MR <= 16, "slots x rows must fit the 16 MFMA rows");
+    static_assert(MT == 1 || (MT == 2 && MR == 16 && KS == 1), "two row tiles: one slot of 16");
+    static_assert(!(FUSED && SM == kGemvConst), "fused quantization: 1x128 groups");
+    constexpr int R = KS * MR;           // A rows in use
     constexpr int TW = 16 / KS;          // output columns per workgroup
-    constexpr int LPR = 64 / KS;         // quantizing lanes per slot
+    constexpr int LPR = 64 / R;          // quantizing lanes per A row
     constexpr int E = 128 / LPR;         // activations per quantizing lane
+    constexpr int NE = MR < 4 ? MR : 4;  // candidate C elements per lane and tile
     const Fp8Operands& op = args.op;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, g = lane >> 4;
     const int t = r16 / TW;              // chunk slot of this lane's column
-    const int ei = t & 3;                // its C element: row t, in lane group t/4
-    const int K = op.K;
+    // This lane's candidate C elements are rows rho + i (i < NE) of the
+    // tile, element e0 + i of its MFMA result: the rows of slot t when
+    // MR < 4 (they sit in lane group t*MR/4), else rows 4g .. 4g+3.
+    const int rho = MR < 4 ? t * MR : 4 * g;
+    const int e0 = MR < 4 ? rho & 3 : 0;
+    const int M = op.M, K = op.K;
     const int KC = K >> 7;
     const int S = (KC + KS - 1) / KS;    // steps of KS chunks
     const int n0 = blockIdx.x * TW;
     const int per = (S + WAVES - 1) / WAVES;
     const int sb = min(S, wave * per);
     const int se = min(S, sb + per);
+    // fused: this lane quantizes piece qpiece of A row qrow (slot tq, row mq)
     const int qrow = lane / LPR, qpiece = lane % LPR;
+    const int tq = qrow / MR, mq = qrow % MR;
+    // separate quantization: this lane loads A row r16 (slot ta, row ma)
+    const int ta = r16 / MR, ma = r16 % MR;
 
-    __shared__ float red[WAVES][64];
+    __shared__ float red[WAVES][MT * NE][64];
     __shared__ int arrive;
     __shared__ __attribute__((aligned(16))) uint8_t qlds[FUSED ? WAVES : 1][FUSED ? U : 1]
-                                                        [KS * kChunk];
+                                                        [FUSED ? MT : 1][R * kChunk];
     if (threadIdx.x == 0) arrive = 0;
     __syncthreads();
 
@@ -154,36 +191,52 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
 
     struct Batch {
         i32x4 blo[U], bhi[U];
-        i32x4 alo[FUSED ? 1 : U], ahi[FUSED ? 1 : U];
-        XVec<E> xv[FUSED ? U : 1];
+        i32x4 alo[FUSED ? 1 : U][MT], ahi[FUSED ? 1 : U][MT];
+        XVec<E> xv[FUSED ? U : 1][MT];
         float sw[U];
-        float sa[FUSED ? 1 : U];
+        // MR = 1: the scale of this lane's candidate row; else the scale of
+        // its own A row r16, passed to the candidate rows by ds_bpermute
+        float sa[FUSED ? 1 : U][MT];
     };
 
     // Loads are unconditional and clamped, so a batch is one straight run
     // of memory instructions: a step past se re-reads step se-1 (never
-    // consumed) and a chunk past KC re-reads chunk KC-1 with a zero
-    // activation row. Activation loads go first so their quantization can
-    // run while the weights are still in flight.
+    // consumed), a chunk past KC re-reads chunk KC-1 and a row past M
+    // re-reads row M-1, both with zero activations. Activation loads go
+    // first so their quantization can run while the weights are in flight.
     auto issue = [&](Batch& b, int s) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int st = min(s + u, se - 1);
             if constexpr (FUSED) {
-                const int jx = st * KS + qrow;
-                const XVec<E> v =
-                    load_xvec<E>(op.x + (size_t)min(jx, KC - 1) * kChunk + qpiece * E);
+                const int jx = st * KS + tq;
 #pragma unroll
-                for (int d = 0; d < E / 2; ++d) b.xv[u].d[d] = jx < KC ? v.d[d] : 0u;
+                for (int mt = 0; mt < MT; ++mt) {
+                    const int row = mt * 16 + mq;
+                    const XVec<E> v =
+                        load_xvec<E>(op.x + (size_t)min(row, M - 1) * K +
+                                     (size_t)min(jx, KC - 1) * kChunk + qpiece * E);
+                    const bool live = jx < KC && row < M;
+#pragma unroll
+                    for (int d = 0; d < E / 2; ++d) b.xv[u][mt].d[d] = live ? v.d[d] : 0u;
+                }
             } else {
-                const int ja = st * KS + r16;
-                const uint8_t* p = op.q + (size_t)min(ja, KC - 1) * kChunk + g * 16;
-                const i32x4 lo = ldg16(p), hi = ldg16(p + 64);
-                const bool live = r16 < KS && ja < KC;
-                b.alo[u] = live ? lo : i32x4{0, 0, 0, 0};
-                b.ahi[u] = live ? hi : i32x4{0, 0, 0, 0};
-                if constexpr (SM != kGemvConst)
-                    b.sa[u] = op.s[(size_t)min(st * KS + t, KC - 1) * op.s_step];
+                const int ja = st * KS + ta;
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const int row = mt * 16 + ma;
+                    const uint8_t* p = op.q + (size_t)min(row, M - 1) * K +
+                                       (size_t)min(ja, KC - 1) * kChunk + g * 16;
+                    const i32x4 lo = ldg16(p), hi = ldg16(p + 64);
+                    const bool live = r16 < R && row < M && ja < KC;
+                    b.alo[u][mt] = live ? lo : i32x4{0, 0, 0, 0};
+                    b.ahi[u][mt] = live ? hi : i32x4{0, 0, 0, 0};
+                    if constexpr (SM != kGemvConst) {
+                        const int tok = MR == 1 ? 0 : min(row, M - 1);
+                        const int j = min(st * KS + (MR == 1 ? t : ta), KC - 1);
+                        b.sa[u][mt] = op.s[(size_t)tok * op.s_ld + (size_t)j * op.s_step];
+                    }
+                }
             }
         }
 #pragma unroll
@@ -197,65 +250,87 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
         }
     };
 
-    float acc = 0.0f;
-    auto contract = [&](const i32x4& alo, const i32x4& ahi, const i32x4& blo,
-                        const i32x4& bhi, float scale) {
+    float acc[MT][NE];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < NE; ++i) acc[mt][i] = 0.0f;
+
+    auto contract = [&](int mt, const i32x4& alo, const i32x4& ahi, const i32x4& blo,
+                        const i32x4& bhi, const float* scl) {
         const f32x4 p = mfma_e4m3(join(alo, ahi), join(blo, bhi), f32x4{0, 0, 0, 0});
-        const float v = ei == 0 ? p[0] : ei == 1 ? p[1] : ei == 2 ? p[2] : p[3];
-        if constexpr (SM == kGemvConst) acc += v;
-        else acc += v * scale;
+#pragma unroll
+        for (int i = 0; i < NE; ++i) {
+            const float v = MR >= 4 ? p[i] : pick(p, e0 + i);
+            if constexpr (SM == kGemvConst) acc[mt][i] += v;
+            else acc[mt][i] += v * scl[i];
+        }
     };
 
     auto consume = [&](Batch& b, int s) {
         if constexpr (FUSED) {
             // 1. quantize the batch's chunks into this wave's LDS tiles
-            float sc[U];
+            float sc[U][MT];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 if (s + u >= se) break;
-                float m = 0.0f;
 #pragma unroll
-                for (int d = 0; d < E / 2; ++d)
-                    m = fmaxf(m, fmaxf(fabsf(bf16lo(b.xv[u].d[d])), fabsf(bf16hi(b.xv[u].d[d]))));
-                m = lanes_max<LPR>(m);
-                float inv;
-                group_scale_div(m, sc[u], inv);
-                uint32_t cd[(E + 3) / 4];
-                if constexpr (E == 2) {
-                    cd[0] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
-                        bf16lo(b.xv[u].d[0]) * inv, bf16hi(b.xv[u].d[0]) * inv, 0, false);
-                } else {
+                for (int mt = 0; mt < MT; ++mt) {
+                    const XVec<E>& xv = b.xv[u][mt];
+                    uint32_t mb = lanes_max_u<LPR>(absmax_bits(xv.d));
+                    if (__builtin_amdgcn_ballot_w64(mb > 0x7F80u) != 0)
+                        mb = lanes_max_u<LPR>(absmax_bits_skip_nan(xv.d));
+                    const float m = bf16_bits_f32(mb);
+                    float inv;
+                    group_scale_div(m, sc[u][mt], inv);
+                    uint32_t cd[(E + 3) / 4];
+                    if constexpr (E == 2) {
+                        cd[0] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
+                            bf16lo(xv.d[0]) * inv, bf16hi(xv.d[0]) * inv, 0, false);
+                    } else {
 #pragma unroll
-                    for (int d = 0; d < E / 4; ++d) {
-                        const uint32_t a0 = b.xv[u].d[2 * d], a1 = b.xv[u].d[2 * d + 1];
-                        cd[d] = pack4_e4m3(bf16lo(a0) * inv, bf16hi(a0) * inv,
-                                           bf16lo(a1) * inv, bf16hi(a1) * inv);
+                        for (int d = 0; d < E / 4; ++d) {
+                            const uint32_t a0 = xv.d[2 * d], a1 = xv.d[2 * d + 1];
+                            cd[d] = pack4_any(bf16lo(a0) * inv, bf16hi(a0) * inv,
+                                              bf16lo(a1) * inv, bf16hi(a1) * inv, a0);
+                        }
                     }
-                }
-                store_codes<E>(qlds[wave][u] + qrow * kChunk + qpiece * E, cd);
-                const int jx = (s + u) * KS + qrow;
-                if (args.write_ws && blockIdx.x == 0 && jx < KC) {
-                    store_codes<E>(op.q + (size_t)jx * kChunk + qpiece * E, cd);
-                    if (qpiece == 0) op.s[jx] = sc[u];
+                    store_codes<E>(qlds[wave][u][mt] + qrow * kChunk + qpiece * E, cd);
+                    const int jx = (s + u) * KS + tq;
+                    const int row = mt * 16 + mq;
+                    if (args.write_ws && blockIdx.x == 0 && jx < KC && row < M) {
+                        store_codes<E>(op.q + (size_t)row * K + (size_t)jx * kChunk + qpiece * E,
+                                       cd);
+                        if (qpiece == 0) op.s[(size_t)row * op.s_ld + jx] = sc[u][mt];
+                    }
                 }
             }
             __builtin_amdgcn_wave_barrier();
-            // 2. contract: A rows 0..KS-1 from LDS, the slot's scale from the
-            //    lanes that quantized it
+            // 2. contract: A rows 0..R-1 from LDS, each candidate row's scale
+            //    from the lanes that quantized it
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 if (s + u >= se) break;
-                const uint8_t* tile = qlds[wave][u];
-                i32x4 lo = i32x4{0, 0, 0, 0}, hi = i32x4{0, 0, 0, 0};
-                if (r16 < KS) {
-                    lo = *reinterpret_cast<const i32x4*>(tile + r16 * kChunk + g * 16);
-                    hi = *reinterpret_cast<const i32x4*>(tile + r16 * kChunk + 64 + g * 16);
-                }
-                const float sa = KS == 1 ? sc[u]
-                                         : __int_as_float(__builtin_amdgcn_ds_bpermute(
-                                               t * LPR * 4, __float_as_int(sc[u])));
                 const float sw = SM == kGemvBlock ? b.sw[u] : swc;
-                contract(lo, hi, b.blo[u], b.bhi[u], sa * sw);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const uint8_t* tile = qlds[wave][u][mt];
+                    i32x4 lo = i32x4{0, 0, 0, 0}, hi = i32x4{0, 0, 0, 0};
+                    if (r16 < R) {
+                        lo = *reinterpret_cast<const i32x4*>(tile + r16 * kChunk + g * 16);
+                        hi = *reinterpret_cast<const i32x4*>(tile + r16 * kChunk + 64 + g * 16);
+                    }
+                    float scl[NE];
+#pragma unroll
+                    for (int i = 0; i < NE; ++i) {
+                        const float sa =
+                            R == 1 ? sc[u][mt]
+                                   : __int_as_float(__builtin_amdgcn_ds_bpermute(
+                                         (rho + i) * LPR * 4, __float_as_int(sc[u][mt])));
+                        scl[i] = sa * sw;
+                    }
+                    contract(mt, lo, hi, b.blo[u], b.bhi[u], scl);
+                }
             }
             __builtin_amdgcn_wave_barrier();
         } else {
@@ -263,8 +338,20 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
             for (int u = 0; u < U; ++u) {
                 if (s + u >= se) break;
                 const float sw = SM == kGemvBlock ? b.sw[u] : swc;
-                contract(b.alo[u], b.ahi[u], b.blo[u], b.bhi[u],
-                         SM == kGemvConst ? 0.0f : b.sa[u] * sw);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    float scl[NE];
+#pragma unroll
+                    for (int i = 0; i < NE; ++i) {
+                        float sa = 0.0f;
+                        if constexpr (SM != kGemvConst)
+                            sa = MR == 1 ? b.sa[u][mt]
+                                         : __int_as_float(__builtin_amdgcn_ds_bpermute(
+                                               (rho + i) * 4, __float_as_int(b.sa[u][mt])));
+                        scl[i] = sa * sw;
+                    }
+                    contract(mt, b.alo[u][mt], b.ahi[u][mt], b.blo[u], b.bhi[u], scl);
+                }
             }
         }
     };
@@ -282,7 +369,10 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
     }
 
     // ---- the last wave to arrive sums the partials in a fixed order ----
-    red[wave][lane] = acc;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < NE; ++i) red[wave][mt * NE + i][lane] = acc[mt][i];
     int old = 0;
     if (lane == 0)
         old = __hip_atomic_fetch_add(&arrive, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -290,21 +380,34 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
     if (old != WAVES - 1) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 
-    if (lane < TW) {
+    // output (token mt*16 + m, column n0 + c2) = sum over waves w and slots
+    // ts of C row ts*MR + m, column ts*TW + c2
+    constexpr int OUTS = MT * MR * TW;
+    for (int o = lane; o < OUTS; o += 64) {
+        const int c2 = o % TW, m = (o / TW) % MR, mt = o / (TW * MR);
+        const int tok = mt * 16 + m;
+        if (tok >= M) continue;
         float v = 0.0f;
 #pragma unroll
         for (int w = 0; w < WAVES; ++w)
 #pragma unroll
-            for (int ts = 0; ts < KS; ++ts) v += red[w][(ts >> 2) * 16 + ts * TW + lane];
-        const int col = n0 + lane;
-        if constexpr (SM == kGemvConst) v = v * (op.s[0] * op.sw[col]);
+            for (int ts = 0; ts < KS; ++ts) {
+                const int rr = ts * MR + m;
+                v += red[w][mt * NE + (MR >= 4 ? (rr & 3) : m)][(rr >> 2) * 16 + ts * TW + c2];
+            }
+        const int col = n0 + c2;
+        if constexpr (SM == kGemvConst) {
+            const float sa = op.s[(size_t)tok * op.s_ld], sw = op.sw[col];
+            v = M == 1 ? v * (sa * sw) : (v * sa) * sw;
+        }
+        const size_t oi = (size_t)tok * op.N + col;
         if (op.c_f32) {
             float* c = static_cast<float*>(op.c);
-            c[col] = op.residual ? v + c[col] : v;
+            c[oi] = op.residual ? v + c[oi] : v;
         } else {
             uint16_t* c = static_cast<uint16_t*>(op.c);
-            if (op.residual) v += __uint_as_float((uint32_t)c[col] << 16);
-            c[col] = f32_to_bf16(v);
+            if (op.residual) v += __uint_as_float((uint32_t)c[oi] << 16);
+            c[oi] = f32_to_bf16(v);
         }
     }
 }
@@ -315,59 +418,102 @@ std::atomic<int> g_tune_ks{0};
 std::atomic<int> g_tune_waves{0};
 std::atomic<int> g_tune_u{0};
 
-template <int WAVES, int KS, int U>
+template <int WAVES, int KS, int MR, int MT, int U>
 hipError_t launch_ks(const GemvArgs& a, bool fused, hipStream_t stream, const LaunchTiming& t)
 {
     const dim3 grid(a.op.N / (16 / KS));
     const dim3 block(WAVES * 64);
     if (fused) {
         if (a.op.w_block)
-            return launch(fp8_gemv_kernel<WAVES, KS, U, true, kGemvBlock>, grid, block, 0,
-                          stream, t, a);
-        return launch(fp8_gemv_kernel<WAVES, KS, U, true, kGemvChannel>, grid, block, 0,
-                      stream, t, a);
+            return launch(fp8_gemv_kernel<WAVES, KS, MR, MT, U, true, kGemvBlock>, grid, block,
+                          0, stream, t, a);
+        return launch(fp8_gemv_kernel<WAVES, KS, MR, MT, U, true, kGemvChannel>, grid, block,
+                      0, stream, t, a);
     }
     if (a.op.w_block)
-        return launch(fp8_gemv_kernel<WAVES, KS, U, false, kGemvBlock>, grid, block, 0,
-                      stream, t, a);
+        return launch(fp8_gemv_kernel<WAVES, KS, MR, MT, U, false, kGemvBlock>, grid, block,
+                      0, stream, t, a);
     if (a.op.s_step == 0)
-        return launch(fp8_gemv_kernel<WAVES, KS, U, false, kGemvConst>, grid, block, 0,
-                      stream, t, a);
-    return launch(fp8_gemv_kernel<WAVES, KS, U, false, kGemvChannel>, grid, block, 0,
+        return launch(fp8_gemv_kernel<WAVES, KS, MR, MT, U, false, kGemvConst>, grid, block,
+                      0, stream, t, a);
+    return launch(fp8_gemv_kernel<WAVES, KS, MR, MT, U, false, kGemvChannel>, grid, block, 0,
                   stream, t, a);
 }
 
-template <int WAVES, int U>
-hipError_t launch_wu(const GemvArgs& a, bool fused, int ks, hipStream_t stream,
+template <int WAVES, int MR, int MT, int U>
+hipError_t launch_mr(const GemvArgs& a, bool fused, int ks, hipStream_t stream,
                      const LaunchTiming& t)
 {
-    switch (ks) {
-    case 8: return launch_ks<WAVES, 8, U>(a, fused, stream, t);
-    case 4: return launch_ks<WAVES, 4, U>(a, fused, stream, t);
-    case 2: return launch_ks<WAVES, 2, U>(a, fused, stream, t);
-    default: return launch_ks<WAVES, 1, U>(a, fused, stream, t);
+    if constexpr (8 * MR <= 16)
+        if (ks == 8) return launch_ks<WAVES, 8, MR, MT, U>(a, fused, stream, t);
+    if constexpr (4 * MR <= 16)
+        if (ks == 4) return launch_ks<WAVES, 4, MR, MT, U>(a, fused, stream, t);
+    if constexpr (2 * MR <= 16)
+        if (ks == 2) return launch_ks<WAVES, 2, MR, MT, U>(a, fused, stream, t);
+    return launch_ks<WAVES, 1, MR, MT, U>(a, fused, stream, t);
+}
+
+template <int WAVES, int U>
+hipError_t launch_wu(const GemvArgs& a, bool fused, int ks, int mr, hipStream_t stream,
+                     const LaunchTiming& t)
+{
+    // 16-wave workgroups (128 VGPRs a lane) serve the one-slot, one-tile
+    // shapes of 8 < M <= 16 only, where N/16 workgroups are few.
+    if constexpr (WAVES < 16) {
+        switch (mr) {
+        case 1: return launch_mr<WAVES, 1, 1, U>(a, fused, ks, stream, t);
+        case 2: return launch_mr<WAVES, 2, 1, U>(a, fused, ks, stream, t);
+        case 4: return launch_mr<WAVES, 4, 1, U>(a, fused, ks, stream, t);
+        case 8: return launch_mr<WAVES, 8, 1, U>(a, fused, ks, stream, t);
+        default: break;
+        }
+        if (a.op.M > 16) return launch_ks<WAVES, 1, 16, 2, U>(a, fused, stream, t);
     }
+    return launch_ks<WAVES, 1, 16, 1, U>(a, fused, stream, t);
 }
 
 }  // namespace
 
-// Launch shape: the fewest chunk slots that give >= 600 workgroups (about
-// 2.3 per CU); 4 waves when there are at most 8 steps, else 8; 2-step
-// batches when each wave has at most 2 steps, else 1-step batches.
-void gemv_shape(int N, int K, int* ks, int* waves, int* u)
+// Fused quantization re-quantizes x in every workgroup (N*KS/16 of them).
+// Up to M = 16 that costs less than a separate quantizer launch on every
+// config shape; with two 16-row tiles it pays only while N*K is small
+// (measured on MI355X: faster at qkv and o_proj, slower at gate_up and
+// down, M = 32).
+bool gemv_fuses(int M, int N, int K)
 {
+    return M <= 16 || (long)N * K <= (16L << 20);
+}
+
+int gemv_rows(int M)
+{
+    return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16;
+}
+
+// Launch shape: the fewest chunk slots (at most 16 / rows-per-slot) that
+// give >= 600 workgroups (about 2.3 per CU); 4 waves when there are at most
+// 8 steps, else 8 (16 only when forced, for 8 < M <= 16); at M = 1, 2-step
+// batches when each wave has at most 2 steps, else (and for M > 1, whose
+// wider activation tiles need the registers) 1-step batches.
+void gemv_shape(int M, int N, int K, int* ks, int* waves, int* u)
+{
+    const int mr = gemv_rows(M);
+    const int kmax = mr >= 2 ? 16 / mr : 8;
     const int tiles = N / 16, KC = K / kChunk;
     int k = 1;
-    while (k < 8 && tiles * k < 600) k *= 2;
+    while (k < kmax && tiles * k < 600) k *= 2;
+    const int fk = g_tune_ks.load(std::memory_order_relaxed);
+    if (fk) k = fk < kmax ? fk : kmax;
     const int S = (KC + k - 1) / k;
     int w = S <= 8 ? 4 : 8;
-    int uu = (S + w - 1) / w <= 2 ? 2 : 1;
-    const int fk = g_tune_ks.load(std::memory_order_relaxed);
     const int fw = g_tune_waves.load(std::memory_order_relaxed);
+    if (fw) w = fw == 16 && (mr != 16 || M > 16) ? 8 : fw;
+    int uu = mr == 1 && (S + w - 1) / w <= 2 ? 2 : 1;
     const int fu = g_tune_u.load(std::memory_order_relaxed);
-    *ks = fk ? fk : k;
-    *waves = fw ? fw : w;
-    *u = fu ? fu : uu;
+    if (fu) uu = fu;
+    if (w == 16) uu = 1;    // two-step batches would not fit 128 VGPRs
+    *ks = k;
+    *waves = w;
+    *u = uu;
 }
 
 hipError_t launch_fp8_gemv(const Fp8Operands& op, bool fused, hipStream_t stream,
@@ -375,13 +521,20 @@ hipError_t launch_fp8_gemv(const Fp8Operands& op, bool fused, hipStream_t stream
 {
     GemvArgs a{op, fused};
     int ks, waves, u;
-    gemv_shape(op.N, op.K, &ks, &waves, &u);
-    *name = fused ? "fp8_gemv_fused_m1" : "fp8_gemv_m1";
-    if (waves == 8)
-        return u == 2 ? launch_wu<8, 2>(a, fused, ks, stream, t)
-                      : launch_wu<8, 1>(a, fused, ks, stream, t);
-    return u == 2 ? launch_wu<4, 2>(a, fused, ks, stream, t)
-                  : launch_wu<4, 1>(a, fused, ks, stream, t);
+    gemv_shape(op.M, op.N, op.K, &ks, &waves, &u);
+    const int mr = gemv_rows(op.M);
+    if (op.M == 1) *name = fused ? "fp8_gemv_fused_m1" : "fp8_gemv_m1";
+    else if (op.M <= 16) *name = fused ? "fp8_gemv_fused_m16" : "fp8_gemv_m16";
+    else *name = fused ? "fp8_gemv_fused_m32" : "fp8_gemv_m32";
+    switch (waves) {
+    case 16: return launch_wu<16, 1>(a, fused, ks, mr, stream, t);
+    case 8:
+        return u == 2 ? launch_wu<8, 2>(a, fused, ks, mr, stream, t)
+                      : launch_wu<8, 1>(a, fused, ks, mr, stream, t);
+    default:
+        return u == 2 ? launch_wu<4, 2>(a, fused, ks, mr, stream, t)
+                      : launch_wu<4, 1>(a, fused, ks, mr, stream, t);
+    }
 }
 
 void gemv_tune(int ks, int waves, int u)

@@ -69,13 +69,56 @@ __device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float 
     return (uint32_t)w;
 }
 
-__device__ __forceinline__ float absmax8(const uint4& v, float m)
+// Largest |x| over bf16 values held two per dword, as bf16 magnitude bits
+// (0 .. 0x7FFF). For values that are not NaN, |x| orders as the unsigned
+// integer bits & 0x7FFF, so two values cost one AND and one packed 16-bit
+// max. A result above 0x7F80 means a NaN is present; then the reference's
+// amax, whose `v > local` test skips NaN (kernels.mojo:153-160), is the
+// *_skip_nan form. (A float max chain is no substitute: v_max3_f32 returns
+// NaN for a signalling-NaN operand and so drops the running maximum.)
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+template <int N>
+__device__ __forceinline__ uint32_t absmax_bits(const uint32_t (&d)[N], uint32_t m = 0)
 {
-    m = fmaxf(m, fabsf(bf16lo(v.x))); m = fmaxf(m, fabsf(bf16hi(v.x)));
-    m = fmaxf(m, fabsf(bf16lo(v.y))); m = fmaxf(m, fabsf(bf16hi(v.y)));
-    m = fmaxf(m, fabsf(bf16lo(v.z))); m = fmaxf(m, fabsf(bf16hi(v.z)));
-    m = fmaxf(m, fabsf(bf16lo(v.w))); m = fmaxf(m, fabsf(bf16hi(v.w)));
+    u16x2 p = {0, 0};
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        p = __builtin_elementwise_max(p, __builtin_bit_cast(u16x2, d[i] & 0x7FFF7FFFu));
+    const uint32_t r = p.x > p.y ? p.x : p.y;
+    return r > m ? r : m;
+}
+
+template <int N>
+__device__ __forceinline__ uint32_t absmax_bits_skip_nan(const uint32_t (&d)[N], uint32_t m = 0)
+{
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const uint32_t lo = d[i] & 0x7FFFu, hi = (d[i] >> 16) & 0x7FFFu;
+        if (lo <= 0x7F80u && lo > m) m = lo;
+        if (hi <= 0x7F80u && hi > m) m = hi;
+    }
     return m;
+}
+
+__device__ __forceinline__ uint32_t absmax_bits8(const uint4& v, uint32_t m = 0)
+{
+    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+    return absmax_bits(d, m);
+}
+
+__device__ __forceinline__ uint32_t absmax_bits8_skip_nan(const uint4& v, uint32_t m = 0)
+{
+    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+    return absmax_bits_skip_nan(d, m);
+}
+
+// The magnitude bits as the float they encode.
+__device__ __forceinline__ float bf16_bits_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ __forceinline__ uint32_t shfl_xor_u(uint32_t v, int o)
+{
+    return (uint32_t)__shfl_xor((int)v, o);
 }
 
 // Eight bf16 times inv -> eight codes in two dwords.

@@ -70,14 +70,18 @@ hipError_t launch_fp8_skinny(const Fp8Operands& op, bool fused, hipStream_t stre
 // Overrides for the skinny kernel's launch shape (0 = automatic).
 void skinny_tune(int waves, int u);
 
-// M = 1 kernel with K-chunk slots in the MFMA rows. fused: quantize x
+// M <= 32 kernel with K-chunk slots in the MFMA rows. fused: quantize x
 // inside the kernel (group 128); workgroup 0 also writes q/s.
 hipError_t launch_fp8_gemv(const Fp8Operands& op, bool fused, hipStream_t stream,
                            const LaunchTiming& t, const char** name);
 
-// Its launch shape (chunk slots, waves, steps per batch) for N x K, and
-// overrides of each (0 = automatic).
-void gemv_shape(int N, int K, int* ks, int* waves, int* u);
+// Rows per chunk slot for M rows (M rounded up to a power of two, at most
+// 16), and the launch shape (chunk slots, waves, steps per batch) for
+// M x N x K with the overrides of each (0 = automatic).
+int gemv_rows(int M);
+// Whether the chunk-slot kernel quantizes x itself for M x N x K (group 128).
+bool gemv_fuses(int M, int N, int K);
+void gemv_shape(int M, int N, int K, int* ks, int* waves, int* u);
 void gemv_tune(int ks, int waves, int u);
 
 // Tiled MFMA GEMM for any M (prefill); reads q/s from the workspace.

@@ -5,7 +5,8 @@
 // e4m3(x * (1/scale)). The reference reduces one whole row with a 256-thread
 // LDS tree; here a 1x128 group is 16 lanes x 8 bf16 reduced with cross-lane
 // max, so one wave quantizes four groups with one 16-byte load per lane and
-// no LDS or barrier. The per-token form (group = K) keeps one workgroup per
+// no LDS or barrier. The amax is taken on the bf16 magnitude bits (NaN
+// skipped, as the reference's `v > local` test does). The per-token form (group = K) keeps one workgroup per
 // row.
 #include "heph_kernels.h"
 
@@ -24,13 +25,14 @@ __global__ __launch_bounds__(256) void quant_g128_kernel(
     const bool live = g < n_groups;
     uint4 v = make_uint4(0, 0, 0, 0);
     if (live) v = ldg16u(x + g * kChunk + j * 8);
-    float m = absmax8(v, 0.0f);
-    m = fmaxf(m, __shfl_xor(m, 1));
-    m = fmaxf(m, __shfl_xor(m, 2));
-    m = fmaxf(m, __shfl_xor(m, 4));
-    m = fmaxf(m, __shfl_xor(m, 8));
+    uint32_t mb = absmax_bits8(v);
+    for (int o = 1; o < 16; o <<= 1) mb = max(mb, shfl_xor_u(mb, o));
+    if (__builtin_amdgcn_ballot_w64(mb > 0x7F80u) != 0) {    // a group holds NaN
+        mb = absmax_bits8_skip_nan(v);
+        for (int o = 1; o < 16; o <<= 1) mb = max(mb, shfl_xor_u(mb, o));
+    }
     float s, inv;
-    group_scale(m, s, inv);
+    group_scale(bf16_bits_f32(mb), s, inv);
     if (live) {
         *reinterpret_cast<uint2*>(q + g * kChunk + j * 8) = quant8(v, inv);
         if (j == 0) scales[g] = s;
@@ -42,18 +44,18 @@ __global__ __launch_bounds__(256) void quant_row_kernel(
     const uint16_t* __restrict__ x, uint8_t* __restrict__ q,
     float* __restrict__ scales, int K)
 {
-    __shared__ float red[4];
+    __shared__ uint32_t red[4];
     const int row = blockIdx.x;
     const uint16_t* xr = x + (size_t)row * K;
     uint8_t* qr = q + (size_t)row * K;
-    float m = 0.0f;
-    for (int k = threadIdx.x * 8; k < K; k += 256 * 8) m = absmax8(ldg16u(xr + k), m);
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    uint32_t m = 0;
+    for (int k = threadIdx.x * 8; k < K; k += 256 * 8) m = absmax_bits8_skip_nan(ldg16u(xr + k), m);
+    for (int o = 32; o >= 1; o >>= 1) m = max(m, shfl_xor_u(m, o));
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    m = max(max(red[0], red[1]), max(red[2], red[3]));
     float s, inv;
-    group_scale(m, s, inv);
+    group_scale(bf16_bits_f32(m), s, inv);
     if (threadIdx.x == 0) scales[row] = s;
     for (int k = threadIdx.x * 8; k < K; k += 256 * 8)
         *reinterpret_cast<uint2*>(qr + k) = quant8(ldg16u(xr + k), inv);

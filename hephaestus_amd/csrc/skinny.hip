@@ -23,7 +23,8 @@
 //     (acc*sa)*sw otherwise (:973, :848);
 //   * fused mode (group 128, M <= 4) quantizes x inside the kernel: lane l
 //     quantizes 8 elements of row l/16 (one 16-byte load), the row's
-//     128-element group max is reduced across its 16 lanes with DPP, and
+//     128-element group max (on bf16 magnitude bits, NaN skipped) is
+//     reduced across its 16 lanes with DPP, and
 //     the codes reach the MFMA operand layout through a per-wave LDS slot.
 //     Workgroup 0 also writes q/s so later SKIP_QUANT calls can reuse them.
 #include <atomic>
@@ -45,19 +46,19 @@ enum ScaleMode { kBlock = 0, kChannel = 1, kConst = 2 };
 namespace {
 
 template <int CTRL>
-__device__ __forceinline__ float dpp_f(float x)
+__device__ __forceinline__ uint32_t dpp_u(uint32_t x)
 {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, CTRL, 0xf, 0xf, false);
 }
 
 // max over the 16 lanes of each DPP row (lanes 16r .. 16r+15):
 // quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror.
-__device__ __forceinline__ float row16_max(float v)
+__device__ __forceinline__ uint32_t row16_max_u(uint32_t v)
 {
-    v = fmaxf(v, dpp_f<0xB1>(v));
-    v = fmaxf(v, dpp_f<0x4E>(v));
-    v = fmaxf(v, dpp_f<0x141>(v));
-    v = fmaxf(v, dpp_f<0x140>(v));
+    v = max(v, dpp_u<0xB1>(v));
+    v = max(v, dpp_u<0x4E>(v));
+    v = max(v, dpp_u<0x141>(v));
+    v = max(v, dpp_u<0x140>(v));
     return v;
 }
 
@@ -192,17 +193,24 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_skinny_kernel(SkinnyArgs args)
             for (int u = 0; u < U; ++u) {
                 const int j = kc + u;
                 if (j >= ke) break;
-                float m = row16_max(absmax8(b.xv[u], 0.0f));
-                if constexpr (LPR == 32) m = fmaxf(m, __shfl_xor(m, 16));
-                if constexpr (LPR == 64) {
-                    const float m0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0));
-                    const float m1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16));
-                    const float m2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32));
-                    const float m3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 48));
-                    m = fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
-                }
+                // group amax on the bf16 magnitude bits (NaN skipped)
+                auto group_max = [&](uint32_t v) {
+                    v = row16_max_u(v);
+                    if constexpr (LPR == 32) v = max(v, shfl_xor_u(v, 16));
+                    if constexpr (LPR == 64) {
+                        const uint32_t m0 = __builtin_amdgcn_readlane((int)v, 0);
+                        const uint32_t m1 = __builtin_amdgcn_readlane((int)v, 16);
+                        const uint32_t m2 = __builtin_amdgcn_readlane((int)v, 32);
+                        const uint32_t m3 = __builtin_amdgcn_readlane((int)v, 48);
+                        v = max(max(m0, m1), max(m2, m3));
+                    }
+                    return v;
+                };
+                uint32_t mb = group_max(absmax_bits8(b.xv[u]));
+                if (__builtin_amdgcn_ballot_w64(mb > 0x7F80u) != 0)
+                    mb = group_max(absmax_bits8_skip_nan(b.xv[u]));
                 float sc, inv;
-                group_scale(m, sc, inv);
+                group_scale(bf16_bits_f32(mb), sc, inv);
                 scl[u] = sc;
                 const uint2 c = quant8(b.xv[u], inv);
                 uint8_t* slot = qlds[wave][u] + qrow * 128 + qpiece * E;

@@ -15,7 +15,7 @@ __global__ __launch_bounds__(256) void wquant_block_kernel(
     const uint16_t* __restrict__ w, uint8_t* __restrict__ q,
     float* __restrict__ scale_inv, int N, int K)
 {
-    __shared__ float red[4];
+    __shared__ uint32_t red[4];
     const int KB = K / kChunk;
     const int bn = blockIdx.y, bk = blockIdx.x;
     const int tid = threadIdx.x;
@@ -23,18 +23,21 @@ __global__ __launch_bounds__(256) void wquant_block_kernel(
     const int col = (tid & 15) * 8;
     uint4 v[8];
     bool ok[8];
-    float m = 0.0f;
+    uint32_t mb = 0;
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
         const int row = bn * kChunk + (tid >> 4) + 16 * r;
         ok[r] = row < N;
         v[r] = ok[r] ? ldg16u(w + (size_t)row * K + bk * kChunk + col) : make_uint4(0, 0, 0, 0);
-        m = absmax8(v[r], m);
+        mb = absmax_bits8(v[r], mb);
     }
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    if ((tid & 63) == 0) red[tid >> 6] = m;
+    for (int o = 32; o >= 1; o >>= 1) mb = max(mb, shfl_xor_u(mb, o));
+    if ((tid & 63) == 0) red[tid >> 6] = mb;
     __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // numpy's max propagates NaN: a block holding NaN has a NaN amax, fails
+    // `amax > 0` and takes s = 1 (as NaN bits sort above every other
+    // magnitude, the integer max carries it through)
+    const float m = bf16_bits_f32(max(max(red[0], red[1]), max(red[2], red[3])));
     float s = m > 0.0f ? __fdiv_rn(m, kE4M3Max) : 1.0f;
     if (s < 1e-12f) s = 1.0f;
     if (tid == 0) scale_inv[(size_t)bn * KB + bk] = s;

@@ -58,11 +58,11 @@ extern "C" {
 /* flags for heph_fp8_linear / heph_bf16_linear */
 #define HEPH_FLAG_ADD_RESIDUAL 0x1  /* c += result (c is read, then written) */
 #define HEPH_FLAG_SKIP_QUANT   0x2  /* q_ws / s_ws already hold this x's codes */
-#define HEPH_FLAG_FORCE_SKINNY 0x4  /* use the M <= 32 kernel (tests) */
+#define HEPH_FLAG_FORCE_SKINNY 0x4  /* use the 16-column M <= 32 kernel (tests) */
 #define HEPH_FLAG_FORCE_GEMM   0x8  /* use the tiled MFMA GEMM (tests) */
 #define HEPH_FLAG_NO_FUSE      0x10 /* quantize in its own kernel (tests) */
 
-/* Largest M served by the weight-streaming (skinny) kernel. */
+/* Largest M served by the weight-streaming kernels (chunk-slot GEMV, skinny). */
 #define HEPH_SKINNY_MAX_M 32
 
 /*
@@ -147,13 +147,15 @@ const char* heph_last_kernel(void);
 /*
  * Launch-shape overrides for measurement sweeps (process-wide; 0 restores
  * the built-in choice). No counterpart in the reference.
- *   HEPH_TUNE_SKINNY_WAVES  waves per workgroup of the 2 <= M <= 32 kernel:
+ *   HEPH_TUNE_SKINNY_WAVES  waves per workgroup of the forced skinny kernel:
  *                           0, 2, 4, 8 or 16
  *   HEPH_TUNE_SKINNY_U      chunks per load batch: 0, 2 or 4
- *   HEPH_TUNE_GEMV_KS       K-chunk slots per MFMA of the M = 1 kernel:
- *                           0, 1, 2, 4 or 8
- *   HEPH_TUNE_GEMV_WAVES    waves per workgroup of the M = 1 kernel: 0, 4, 8
- *   HEPH_TUNE_GEMV_U        steps per load batch of the M = 1 kernel: 0, 1, 2
+ *   HEPH_TUNE_GEMV_KS       K-chunk slots per MFMA of the M <= 32 chunk-slot
+ *                           kernel: 0, 1, 2, 4 or 8 (capped at 16 / rows per
+ *                           slot, i.e. 1 for M > 8)
+ *   HEPH_TUNE_GEMV_WAVES    its waves per workgroup: 0, 4, 8 or 16 (16 only
+ *                           for 8 < M <= 16; 8 is used otherwise)
+ *   HEPH_TUNE_GEMV_U        its steps per load batch: 0, 1, 2 (1 with 16 waves)
  *   HEPH_TUNE_GEMM_BM       tile height of the M >= 1024 GEMM: 0, 128, 192, 256
  */
 #define HEPH_TUNE_SKINNY_WAVES 1

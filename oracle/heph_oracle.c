@@ -163,8 +163,10 @@ int heph_oracle_quant_weight(const float* w, int N, int K, int bn, int bk,
             float amax = 0.0f;
             for (int n = n0; n < n1; ++n)
                 for (int k = k0; k < k1; ++k) {
+                    /* np.max propagates NaN; a NaN amax then fails
+                     * `amax > 0` below and takes s = 1 */
                     const float v = fabsf(w[(size_t)n * K + k]);
-                    if (v > amax) amax = v;
+                    if (v > amax || v != v) amax = v;
                 }
             float s = amax > 0.0f ? amax / 448.0f : 1.0f;
             if (s < 1e-12f) s = 1.0f;

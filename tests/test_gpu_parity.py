@@ -114,16 +114,79 @@ def test_quant_codes_bit_exact_oracle(M, K):
         assert np.array_equal(q.cpu().numpy().reshape(qo.shape), qo)
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 9, 16, 17, 32])
 def test_fused_quant_writes_workspace(M):
     N, K = 256, 4096
     x = O.gen_act_bf16(40 + M, M, K)
     qw, sw = O.gen_weight(41, N, K)
     _, q_ws, s_ws = run_linear(qw, sw, x, M=M, N=N, K=K)
-    assert HK.last_kernel() == ("fp8_gemv_fused_m1" if M == 1 else "fp8_skinny_fused_m4")
+    assert HK.last_kernel() == ("fp8_gemv_fused_m1" if M == 1 else
+                                "fp8_gemv_fused_m16" if M <= 16 else "fp8_gemv_fused_m32")
     qo, so = O.quant_act(x, 128)
     assert np.array_equal(q_ws.cpu().numpy().reshape(M, K), qo)
     assert np.array_equal(s_ws.cpu().numpy().reshape(M, K // 128), so)
+
+
+def nan_inf_rows(M, K, seed):
+    """bf16 rows whose 1x128 groups hold NaN (both signs, quiet and
+    signalling payloads), +-inf, NaN beside the group's largest value, or
+    nothing special."""
+    x = O.gen_act_bf16(seed, M, K).copy()
+    rng = np.random.default_rng(seed)
+    specials = [0x7FC0, 0xFFC0, 0x7F81, 0xFF81, 0x7F80, 0xFF80]
+    for r in range(M):
+        for gi in range(K // 128):
+            kind = (r * 7 + gi) % 5
+            if kind == 4:
+                continue
+            pos = gi * 128 + rng.choice(128, size=2, replace=False)
+            if kind < 3:
+                x[r, pos[0]] = specials[(r + gi) % 4]        # a NaN
+            if kind == 1:
+                x[r, pos[1]] = 0x4400                        # 512 beside it
+            if kind == 3:
+                x[r, pos[1]] = specials[4 + (r + gi) % 2]    # an infinity
+    return x
+
+
+def codes_match(got, want):
+    """Codes equal, except that a NaN code may carry either sign."""
+    nan_w = (want & 0x7F) == 0x7F
+    nan_g = (got & 0x7F) == 0x7F
+    return np.array_equal(nan_w, nan_g) and np.array_equal(got[~nan_w], want[~nan_w])
+
+
+@pytest.mark.parametrize("M", [1, 3, 4, 16, 32])
+def test_quant_nan_and_inf_groups(M):
+    # NaN is skipped by the amax (the reference's `v > local` test,
+    # kernels.mojo:153-160); an infinite amax gives s = inf, inv = 0 and so
+    # NaN codes for the infinities and zero for the rest. Scales are
+    # bit-exact in every path (separate kernel, every fused kernel), codes
+    # too except the sign of NaN codes.
+    N, K = 256, 2560
+    x = nan_inf_rows(M, K, 90 + M)
+    qo, so = O.quant_act(x, 128)
+    assert np.isinf(so).any() and ((qo & 0x7F) == 0x7F).any()
+    q = torch.zeros(M * K, dtype=torch.uint8, device="cuda")
+    s = torch.zeros(M * (K // 128), dtype=torch.float32, device="cuda")
+    HK.quantize_act_rows_fp8(q, s, dev(x), M, K, group_k=128)
+    torch.cuda.synchronize()
+    sg = s.cpu().numpy().reshape(so.shape)
+    bad = np.argwhere(sg.view(np.uint32) != so.view(np.uint32))
+    assert bad.size == 0, [(r, g, sg[r, g], so[r, g],
+                            [hex(v) for v in x[r, g * 128:(g + 1) * 128] if (v & 0x7F80) == 0x7F80])
+                           for r, g in bad[:4]]
+    assert codes_match(q.cpu().numpy().reshape(qo.shape), qo)
+    qw, sw = O.gen_weight(91, N, K)
+    try:
+        for ks in ((1, 2, 4, 8) if M == 1 else (0,)):
+            HK.set_tuning(L.TUNE_GEMV_KS, ks)
+            _, q_ws, s_ws = run_linear(qw, sw, x, M=M, N=N, K=K)
+            assert HK.last_kernel().startswith("fp8_gemv_fused"), HK.last_kernel()
+            assert np.array_equal(s_ws.cpu().numpy().reshape(so.shape), so), ks
+            assert codes_match(q_ws.cpu().numpy().reshape(qo.shape), qo), ks
+    finally:
+        HK.set_tuning(L.TUNE_GEMV_KS, 0)
 
 
 # ------------------------------------------------ exact-integer parity ----
@@ -147,7 +210,7 @@ def test_exact_integer_bit_exact(M, N, K):
     ref = (ia.astype(np.float64) @ iw.astype(np.float64).T) * 0.0625 * 2.0 ** -5
     want = bf16_of(ref.astype(np.float32))
     forced = ((L.FLAG_FORCE_SKINNY,) if M <= 32 else ()) + (L.FLAG_FORCE_GEMM,)
-    for flags in ((0,) if M == 1 else ()) + forced:
+    for flags in ((0,) if M <= 32 else ()) + forced:
         c, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, flags=flags, skip_quant=True,
                              q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
         got = host_bf16(c)
@@ -178,7 +241,7 @@ def test_reference_smoke_cross_kernel(M, N, K):
         ref = (acc * np.float32(0.02)) * np.float32(0.01)
     want = bf16_of(np.float32([ref]))[0]
     outs = []
-    for flags in ((0,) if M == 1 else ()) + (L.FLAG_FORCE_SKINNY, L.FLAG_FORCE_GEMM):
+    for flags in (0, L.FLAG_FORCE_SKINNY, L.FLAG_FORCE_GEMM):
         c, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, group_k=K, flags=flags,
                              skip_quant=True, q_ws=dev(qa), s_ws=dev(sa))
         outs.append(host_bf16(c))
@@ -196,12 +259,13 @@ def test_reference_granularity_random_cross_kernel():
     w = O.gen_normal(32, N * K, 0.0, 0.02).reshape(N, K)
     qw, sw = O.quant_weight(w, 1, K)
     outs = []
-    for flags in (L.FLAG_FORCE_SKINNY, L.FLAG_FORCE_GEMM):
+    for flags in (0, L.FLAG_FORCE_SKINNY, L.FLAG_FORCE_GEMM):
         c, _, _ = run_linear(qw, sw, x, M=M, N=N, K=K, group_k=K, flags=flags)
         outs.append(host_bf16(c))
     ref = O.quant_linear(x, qw, sw, group_k=K, bn=1, bk=K)
-    check_close(outs[0], ref, "per-channel skinny")
-    check_close(outs[1], ref, "per-channel gemm")
+    check_close(outs[0], ref, "per-channel chunk-slot")
+    check_close(outs[1], ref, "per-channel skinny")
+    check_close(outs[2], ref, "per-channel gemm")
 
 
 @pytest.mark.parametrize("N,K", [(16, 128), (48, 384), (2560, 1152), (2560, 9728)])
@@ -252,6 +316,75 @@ def test_gemv_every_launch_shape(N, K):
             HK.set_tuning(knob, 0)
 
 
+def gemv_shapes(M):
+    """Distinct (chunk slots, waves, steps per batch) launch shapes of the
+    chunk-slot kernel at M rows: slots are capped at 16 / rows-per-slot,
+    16 waves serve 8 < M <= 16 only and always take 1-step batches."""
+    mr = 1 if M == 1 else 2 if M <= 2 else 4 if M <= 4 else 8 if M <= 8 else 16
+    kmax = 8 if mr == 1 else 16 // mr
+    out = []
+    for ks in (1, 2, 4, 8):
+        if ks > kmax:
+            continue
+        for waves in (4, 8, 16) if 8 < M <= 16 else (4, 8):
+            for u in ((1,) if waves == 16 else (1, 2)):
+                out.append((ks, waves, u))
+    return out
+
+
+@pytest.mark.parametrize("M", [2, 3, 4, 5, 8, 9, 16, 17, 32])
+@pytest.mark.parametrize("N,K", [(48, 384), (2560, 1152)])
+def test_gemv_rows_every_launch_shape(M, N, K):
+    # The chunk-slot kernel at M rows (KS slots of MR rows, or two 16-row
+    # tiles past M = 16) at every launch shape, with ragged step counts
+    # (K/128 = 3 and 9 chunks): exact-integer inputs stay bit-exact; fused
+    # quantization stays within tolerance of the oracle, writes
+    # the oracle's codes and equals separate quantization bit for bit;
+    # per-token activations with per-channel weights and per-channel
+    # weights with 1x128 activation groups stay within tolerance.
+    ia, qa = lattice(M, K, 800 + M + K)
+    iw, qw = lattice(N, K, 900 + N)
+    sa = np.full(M * (K // 128), 2.0 ** -3, np.float32)
+    sw = np.full((-(-N // 128), K // 128), 2.0 ** -2, np.float32)
+    want = bf16_of(((ia.astype(np.float64) @ iw.astype(np.float64).T) * 2.0 ** -9)
+                   .astype(np.float32))
+    x = O.gen_act_bf16(710 + M + N + K, M, K)
+    rw = O.gen_normal(711 + N, N * K, 0.0, 0.02).reshape(N, K)
+    bq, bs = O.quant_weight(rw)
+    cq, cs = O.quant_weight(rw, 1, K)
+    ref_b = O.quant_linear(x, bq, bs)
+    ref_c = O.quant_linear(x, cq, cs, group_k=K, bn=1, bk=K)
+    ref_bc = O.quant_linear(x, cq, cs, group_k=128, bn=1, bk=K)
+    qo, so = O.quant_act(x, 128)
+    plain = "fp8_gemv_m32" if M > 16 else "fp8_gemv_m16"
+    try:
+        for cfg in gemv_shapes(M):
+            ks, waves, u = cfg
+            HK.set_tuning(L.TUNE_GEMV_KS, ks)
+            HK.set_tuning(L.TUNE_GEMV_WAVES, waves)
+            HK.set_tuning(L.TUNE_GEMV_U, u)
+            c, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, skip_quant=True,
+                                 q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
+            assert HK.last_kernel() == plain
+            got = host_bf16(c)
+            assert np.array_equal(got, want), (cfg, np.argwhere(got != want)[:5].tolist())
+            f, q_ws, s_ws = run_linear(bq, bs, x, M=M, N=N, K=K)
+            check_close(host_bf16(f), ref_b, f"block {cfg}")
+            assert HK.last_kernel() == "fp8_gemv_fused_" + plain[-3:]
+            assert np.array_equal(q_ws.cpu().numpy().reshape(M, K), qo), cfg
+            assert np.array_equal(s_ws.cpu().numpy().reshape(M, K // 128), so), cfg
+            nf, _, _ = run_linear(bq, bs, x, M=M, N=N, K=K, flags=L.FLAG_NO_FUSE)
+            assert HK.last_kernel() == plain
+            assert np.array_equal(host_bf16(f), host_bf16(nf)), cfg
+            pc, _, _ = run_linear(cq, cs, x, M=M, N=N, K=K, group_k=K)
+            check_close(host_bf16(pc), ref_c, f"per-token {cfg}")
+            pf, _, _ = run_linear(cq, cs, x, M=M, N=N, K=K)
+            check_close(host_bf16(pf), ref_bc, f"per-channel {cfg}")
+    finally:
+        for knob in (L.TUNE_GEMV_KS, L.TUNE_GEMV_WAVES, L.TUNE_GEMV_U):
+            HK.set_tuning(knob, 0)
+
+
 # ----------------------------------------------------- random parity ----
 
 @pytest.mark.parametrize("name", sorted(SHAPES))
@@ -273,6 +406,10 @@ def test_small_m(M, name):
     x = O.gen_act_bf16(100 + M, M, K)
     qw, sw = O.gen_weight(1000 + N + K, N, K)
     c, _, _ = run_linear(qw, sw, x, M=M, N=N, K=K)
+    # M = 32 quantizes in the kernel at qkv (N*K <= 16M), separately at down
+    want = ("fp8_gemv_fused_m16" if M <= 16 else
+            "fp8_gemv_fused_m32" if N * K <= 16 << 20 else "fp8_gemv_m32")
+    assert HK.last_kernel() == want
     check_close(host_bf16(c), O.quant_linear(x, qw, sw), f"{name} M={M}")
 
 
@@ -305,7 +442,7 @@ def test_prefill_m4096_sampled_rows():
 
 # ------------------------------------------------ variant equivalence ----
 
-@pytest.mark.parametrize("M", [1, 2, 4])
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 16, 32])
 def test_fused_equals_separate_quant(M):
     N, K = SHAPES["o_proj"]
     x = O.gen_act_bf16(7 + M, M, K)
@@ -420,11 +557,17 @@ def test_weight_quant_vs_oracle(N, K):
     from hephaestus_amd.weights import quantize_weight_fp8
     w = bf16_of(O.gen_normal(N + K, N * K, 0.0, 0.02)).reshape(N, K)
     w[0, :7] = bf16_of(np.float32([0.5, -0.7, 1e-3, 0, 0, 3.0, -3.0]))   # a wide block
+    # a block holding a signalling NaN beside its largest value takes s = 1
+    # (numpy's max propagates NaN, scripts/stage_tiny_fp8_from_bf16.py:65-68);
+    # one holding an infinity takes s = inf
+    w[N - 1, 3], w[N - 1, 4] = 0xFF81, bf16_of(np.float32([5.0]))[0]
+    w[N // 2, K - 1] = 0x7F80
     q, s = quantize_weight_fp8(dev(w))
     torch.cuda.synchronize()
     qo, so = O.quant_weight(f32_of_bf16(w), 128, 128)
+    assert so[(N - 1) // 128, 0] == 1.0 and np.isinf(so[(N // 2) // 128, (K - 1) // 128])
     assert np.array_equal(s.cpu().numpy(), so)
-    assert np.array_equal(q.cpu().numpy(), qo)
+    assert codes_match(q.cpu().numpy(), qo)
 
 
 def test_graph_capture_replays_match_eager():

@@ -117,9 +117,32 @@ def test_token_group_is_reference_per_row(oracle):
     assert not np.array_equal(q, qg)   # granularity matters
 
 
+def test_act_quant_skips_nan(oracle):
+    # The reference's `if v > local: local = v` never takes a NaN
+    # (kernels.mojo:153-160): the amax is numpy's nanmax of |x|; quiet and
+    # signalling NaN of both signs, beside the group's largest value.
+    from oracle import oracle as O
+    x = O.gen_act_bf16(11, 2, 512).copy()
+    x[0, 5], x[0, 9] = 0x7FC0, 0x4400             # qNaN and 512 in group 0
+    x[0, 130], x[0, 131] = 0xFF81, 0xC3F0         # -sNaN and -480 in group 1
+    x[1, 300] = 0x7F81                            # +sNaN alone in group 2
+    q, s = oracle.quant_act(x, 128)
+    xf = oracle.bf16_to_f32(x).reshape(2, 4, 128)
+    want = (np.nanmax(np.abs(xf), axis=2) / np.float32(448)).astype(np.float32)
+    assert np.array_equal(s, want)
+    assert s[0, 0] == np.float32(512) / np.float32(448)
+    assert s[0, 1] == np.float32(480) / np.float32(448)
+    nan = np.isnan(oracle.bf16_to_f32(x))
+    assert np.all((q[nan] & 0x7F) == 0x7F) and not np.any((q[~nan] & 0x7F) == 0x7F)
+
+
 def test_weight_quant_matches_independent_numpy(oracle):
     from oracle import oracle as O
     w = O.gen_normal(3, 300 * 384, 0.0, 0.02).reshape(300, 384)
+    # numpy's max propagates NaN, so a block holding one takes s = 1
+    # (scripts/stage_tiny_fp8_from_bf16.py:65-68); an infinity gives s = inf
+    w[5, 7] = np.nan
+    w[140, 300] = np.inf
     for bn, bk in ((128, 128), (1, 384)):
         q, s = oracle.quant_weight(w, bn, bk)
         nb, kb = -(-300 // bn), -(-384 // bk)
@@ -131,5 +154,9 @@ def test_weight_quant_matches_independent_numpy(oracle):
                 sc = amax / np.float32(448) if amax > 0 else np.float32(1)
                 assert s[i, j] == sc
                 ref = torch.from_numpy((blk / sc).astype(np.float32)).to(torch.float8_e4m3fn)
-                assert np.array_equal(q[i * bn:(i + 1) * bn, j * bk:(j + 1) * bk],
-                                      ref.view(torch.uint8).numpy())
+                got = q[i * bn:(i + 1) * bn, j * bk:(j + 1) * bk]
+                ref = ref.view(torch.uint8).numpy()
+                nan = (ref & 0x7F) == 0x7F          # NaN codes: sign not compared
+                assert np.array_equal((got & 0x7F) == 0x7F, nan)
+                assert np.array_equal(got[~nan], ref[~nan])
+        assert s[5 // bn, 7 // bk] == 1.0 and np.isinf(s[140 // bn, 300 // bk])
