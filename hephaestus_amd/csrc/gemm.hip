@@ -211,8 +211,11 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8Operands op)
 }
 
 // ---------------------------------------------------------------------------
-// Large-M kernel: 256x256 tile per 512-thread workgroup (8 waves of 128x64,
-// 8x4 MFMA 16x16x128 each). Operand tiles reach LDS by direct DMA
+// Large-M kernel: BMx256 tile per 512-thread workgroup (8 waves of
+// (BM/2)x64, (BM/32)x4 MFMA 16x16x128 each). The weight fragment is the
+// MFMA's first operand, so lane l holds row l&15 of each 16x16 output block
+// at columns 4*(l>>4) .. +3: one activation-scale product per row tile and
+// chunk, and four consecutive outputs to pack. Operand tiles reach LDS by direct DMA
 // (global_load_lds_dwordx4, 1 KB = 8 rows per instruction, no VGPR
 // staging); a 16-byte piece p of row r lands in slot p ^ (r & 7), which
 // spreads the fragment reads over the banks. Two stages of
@@ -222,10 +225,10 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8Operands op)
 //   other buffer -> contract chunk j.
 // The compiler does not model the DMA's LDS writes, so the waits are
 // explicit s_waitcnt vmcnt(0) plus compiler memory barriers.
-// Epilogue: accumulators staged through LDS in f32, 128 rows at a time, then
-// written as coalesced 16-byte rows (residual added before the one rounding):
-// full 128-byte lines per store, which measured far cheaper than storing
-// the MFMA layout from registers.
+// Epilogue, bf16 output: the tile is rounded (v_cvt_pk_bf16_f32), written to
+// LDS once as bf16 (8 bytes per lane and block) and stored as coalesced
+// 16-byte row pieces. f32 output or a residual: staged in f32, BM/2 rows at
+// a time, the residual added before the one rounding.
 namespace {
 constexpr int L_BN = 256, L_WN = 64, L_NT = L_WN / 16;
 constexpr int L_STAGE_B = L_BN * kChunk;
@@ -258,6 +261,16 @@ __device__ __forceinline__ void wait_dma()
 }
 }  // namespace
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> two bf16 (round to nearest even) in one v_cvt_pk_bf16_f32;
+// equal bit for bit to f32_to_bf16 on non-NaN values (checked on the GPU
+// against the f32 output of the same kernel rounded on the host).
+__device__ __forceinline__ uint32_t pack_bf16_hw(float a, float b)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
 template <int SM, int BM>
 __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
 {
@@ -308,12 +321,16 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
             dma4(ssrc + j * op.s_step, st + L_STAGE_A + L_STAGE_B + wave * 256);
     };
 
-    float swc[L_NT];
+    // With the weight fragment as the MFMA's first operand, lane l holds
+    // row r16 of each 16x16 block and its columns 4*slice .. 4*slice+3.
+    float swc[L_NT][4];
 #pragma unroll
-    for (int ni = 0; ni < L_NT; ++ni) {
-        const int n = min(n0 + wn * L_WN + ni * 16 + r16, N - 1);
-        swc[ni] = SM == 1 ? op.sw[n] : 0.0f;
-    }
+    for (int ni = 0; ni < L_NT; ++ni)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int n = min(n0 + wn * L_WN + ni * 16 + slice * 4 + e, N - 1);
+            swc[ni][e] = SM == 1 ? op.sw[n] : 0.0f;
+        }
     // A wave whose columns all lie past N still reads a valid scale row
     // (its results are never stored).
     const int wblk = min((n0 + wn * L_WN) >> 7, (N - 1) >> 7);
@@ -359,14 +376,14 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
                 const i32x8 a = join(*reinterpret_cast<const i32x4*>(row + sl0),
                                      *reinterpret_cast<const i32x4*>(row + sl1));
 #pragma unroll
-                for (int ni = 0; ni < L_NT; ++ni) acc[mi][ni] = mfma_e4m3(a, b[ni], acc[mi][ni]);
+                for (int ni = 0; ni < L_NT; ++ni) acc[mi][ni] = mfma_e4m3(b[ni], a, acc[mi][ni]);
             }
         } else {
             // Software pipeline: the rescale FMAs of m-tile mi - 1 run while
             // the MFMAs of m-tile mi execute, so no FMA waits on the MFMA it
             // reads.
             f32x4 p[2][L_NT];
-            float sc[2][4];
+            float sc[2];
 #pragma unroll
             for (int mi = 0; mi <= L_MT; ++mi) {
                 const int cur = mi & 1, prv = cur ^ 1;
@@ -374,33 +391,69 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
                     const uint8_t* row = As + (wm * L_WM + mi * 16 + r16) * kChunk;
                     const i32x8 a = join(*reinterpret_cast<const i32x4*>(row + sl0),
                                          *reinterpret_cast<const i32x4*>(row + sl1));
-                    const f32x4 s4 =
-                        *reinterpret_cast<const f32x4*>(Ss + wm * L_WM + mi * 16 + slice * 4);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) sc[cur][i] = s4[i] * swj;
+                    sc[cur] = Ss[wm * L_WM + mi * 16 + r16] * swj;
 #pragma unroll
                     for (int ni = 0; ni < L_NT; ++ni)
-                        p[cur][ni] = mfma_e4m3(a, b[ni], f32x4{0, 0, 0, 0});
+                        p[cur][ni] = mfma_e4m3(b[ni], a, f32x4{0, 0, 0, 0});
                 }
                 if (mi > 0) {
 #pragma unroll
                     for (int ni = 0; ni < L_NT; ++ni)
 #pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            acc[mi - 1][ni][i] +=
-                                p[prv][ni][i] * (SM == 0 ? sc[prv][i] : sc[prv][i] * swc[ni]);
+                        for (int e = 0; e < 4; ++e)
+                            acc[mi - 1][ni][e] +=
+                                p[prv][ni][e] * (SM == 0 ? sc[prv] : sc[prv] * swc[ni][e]);
                 }
             }
         }
     }
 
-    // ---- epilogue: two passes of L_WM rows through LDS (f32) ----
-    // Rows are padded to 260 floats (4 banks of skew per row), so every
-    // lane's address is one base plus immediate offsets.
+    // ---- epilogue ----
+    // Lane l holds C[row r16][cols 4*slice .. +3] of each 16x16 block.
+    const int r_lane = wm * L_WM + r16;                  // tile row of (mi = 0)
+    const int c_lane = wn * L_WN + slice * 4;            // tile col of (ni = 0)
+    if (!op.residual && !op.c_f32) {
+        // bf16 output: the whole tile goes through LDS once as bf16, rows
+        // padded to 520 bytes (130 dwords: consecutive rows 2 banks apart),
+        // each lane writing 8 bytes per block; then 16-byte coalesced stores.
+        constexpr int RB = 520;
+        static_assert(L_BM * RB <= 2 * L_STAGE, "bf16 tile must fit the stage buffers");
+        __syncthreads();
+#pragma unroll
+        for (int mi = 0; mi < L_MT; ++mi) {
+            float sa = 1.0f;
+            if constexpr (SM == 2) sa = op.s[min(m0 + r_lane + mi * 16, M - 1)];
+#pragma unroll
+            for (int ni = 0; ni < L_NT; ++ni) {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[e] = acc[mi][ni][e];
+                    if constexpr (SM == 2)
+                        v[e] = (v[e] * sa) * op.sw[min(n0 + c_lane + ni * 16 + e, N - 1)];
+                }
+                const uint2 pk = make_uint2(pack_bf16_hw(v[0], v[1]), pack_bf16_hw(v[2], v[3]));
+                *reinterpret_cast<uint2*>(smem + (r_lane + mi * 16) * RB +
+                                          (c_lane + ni * 16) * 2) = pk;
+            }
+        }
+        __syncthreads();
+        for (int e = tid; e < L_BM * (L_BN / 8); e += 512) {
+            const int r = e / (L_BN / 8);
+            const int c8 = (e % (L_BN / 8)) * 8;
+            const int grow = m0 + r, gcol = n0 + c8;
+            if (grow >= M || gcol >= N) continue;
+            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(op.c) + (size_t)grow * N + gcol) =
+                *reinterpret_cast<const uint4*>(smem + r * RB + c8 * 2);
+        }
+        return;
+    }
+    // f32 output or residual: two passes of L_WM rows through LDS in f32
+    // (the residual is added before the one rounding).
     constexpr int CST = L_BN + 4;
     static_assert(L_WM * CST * 4 <= 2 * L_STAGE, "epilogue tile must fit the stage buffers");
     float* Cs = reinterpret_cast<float*>(smem);
-    float* cw = Cs + (slice * 4) * CST + wn * L_WN + r16;
+    float* cw = Cs + r16 * CST + c_lane;
     for (int pass = 0; pass < 2; ++pass) {
         __syncthreads();
         if (wm == pass) {
@@ -408,9 +461,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
             for (int mi = 0; mi < L_MT; ++mi)
 #pragma unroll
                 for (int ni = 0; ni < L_NT; ++ni)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        cw[(mi * 16 + i) * CST + ni * 16] = acc[mi][ni][i];
+                    *reinterpret_cast<f32x4*>(cw + mi * 16 * CST + ni * 16) = acc[mi][ni];
         }
         __syncthreads();
         // L_WM rows x 256 cols: each thread writes 8 consecutive outputs
@@ -442,13 +493,11 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
                 *reinterpret_cast<float4*>(c + 4) = make_float4(v[4], v[5], v[6], v[7]);
             } else {
                 uint16_t* c = static_cast<uint16_t*>(op.c) + o;
-                if (op.residual) {
-                    const uint4 rr = *reinterpret_cast<const uint4*>(c);
-                    v[0] += bf16lo(rr.x); v[1] += bf16hi(rr.x);
-                    v[2] += bf16lo(rr.y); v[3] += bf16hi(rr.y);
-                    v[4] += bf16lo(rr.z); v[5] += bf16hi(rr.z);
-                    v[6] += bf16lo(rr.w); v[7] += bf16hi(rr.w);
-                }
+                const uint4 rr = *reinterpret_cast<const uint4*>(c);
+                v[0] += bf16lo(rr.x); v[1] += bf16hi(rr.x);
+                v[2] += bf16lo(rr.y); v[3] += bf16hi(rr.y);
+                v[4] += bf16lo(rr.z); v[5] += bf16hi(rr.z);
+                v[6] += bf16lo(rr.w); v[7] += bf16hi(rr.w);
                 uint4 out;
                 out.x = f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
                 out.y = f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);

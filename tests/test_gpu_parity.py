@@ -642,6 +642,41 @@ def test_large_m_gemm_modes(mode, out, resid, tile_m):
     assert np.array_equal(q_ws.cpu().numpy().reshape(M, K), qo)
 
 
+@pytest.mark.parametrize("mode", ["block", "channel_token", "channel_g128"])
+def test_large_m_bf16_is_rounded_f32(mode, tile_m):
+    # The bf16 epilogue rounds with v_cvt_pk_bf16_f32; the f32 epilogue
+    # stores the same sums unrounded. The bf16 output must be the f32
+    # output rounded to nearest even on the host, bit for bit, on ragged M
+    # and N, in every scale mode.
+    M, N, K = 1300, 400, 1024
+    x = O.gen_act_bf16(63, M, K, outlier_p=1e-3)
+    if mode == "block":
+        qw, sw = O.gen_weight(64, N, K)
+        g = 128
+    else:
+        qw, sw = O.quant_weight(O.gen_normal(64, N * K, 0.0, 0.02).reshape(N, K), 1, K)
+        g = K if mode == "channel_token" else 128
+    f, _, _ = run_linear(qw, sw, x, M=M, N=N, K=K, group_k=g, out=torch.float32)
+    b, _, _ = run_linear(qw, sw, x, M=M, N=N, K=K, group_k=g)
+    assert HK.last_kernel() == f"fp8_gemm_{tile_m}x256"
+    assert np.array_equal(host_bf16(b), bf16_of(f.cpu().numpy()))
+
+
+def test_large_m_bf16_rounding_ties():
+    # At config-3 size about 2^-16 of the f32 sums sit exactly on a bf16
+    # rounding tie (low 16 bits 0x8000): the hardware conversion must round
+    # them to even as the host does.
+    M, N, K = 4096, 2560, 2560
+    x = O.gen_act_bf16(65, M, K, outlier_p=1e-3)
+    qw, sw = O.gen_weight(66, N, K)
+    f, _, _ = run_linear(qw, sw, x, M=M, N=N, K=K, out=torch.float32)
+    b, _, _ = run_linear(qw, sw, x, M=M, N=N, K=K)
+    fh = f.cpu().numpy()
+    ties = np.count_nonzero((fh.view(np.uint32) & 0xFFFF) == 0x8000)
+    assert ties > 20, ties
+    assert np.array_equal(host_bf16(b), bf16_of(fh))
+
+
 @pytest.mark.parametrize("M", [1024, 1100])
 def test_large_m_exact_integer(M, tile_m):
     N, K = 272, 2560
