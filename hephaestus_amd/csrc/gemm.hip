@@ -384,14 +384,28 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
             // reads.
             f32x4 p[2][L_NT];
             float sc[2];
+            // A fragment and row scale of m-tile mi + 1 are read from LDS
+            // while the MFMAs of m-tile mi execute.
+            i32x4 alo[2], ahi[2];
+            float sa_[2];
+            {
+                const uint8_t* row = As + (wm * L_WM + r16) * kChunk;
+                alo[0] = *reinterpret_cast<const i32x4*>(row + sl0);
+                ahi[0] = *reinterpret_cast<const i32x4*>(row + sl1);
+                sa_[0] = Ss[wm * L_WM + r16];
+            }
 #pragma unroll
             for (int mi = 0; mi <= L_MT; ++mi) {
                 const int cur = mi & 1, prv = cur ^ 1;
+                if (mi + 1 < L_MT) {
+                    const uint8_t* row = As + (wm * L_WM + (mi + 1) * 16 + r16) * kChunk;
+                    alo[prv] = *reinterpret_cast<const i32x4*>(row + sl0);
+                    ahi[prv] = *reinterpret_cast<const i32x4*>(row + sl1);
+                    sa_[prv] = Ss[wm * L_WM + (mi + 1) * 16 + r16];
+                }
                 if (mi < L_MT) {
-                    const uint8_t* row = As + (wm * L_WM + mi * 16 + r16) * kChunk;
-                    const i32x8 a = join(*reinterpret_cast<const i32x4*>(row + sl0),
-                                         *reinterpret_cast<const i32x4*>(row + sl1));
-                    sc[cur] = Ss[wm * L_WM + mi * 16 + r16] * swj;
+                    const i32x8 a = join(alo[cur], ahi[cur]);
+                    sc[cur] = sa_[cur] * swj;
 #pragma unroll
                     for (int ni = 0; ni < L_NT; ++ni)
                         p[cur][ni] = mfma_e4m3(b[ni], a, f32x4{0, 0, 0, 0});
