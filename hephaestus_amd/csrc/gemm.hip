@@ -21,6 +21,7 @@
 //     a grouped (8 tile-rows) order, so A and B tiles are reused from that
 //     XCD's L2.
 #include <atomic>
+#include <type_traits>
 
 #include "heph_kernels.h"
 
@@ -215,14 +216,20 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8Operands op)
 // (BM/2)x64, (BM/32)x4 MFMA 16x16x128 each). The weight fragment is the
 // MFMA's first operand, so lane l holds row l&15 of each 16x16 output block
 // at columns 4*(l>>4) .. +3: one activation-scale product per row tile and
-// chunk, and four consecutive outputs to pack. Operand tiles reach LDS by direct DMA
-// (global_load_lds_dwordx4, 1 KB = 8 rows per instruction, no VGPR
-// staging); a 16-byte piece p of row r lands in slot p ^ (r & 7), which
-// spreads the fragment reads over the banks. Two stages of
-// A 32 KB + B 32 KB + row scales 1 KB; one barrier per 128-wide chunk:
+// chunk, and four consecutive outputs to pack. Operand tiles reach LDS by
+// direct DMA (buffer_load_dwordx4 ... lds, 1 KB = 8 rows per instruction,
+// no VGPR staging); a 16-byte piece p of row r lands in slot p ^ (r & 7),
+// which spreads the fragment reads over the banks. Two stages of
+// A BM*128 B + B 32 KB + row scales BM*4 B; one barrier per 128-wide chunk:
 //   wait own DMA of chunk j -> barrier (chunk j visible everywhere, and
 //   every wave is done with the other buffer) -> DMA chunk j+1 into the
 //   other buffer -> contract chunk j.
+// The chunk loop is unrolled by two so that each stage's LDS addresses are
+// fixed registers plus instruction offsets, and the DMA advances through K
+// with a scalar offset only: apart from the rescale (one FMA per
+// accumulator and chunk, one multiply per row tile) the loop holds almost
+// no VALU work, because a wave's VALU instructions do not overlap its own
+// MFMAs. The block scales come through the scalar cache.
 // The compiler does not model the DMA's LDS writes, so the waits are
 // explicit s_waitcnt vmcnt(0) plus compiler memory barriers.
 // Epilogue, bf16 output: the tile is rounded (v_cvt_pk_bf16_f32), written to
@@ -245,13 +252,28 @@ struct BigTile {
     static constexpr int STAGE = STAGE_A + L_STAGE_B + STAGE_S;
 };
 
-__device__ __forceinline__ void dma16(const void* g, void* lds)
+template <int V>
+using ic = std::integral_constant<int, V>;
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Raw buffer resource over [p, p + 2^31): offsets are byte offsets from p.
+// Word 3 = 0x00020000 (32-bit data format, as gfx9 raw buffers need).
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p)
 {
-    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, 0x7fffffff, 0x00020000);
 }
-__device__ __forceinline__ void dma4(const void* g, void* lds)
+// 16 (4) bytes per lane from base + voff + soff straight into LDS at
+// lds + 16 * lane (4 * lane); lds must be uniform.
+__device__ __forceinline__ void dma16(rsrc_t r, uint32_t voff, uint32_t soff, void* lds)
 {
-    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
+                                             voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma4(rsrc_t r, uint32_t voff, uint32_t soff, void* lds)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4,
+                                             voff, soff, 0, 0);
 }
 __device__ __forceinline__ void wait_dma()
 {
@@ -259,6 +281,12 @@ __device__ __forceinline__ void wait_dma()
     __builtin_amdgcn_s_waitcnt(0x0F70);
     asm volatile("" ::: "memory");
 }
+// Keeps v where the program computes it: the scheduler may not sink the
+// rescale FMAs below the next row tile's MFMAs (their partials would then
+// all be live at once).
+__device__ __forceinline__ void pin(f32x4& v) { asm volatile("" : "+v"(v)); }
+
+typedef const __attribute__((address_space(4))) float* const_f32_ptr;
 }  // namespace
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -293,8 +321,10 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     // DMA sources: wave w moves operand rows [32w, 32w+32) of A and of B
     // (4 instructions each); lane i covers row 8q + (i >> 3) of block q and
     // global piece (i & 7) ^ (row & 7). Rows past M (N) are clamped to the
-    // last row: they feed output rows (columns) that are never stored. One
-    // 32-bit offset per block and operand is kept, not a pointer.
+    // last row: they feed output rows (columns) that are never stored. Each
+    // lane keeps one 32-bit byte offset per block and operand; chunk j adds
+    // the scalar offset 128 * j.
+    const rsrc_t rq = make_rsrc(op.q), rw = make_rsrc(op.w), rs = make_rsrc(op.s);
     const int lr = lane >> 3;
     const int piece = ((lane & 7) ^ lr) * 16;     // rows 8q + lr share r & 7 = lr
     uint32_t aoff[4], boff[4];
@@ -304,21 +334,23 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
         aoff[q] = (uint32_t)min(m0 + r, M - 1) * (uint32_t)K + piece;
         boff[q] = (uint32_t)min(n0 + r, N - 1) * (uint32_t)K + piece;
     }
-    const float* ssrc = op.s + (size_t)min(m0 + wave * 64 + lane, M - 1) * op.s_ld;
+    const uint32_t soff = (uint32_t)min(m0 + wave * 64 + lane, M - 1) * (uint32_t)op.s_ld * 4u;
+    const uint32_t s_step = (uint32_t)op.s_step * 4u;
 
-    auto issue = [&](int j, int buf) {
+    // DMA instruction `part` (0..8) of this wave for chunk j into stage
+    // buf: parts 0-3 move A rows, 4-7 B rows, 8 the row scales.
+    constexpr int kParts = 9;
+    auto issue_part = [&](int j, auto bufc, int part) {
+        constexpr int buf = decltype(bufc)::value;
         uint8_t* st = smem + buf * L_STAGE;
-        const uint8_t* qa = op.q + (size_t)j * kChunk;
-        const uint8_t* wb = op.w + (size_t)j * kChunk;
-        if (wave * 32 < L_BM) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) dma16(qa + aoff[q], st + (wave * 32 + q * 8) * kChunk);
+        const uint32_t ko = (uint32_t)j * kChunk;
+        if (part < 4) {
+            if (wave * 32 < L_BM) dma16(rq, aoff[part], ko, st + (wave * 32 + part * 8) * kChunk);
+        } else if (part < 8) {
+            dma16(rw, boff[part - 4], ko, st + L_STAGE_A + (wave * 32 + (part - 4) * 8) * kChunk);
+        } else if (SM != 2 && wave * 64 < L_BM) {
+            dma4(rs, soff, (uint32_t)j * s_step, st + L_STAGE_A + L_STAGE_B + wave * 256);
         }
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            dma16(wb + boff[q], st + L_STAGE_A + (wave * 32 + q * 8) * kChunk);
-        if (SM != 2 && wave * 64 < L_BM)
-            dma4(ssrc + j * op.s_step, st + L_STAGE_A + L_STAGE_B + wave * 256);
     };
 
     // With the weight fragment as the MFMA's first operand, lane l holds
@@ -332,9 +364,17 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
             swc[ni][e] = SM == 1 ? op.sw[n] : 0.0f;
         }
     // A wave whose columns all lie past N still reads a valid scale row
-    // (its results are never stored).
+    // (its results are never stored). The row is uniform per wave: the
+    // block scales are scalar loads.
     const int wblk = min((n0 + wn * L_WN) >> 7, (N - 1) >> 7);
-    const float* swb = op.sw + (size_t)wblk * op.sw_ld;
+    const const_f32_ptr swb = (const_f32_ptr)(op.sw + (size_t)wblk * op.sw_ld);
+
+    // Per-lane LDS byte offsets inside a stage: fragment rows of A and B at
+    // the two 16-byte slots this lane reads, and the row scale.
+    const int sl0 = (slice ^ (r16 & 7)) * 16, sl1 = sl0 ^ 64;
+    const int a_row = (wm * L_WM + r16) * kChunk;
+    const int b_row = L_STAGE_A + (wn * L_WN + r16) * kChunk;
+    const int s_row = L_STAGE_A + L_STAGE_B + (wm * L_WM + r16) * 4;
 
     f32x4 acc[L_MT][L_NT];
 #pragma unroll
@@ -342,85 +382,89 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
 #pragma unroll
         for (int ni = 0; ni < L_NT; ++ni) acc[mi][ni] = f32x4{0, 0, 0, 0};
 
-    issue(0, 0);
-    // The block scale of chunk j + 1 is fetched with chunk j + 1's DMA, so
-    // the wait at the top of the next iteration covers it too.
     float sw_cur = SM == 0 ? swb[0] : 1.0f, sw_nxt = 1.0f;
-    for (int j = 0; j < KC; ++j) {
-        const int buf = j & 1;
-        wait_dma();
-        __syncthreads();
-        if (j + 1 < KC) {
-            issue(j + 1, buf ^ 1);
-            if constexpr (SM == 0) sw_nxt = swb[j + 1];
-        }
 
-        const uint8_t* As = smem + buf * L_STAGE;
-        const uint8_t* Bs = As + L_STAGE_A;
-        const float* Ss = reinterpret_cast<const float*>(As + L_STAGE_A + L_STAGE_B);
-        const int sl0 = (slice ^ (r16 & 7)) * 16, sl1 = ((slice + 4) ^ (r16 & 7)) * 16;
-
-        i32x8 b[L_NT];
+    // Software pipeline over the row tiles of a wave: the MFMAs of tile mi
+    // run while the rescale FMAs of tile mi - 1 execute and the A fragment
+    // and row scale of tile mi + 1 are read. The last tile's FMAs are done
+    // at the start of the next chunk, so its partials and scale product
+    // live across the barrier.
+    static_assert(L_MT % 2 == 0, "row tiles per wave must be even");
+    f32x4 p[2][L_NT];
+    float sc[2] = {0.0f, 0.0f};
+    auto rescale = [&](int mi, int slot) {
 #pragma unroll
         for (int ni = 0; ni < L_NT; ++ni) {
-            const uint8_t* row = Bs + (wn * L_WN + ni * 16 + r16) * kChunk;
-            b[ni] = join(*reinterpret_cast<const i32x4*>(row + sl0),
-                         *reinterpret_cast<const i32x4*>(row + sl1));
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                acc[mi][ni][e] += p[slot][ni][e] * (SM == 0 ? sc[slot] : sc[slot] * swc[ni][e]);
+            pin(acc[mi][ni]);
         }
+    };
+
+    // One 128-wide chunk j held in stage buf (a compile-time constant). The
+    // wave's nine DMA instructions for chunk j + 1 are spread over the row
+    // tiles: issued together right after the barrier, the DMAs of all eight
+    // waves stall every wave's instruction issue.
+    auto chunk = [&](auto bufc, int j) {
+        constexpr int buf = decltype(bufc)::value;
+        wait_dma();
+        __syncthreads();
+        const bool more = j + 1 < KC;
+        if constexpr (SM == 0) {
+            if (more) sw_nxt = swb[j + 1];
+        }
+        const uint8_t* st = smem + buf * L_STAGE;
+        auto frag = [&](int row_off) {
+            return join(*reinterpret_cast<const i32x4*>(st + row_off + sl0),
+                        *reinterpret_cast<const i32x4*>(st + row_off + sl1));
+        };
+        i32x8 b[L_NT];
+#pragma unroll
+        for (int ni = 0; ni < L_NT; ++ni) b[ni] = frag(b_row + ni * 16 * kChunk);
         const float swj = sw_cur;
         sw_cur = sw_nxt;
-        if constexpr (SM == 2) {
+        i32x8 a_[2];
+        float sa_[2];
+        a_[0] = frag(a_row);
+        sa_[0] = *reinterpret_cast<const float*>(st + s_row);
 #pragma unroll
-            for (int mi = 0; mi < L_MT; ++mi) {
-                const uint8_t* row = As + (wm * L_WM + mi * 16 + r16) * kChunk;
-                const i32x8 a = join(*reinterpret_cast<const i32x4*>(row + sl0),
-                                     *reinterpret_cast<const i32x4*>(row + sl1));
-#pragma unroll
-                for (int ni = 0; ni < L_NT; ++ni) acc[mi][ni] = mfma_e4m3(b[ni], a, acc[mi][ni]);
+        for (int mi = 0; mi < L_MT; ++mi) {
+            const int cur = mi & 1, prv = cur ^ 1;
+            if (mi + 1 < L_MT) {
+                a_[prv] = frag(a_row + (mi + 1) * 16 * kChunk);
+                sa_[prv] = *reinterpret_cast<const float*>(st + s_row + (mi + 1) * 64);
             }
-        } else {
-            // Software pipeline: the rescale FMAs of m-tile mi - 1 run while
-            // the MFMAs of m-tile mi execute, so no FMA waits on the MFMA it
-            // reads.
-            f32x4 p[2][L_NT];
-            float sc[2];
-            // A fragment and row scale of m-tile mi + 1 are read from LDS
-            // while the MFMAs of m-tile mi execute.
-            i32x4 alo[2], ahi[2];
-            float sa_[2];
-            {
-                const uint8_t* row = As + (wm * L_WM + r16) * kChunk;
-                alo[0] = *reinterpret_cast<const i32x4*>(row + sl0);
-                ahi[0] = *reinterpret_cast<const i32x4*>(row + sl1);
-                sa_[0] = Ss[wm * L_WM + r16];
+            if (more) {
+#pragma unroll
+                for (int part = 0; part < kParts; ++part)
+                    if (part * L_MT / kParts == mi) issue_part(j + 1, ic<buf ^ 1>{}, part);
             }
+            if constexpr (SM == 2) {
 #pragma unroll
-            for (int mi = 0; mi <= L_MT; ++mi) {
-                const int cur = mi & 1, prv = cur ^ 1;
-                if (mi + 1 < L_MT) {
-                    const uint8_t* row = As + (wm * L_WM + (mi + 1) * 16 + r16) * kChunk;
-                    alo[prv] = *reinterpret_cast<const i32x4*>(row + sl0);
-                    ahi[prv] = *reinterpret_cast<const i32x4*>(row + sl1);
-                    sa_[prv] = Ss[wm * L_WM + (mi + 1) * 16 + r16];
-                }
-                if (mi < L_MT) {
-                    const i32x8 a = join(alo[cur], ahi[cur]);
-                    sc[cur] = sa_[cur] * swj;
+                for (int ni = 0; ni < L_NT; ++ni)
+                    acc[mi][ni] = mfma_e4m3(b[ni], a_[cur], acc[mi][ni]);
+            } else {
+                sc[cur] = sa_[cur] * swj;
 #pragma unroll
-                    for (int ni = 0; ni < L_NT; ++ni)
-                        p[cur][ni] = mfma_e4m3(b[ni], a, f32x4{0, 0, 0, 0});
-                }
-                if (mi > 0) {
-#pragma unroll
-                    for (int ni = 0; ni < L_NT; ++ni)
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            acc[mi - 1][ni][e] +=
-                                p[prv][ni][e] * (SM == 0 ? sc[prv] : sc[prv] * swc[ni][e]);
-                }
+                for (int ni = 0; ni < L_NT; ++ni)
+                    p[cur][ni] = mfma_e4m3(b[ni], a_[cur], f32x4{0, 0, 0, 0});
+                if (mi > 0) rescale(mi - 1, prv);
+                else if (j > 0) rescale(L_MT - 1, prv);
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
+    };
+
+#pragma unroll
+    for (int part = 0; part < kParts; ++part) issue_part(0, ic<0>{}, part);
+    int j = 0;
+    for (; j + 1 < KC; j += 2) {
+        chunk(ic<0>{}, j);
+        chunk(ic<1>{}, j + 1);
     }
+    if (j < KC) chunk(ic<0>{}, j);
+    if constexpr (SM != 2) rescale(L_MT - 1, (L_MT - 1) & 1);
 
     // ---- epilogue ----
     // Lane l holds C[row r16][cols 4*slice .. +3] of each 16x16 block.
@@ -555,23 +599,26 @@ hipError_t launch_big(const Fp8Operands& op, hipStream_t stream, const LaunchTim
 
 }  // namespace
 
-// Tile height of the large-M kernel: the one whose tile count fills the
-// CUs best (one 512-thread workgroup per CU; fraction of the last round's
-// slots used), the taller tile on a tie.
+// Tile height of the large-M kernel: the one with the least estimated time,
+// rounds of tiles over the CUs (one 512-thread workgroup per CU) times the
+// measured cost of one 128-wide chunk at that height (MI355X shader cycles
+// per chunk at M = 4096: 2990 for 256 rows, 2480 for 192, 2240 for 128 --
+// a taller tile does more MFMA work per chunk, a shorter one fills the CUs
+// in finer steps). The taller tile wins a tie.
 int gemm_tile_m(int M, int N)
 {
     const int forced = g_tune_bm.load(std::memory_order_relaxed);
     if (forced) return forced;
-    const int cus = cu_count();
+    const long cus = cu_count();
+    struct { int bm; long cycles; } const tiles_cost[] = {{256, 2990}, {192, 2480}, {128, 2240}};
     int best = 256;
-    double best_fill = -1.0;
-    for (int bm : {256, 192, 128}) {
-        const long tiles = (long)((M + bm - 1) / bm) * ((N + L_BN - 1) / L_BN);
-        const long rounds = (tiles + cus - 1) / cus;
-        const double fill = (double)tiles / (double)(rounds * cus);
-        if (fill > best_fill + 0.01) {
-            best_fill = fill;
-            best = bm;
+    long best_t = -1;
+    for (const auto& tc : tiles_cost) {
+        const long tiles = (long)((M + tc.bm - 1) / tc.bm) * ((N + L_BN - 1) / L_BN);
+        const long t = (tiles + cus - 1) / cus * tc.cycles;
+        if (best_t < 0 || t < best_t) {
+            best_t = t;
+            best = tc.bm;
         }
     }
     return best;

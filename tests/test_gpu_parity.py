@@ -691,12 +691,37 @@ def test_large_m_exact_integer(M, tile_m):
     assert np.array_equal(host_bf16(c), bf16_of(ref.astype(np.float32)))
 
 
+@pytest.mark.parametrize("K", [128, 384, 1152])
+def test_large_m_odd_chunk_counts(K, tile_m):
+    # The large-M kernel walks K two 128-wide chunks at a time (one per LDS
+    # stage) and finishes an odd count with a single chunk; K = 128 is one
+    # chunk and no loop. Ragged M and N, random data against the oracle, and
+    # exact-integer lattices bit for bit.
+    M, N = 1100, 400
+    x = O.gen_act_bf16(80 + K, M, K, outlier_p=1e-3)
+    qw, sw = O.gen_weight(81 + K, N, K)
+    c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K)
+    assert HK.last_kernel() == f"fp8_gemm_{tile_m}x256"
+    ref = O.quant_linear(x, qw, sw)
+    assert max_abs_rel(f32_of_bf16(host_bf16(c)), ref) <= TOL
+    ia, qa = lattice(M, K, 5000 + K)
+    iw, qwl = lattice(N, K, 6000 + K)
+    sa = np.full(M * (K // 128), 2.0 ** -3, np.float32)
+    swl = np.full((-(-N // 128), K // 128), 2.0 ** -2, np.float32)
+    exact = (ia.astype(np.float64) @ iw.astype(np.float64).T) * 0.0625 * 2.0 ** -5
+    c, _, _ = run_linear(qwl, swl, None, M=M, N=N, K=K, skip_quant=True,
+                         q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
+    assert HK.last_kernel() == f"fp8_gemm_{tile_m}x256"
+    assert np.array_equal(host_bf16(c), bf16_of(exact.astype(np.float32)))
+
+
 def test_large_m_tile_choice_fills_the_cus():
-    # At M = 4096 the automatic tile height is the one whose tile count
-    # best fills 256 CUs: 128 for N = 6144 (768 tiles), 192 for N = 2560
-    # (220 tiles), 256 for N = 19456 (1216 tiles).
+    # At M = 4096 the automatic tile height minimises rounds of tiles over
+    # 256 CUs times the per-chunk cost of the height: 256 for N = 6144
+    # (384 tiles, 2 rounds), 192 for N = 2560 (220 tiles, 1 round), 256 for
+    # N = 19456 (1216 tiles, 5 rounds).
     x = O.gen_act_bf16(70, 4096, 256)
-    for N, want in ((6144, 128), (2560, 192), (19456, 256)):
+    for N, want in ((6144, 256), (2560, 192), (19456, 256)):
         if torch.cuda.get_device_properties(0).multi_processor_count != 256:
             pytest.skip("expectations are for a 256-CU MI355X")
         qw, sw = O.gen_weight(71, N, 256)
