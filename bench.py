@@ -150,7 +150,7 @@ class Linear:
         copies = max(1, math.ceil(ROTATE_BYTES / (N * K))) if rotate else 1
         self.w = [q] + [q.clone() for _ in range(copies - 1)]
         self.s = [s] + [s.clone() for _ in range(copies - 1)]
-        self.q_ws, self.s_ws = HK.workspace(M_max, K)
+        self.q_ws, self.s_ws = HK.workspace(M_max, K, n=N)
         self.i = 0
 
     def next(self):
@@ -363,7 +363,7 @@ def detail_sweeps(lins):
         for lin in lins:
             xm = act(M, lin.K, seed=M + 1, outliers=True)
             cm = torch.empty(M, lin.N, dtype=torch.bfloat16, device="cuda")
-            q_ws, s_ws = HK.workspace(M, lin.K)
+            q_ws, s_ws = HK.workspace(M, lin.K, n=lin.N)
             w, s = lin.w[0], lin.s[0]
 
             def run_p(lin=lin, xm=xm, cm=cm, M=M, q_ws=q_ws, s_ws=s_ws, w=w, s=s):

@@ -57,6 +57,7 @@ SIGNATURES = {
     "heph_bf16_linear": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _i, _vp]),
     "heph_fp8_q_ws_bytes": (_sz, [_i, _i]),
     "heph_fp8_s_ws_floats": (_sz, [_i, _i, _i]),
+    "heph_fp8_linear_ws_bytes": (_sz, [_i, _i, _i]),
     "heph_strerror": (ctypes.c_char_p, [_i]),
     "heph_abi_version": (_i, []),
     "heph_profile_next_launch": (_i, [_vp, _vp]),

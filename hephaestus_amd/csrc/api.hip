@@ -76,6 +76,14 @@ size_t heph_fp8_q_ws_bytes(int M, int K)
     return (size_t)M * (size_t)K;
 }
 
+size_t heph_fp8_linear_ws_bytes(int M, int N, int K)
+{
+    if (M < 1 || N < 1 || K < 1) return 0;
+    const size_t q = ((size_t)M * (size_t)K + 255) & ~(size_t)255;
+    if (check_device() != HEPH_OK) return q;
+    return q + gemm_split_bytes(M, N, K);
+}
+
 size_t heph_fp8_s_ws_floats(int M, int K, int group_k)
 {
     if (M < 1 || K < 1 || group_k < 1 || K % group_k) return 0;
@@ -152,6 +160,13 @@ int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
     op.M = M;
     op.N = N;
     op.K = K;
+    // The part of q_ws past the codes (from the next 256-byte boundary) is
+    // scratch for the large-M GEMM's split-K partials.
+    const size_t qb = ((size_t)M * (size_t)K + 255) & ~(size_t)255;
+    if (q_ws_bytes > qb) {
+        op.part = reinterpret_cast<float*>(q_ws + qb);
+        op.part_bytes = q_ws_bytes - qb;
+    }
 
     // M <= 32 takes the chunk-slot GEMV unless a kernel is forced; the
     // skinny kernel serves FORCE_SKINNY (cross-kernel checks) only.

@@ -20,6 +20,7 @@
 //   * the block -> tile order gives each XCD a contiguous run of tiles in
 //     a grouped (8 tile-rows) order, so A and B tiles are reused from that
 //     XCD's L2.
+#include <algorithm>
 #include <atomic>
 #include <type_traits>
 
@@ -314,8 +315,13 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     const int wm = wave >> 2, wn = wave & 3;
     const int M = op.M, N = op.N, K = op.K, KC = K >> 7;
     const int tiles_m = (M + L_BM - 1) / L_BM, tiles_n = (N + L_BN - 1) / L_BN;
+    // Split over K: workgroup b takes tile b % tiles and the chunks
+    // [split * KC / S, (split + 1) * KC / S) of split b / tiles.
+    const int S = op.splits, tiles = tiles_m * tiles_n;
+    const int split = blockIdx.x / tiles;
+    const int jb = split * KC / S, je = (split + 1) * KC / S;
     int tm, tn;
-    tile_of_block(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+    tile_of_block(blockIdx.x - split * tiles, tiles_m, tiles_n, &tm, &tn);
     const int m0 = tm * L_BM, n0 = tn * L_BN;
 
     // DMA sources: wave w moves operand rows [32w, 32w+32) of A and of B
@@ -382,7 +388,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
 #pragma unroll
         for (int ni = 0; ni < L_NT; ++ni) acc[mi][ni] = f32x4{0, 0, 0, 0};
 
-    float sw_cur = SM == 0 ? swb[0] : 1.0f, sw_nxt = 1.0f;
+    float sw_cur = SM == 0 ? swb[jb] : 1.0f, sw_nxt = 1.0f;
 
     // Software pipeline over the row tiles of a wave: the MFMAs of tile mi
     // run while the rescale FMAs of tile mi - 1 execute and the A fragment
@@ -410,7 +416,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
         constexpr int buf = decltype(bufc)::value;
         wait_dma();
         __syncthreads();
-        const bool more = j + 1 < KC;
+        const bool more = j + 1 < je;
         if constexpr (SM == 0) {
             if (more) sw_nxt = swb[j + 1];
         }
@@ -450,26 +456,44 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
                 for (int ni = 0; ni < L_NT; ++ni)
                     p[cur][ni] = mfma_e4m3(b[ni], a_[cur], f32x4{0, 0, 0, 0});
                 if (mi > 0) rescale(mi - 1, prv);
-                else if (j > 0) rescale(L_MT - 1, prv);
+                else if (j > jb) rescale(L_MT - 1, prv);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
 #pragma unroll
-    for (int part = 0; part < kParts; ++part) issue_part(0, ic<0>{}, part);
-    int j = 0;
-    for (; j + 1 < KC; j += 2) {
+    for (int part = 0; part < kParts; ++part) issue_part(jb, ic<0>{}, part);
+    int j = jb;
+    for (; j + 1 < je; j += 2) {
         chunk(ic<0>{}, j);
         chunk(ic<1>{}, j + 1);
     }
-    if (j < KC) chunk(ic<0>{}, j);
+    if (j < je) chunk(ic<0>{}, j);
     if constexpr (SM != 2) rescale(L_MT - 1, (L_MT - 1) & 1);
 
     // ---- epilogue ----
     // Lane l holds C[row r16][cols 4*slice .. +3] of each 16x16 block.
     const int r_lane = wm * L_WM + r16;                  // tile row of (mi = 0)
     const int c_lane = wn * L_WN + slice * 4;            // tile col of (ni = 0)
+    if constexpr (SM != 2) {
+        if (S > 1) {
+            // split over K: the fp32 partial tile goes to the scratch
+            // [split][M][N]; splitk_reduce_kernel finishes the output.
+            float* pp = op.part + (size_t)split * M * N;
+#pragma unroll
+            for (int mi = 0; mi < L_MT; ++mi) {
+                const int row = m0 + r_lane + mi * 16;
+                if (row >= M) continue;
+#pragma unroll
+                for (int ni = 0; ni < L_NT; ++ni) {
+                    const int col = n0 + c_lane + ni * 16;
+                    if (col < N) *reinterpret_cast<f32x4*>(pp + (size_t)row * N + col) = acc[mi][ni];
+                }
+            }
+            return;
+        }
+    }
     if (!op.residual && !op.c_f32) {
         // bf16 output: the whole tile goes through LDS once as bf16, rows
         // padded to 520 bytes (130 dwords: consecutive rows 2 banks apart),
@@ -533,7 +557,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
             const f32x4 hi = *reinterpret_cast<const f32x4*>(&Cs[r * CST + c8 + 4]);
             float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             if constexpr (SM == 2) {
-                // reference association (acc * sa) * sw (M >= 1024 here)
+                // reference association (acc * sa) * sw (M >= 128 here)
                 const float sa = op.s[grow];
 #pragma unroll
                 for (int t = 0; t < 8; ++t) v[t] = (v[t] * sa) * op.sw[gcol + t];
@@ -567,6 +591,34 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     }
 }
 
+// Sums the K-split partials of the large-M GEMM in split order, adds the
+// residual and stores bf16 or f32 (four outputs per thread; N % 16 == 0).
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(Fp8Operands op)
+{
+    const size_t mn = (size_t)op.M * op.N, n4 = mn / 4;
+    const f32x4* part = reinterpret_cast<const f32x4*>(op.part);
+    for (size_t i = blockIdx.x * (size_t)256 + threadIdx.x; i < n4;
+         i += (size_t)gridDim.x * 256) {
+        f32x4 v = part[i];
+        for (int s = 1; s < op.splits; ++s) v += part[(size_t)s * n4 + i];
+        if (op.c_f32) {
+            f32x4* c = static_cast<f32x4*>(op.c) + i;
+            if (op.residual) v += *c;
+            *c = v;
+        } else {
+            uint2* c = static_cast<uint2*>(op.c) + i;
+            if (op.residual) {
+                const uint2 r = *c;
+                v[0] += bf16lo(r.x);
+                v[1] += bf16hi(r.x);
+                v[2] += bf16lo(r.y);
+                v[3] += bf16hi(r.y);
+            }
+            *c = make_uint2(pack_bf16_hw(v[0], v[1]), pack_bf16_hw(v[2], v[3]));
+        }
+    }
+}
+
 namespace {
 
 std::atomic<int> g_tune_bm{0};
@@ -590,11 +642,27 @@ template <int BM>
 hipError_t launch_big(const Fp8Operands& op, hipStream_t stream, const LaunchTiming& t)
 {
     const int tiles = ((op.M + BM - 1) / BM) * ((op.N + L_BN - 1) / L_BN);
+    const dim3 grid(tiles * op.splits);
+    if (op.splits > 1) {
+        // the GEMM carries the start stamp, the reduction the stop stamp
+        hipError_t e;
+        if (op.w_block)
+            e = launch(fp8_gemm256_kernel<0, BM>, grid, dim3(512), 0, stream,
+                       LaunchTiming{t.start, nullptr}, op);
+        else
+            e = launch(fp8_gemm256_kernel<1, BM>, grid, dim3(512), 0, stream,
+                       LaunchTiming{t.start, nullptr}, op);
+        if (e != hipSuccess) return e;
+        const size_t n4 = (size_t)op.M * op.N / 4;
+        const int blocks = (int)std::min<size_t>((n4 + 255) / 256, 4096);
+        return launch(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream,
+                      LaunchTiming{nullptr, t.stop}, op);
+    }
     if (op.w_block)
-        return launch(fp8_gemm256_kernel<0, BM>, dim3(tiles), dim3(512), 0, stream, t, op);
+        return launch(fp8_gemm256_kernel<0, BM>, grid, dim3(512), 0, stream, t, op);
     if (op.s_step == 0)
-        return launch(fp8_gemm256_kernel<2, BM>, dim3(tiles), dim3(512), 0, stream, t, op);
-    return launch(fp8_gemm256_kernel<1, BM>, dim3(tiles), dim3(512), 0, stream, t, op);
+        return launch(fp8_gemm256_kernel<2, BM>, grid, dim3(512), 0, stream, t, op);
+    return launch(fp8_gemm256_kernel<1, BM>, grid, dim3(512), 0, stream, t, op);
 }
 
 }  // namespace
@@ -626,18 +694,72 @@ int gemm_tile_m(int M, int N)
 
 void gemm_tune(int bm) { g_tune_bm.store(bm, std::memory_order_relaxed); }
 
+// K splits of the large-M GEMM: the count with the least estimated time,
+// rounds of (tile, split) workgroups over the CUs times the chunks of a
+// split times the per-chunk cost of the tile height (MI355X: about 1.2 us
+// at 128 rows), plus, when split, the reduction: about 8 us of extra
+// launch and per-workgroup set-up, and the partials (M*N*4 bytes a split)
+// read back at about 5 TB/s. At most 8 splits of at least 4 chunks. So M =
+// 512 splits o_proj and down (N = 2560: 40 tiles) 6 ways and leaves qkv
+// and gate_up whole; M = 4096 never splits.
+int gemm_splits(int M, int N, int K)
+{
+    if (M < 128) return 1;
+    const int bm = gemm_tile_m(M, N);
+    const long tiles = (long)((M + bm - 1) / bm) * ((N + L_BN - 1) / L_BN);
+    const long cus = cu_count();
+    const int KC = K / kChunk;
+    const double chunk_us = (bm == 256 ? 2990.0 : bm == 192 ? 2480.0 : 2240.0) / 1900.0;
+    int best = 1;
+    double best_t = 0.0;
+    for (int s = 1; s <= 8; ++s) {
+        if (s > 1 && KC / s < 4) break;
+        const long rounds = (tiles * s + cus - 1) / cus;
+        double t = (double)rounds * ((KC + s - 1) / s) * chunk_us;
+        if (s > 1) t += 8.0 + (double)s * M * N * 4.0 / 5.0e6;
+        if (s == 1 || t < best_t) {
+            best_t = t;
+            best = s;
+        }
+    }
+    return best;
+}
+
+size_t gemm_split_bytes(int M, int N, int K)
+{
+    const int s = gemm_splits(M, N, K);
+    return s > 1 ? (size_t)s * M * N * 4 : 0;
+}
+
 hipError_t launch_fp8_gemm(const Fp8Operands& op, hipStream_t stream,
                            const LaunchTiming& t, const char** name)
 {
-    // Large M: the 256-column DMA kernel (N % 16 == 0 keeps every 8-wide
-    // output group inside the row; its 32-bit operand offsets need
-    // M*K and N*K below 2^31). Otherwise the 128x128 kernel.
+    // M >= 128: the 256-column DMA kernel (N % 16 == 0 keeps every 8-wide
+    // output group inside the row; its 32-bit operand offsets need M*K and
+    // N*K below 2^31). It is as fast as the 128x128 kernel below M = 128
+    // and faster from there on (MI355X, the configs[3] shapes: 1.3-2x at
+    // M = 128..512). Otherwise the 128x128 kernel.
     const bool small_offsets = (long)op.M * op.K < (1L << 31) && (long)op.N * op.K < (1L << 31);
-    if (op.M >= 1024 && small_offsets) {
-        switch (gemm_tile_m(op.M, op.N)) {
-        case 128: *name = "fp8_gemm_128x256"; return launch_big<128>(op, stream, t);
-        case 192: *name = "fp8_gemm_192x256"; return launch_big<192>(op, stream, t);
-        default: *name = "fp8_gemm_256x256"; return launch_big<256>(op, stream, t);
+    if (op.M >= 128 && small_offsets) {
+        // K splits when the caller's scratch holds their partials (block or
+        // per-channel weights with per-chunk activation scales).
+        Fp8Operands o = op;
+        o.splits = 1;
+        if (o.part && o.s_step != 0) {
+            const int s = gemm_splits(o.M, o.N, o.K);
+            if (s > 1 && o.part_bytes >= (size_t)s * o.M * o.N * 4) o.splits = s;
+        }
+        const bool sk = o.splits > 1;
+        switch (gemm_tile_m(o.M, o.N)) {
+        case 128:
+            *name = sk ? "fp8_gemm_128x256_splitk" : "fp8_gemm_128x256";
+            return launch_big<128>(o, stream, t);
+        case 192:
+            *name = sk ? "fp8_gemm_192x256_splitk" : "fp8_gemm_192x256";
+            return launch_big<192>(o, stream, t);
+        default:
+            *name = sk ? "fp8_gemm_256x256_splitk" : "fp8_gemm_256x256";
+            return launch_big<256>(o, stream, t);
         }
     }
     const int tiles = ((op.M + BM - 1) / BM) * ((op.N + BN - 1) / BN);

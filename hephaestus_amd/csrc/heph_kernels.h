@@ -51,6 +51,11 @@ struct Fp8Operands {
     bool c_f32;
     bool residual;
     int M, N, K;
+    // Large-M GEMM split over K: scratch for the fp32 partials (nullptr:
+    // none) and its size, and the number of splits the launch uses.
+    float* part = nullptr;
+    size_t part_bytes = 0;
+    int splits = 1;
 };
 
 hipError_t launch_quant(const uint16_t* x, uint8_t* q, float* scales, int M,
@@ -92,6 +97,10 @@ hipError_t launch_fp8_gemm(const Fp8Operands& op, hipStream_t stream,
 // override (0 = automatic).
 int gemm_tile_m(int M, int N);
 void gemm_tune(int bm);
+// K splits the large-M GEMM uses for M x N x K when scratch allows (1 =
+// none), and the scratch bytes that takes.
+int gemm_splits(int M, int N, int K);
+size_t gemm_split_bytes(int M, int N, int K);
 
 // bf16 x [M,K] @ w [N,K]^T, f32 accumulation, M <= 32.
 hipError_t launch_bf16_skinny(void* c, bool c_f32, bool residual, const uint16_t* x,

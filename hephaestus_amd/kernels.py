@@ -161,9 +161,13 @@ def linear(c, a, b, m, n, k, ctx=None, *, add_residual=False):
     _check(s, "linear")
 
 
-def workspace(m: int, k: int, device="cuda", group_k: int = 128):
-    """Allocate (a_fp8_ws, act_scale_ws) for up to m rows of width k."""
-    q = torch.empty(L.lib().heph_fp8_q_ws_bytes(m, k), dtype=torch.uint8, device=device)
+def workspace(m: int, k: int, device="cuda", group_k: int = 128, n: int | None = None):
+    """Allocate (a_fp8_ws, act_scale_ws) for up to m rows of width k. With
+    n, a_fp8_ws also holds the scratch the large-M GEMM splits K into for
+    an m x n output (heph_fp8_linear_ws_bytes)."""
+    qb = (L.lib().heph_fp8_linear_ws_bytes(m, n, k) if n is not None
+          else L.lib().heph_fp8_q_ws_bytes(m, k))
+    q = torch.empty(qb, dtype=torch.uint8, device=device)
     s = torch.empty(L.lib().heph_fp8_s_ws_floats(m, k, group_k), dtype=torch.float32,
                     device=device)
     return q, s

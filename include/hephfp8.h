@@ -124,6 +124,17 @@ int heph_bf16_linear(void* c, int c_dtype, const uint16_t* x_bf16,
 size_t heph_fp8_q_ws_bytes(int M, int K);
 size_t heph_fp8_s_ws_floats(int M, int K, int group_k);
 
+/*
+ * Optional larger q_ws for (M, N, K): the activation codes, rounded up to
+ * 256 bytes, plus scratch for the fp32 partials of the large-M GEMM when it
+ * splits K (M >= 128 and few output tiles, e.g. M = 512 with N = 2560).
+ * Passing a q_ws of this size (q_ws_bytes) lets heph_fp8_linear use the
+ * part past the codes as that scratch; with the minimal q_ws it does not
+ * split. No counterpart in the reference, whose workspaces are sized for
+ * the codes and scales only (forward.mojo:121-125).
+ */
+size_t heph_fp8_linear_ws_bytes(int M, int N, int K);
+
 /* Message for a status code (static storage). */
 const char* heph_strerror(int status);
 

@@ -617,7 +617,7 @@ def tile_m(request):
 @pytest.mark.parametrize("mode", ["block", "channel_token", "channel_g128"])
 @pytest.mark.parametrize("out,resid", [("bf16", False), ("bf16", True), ("f32", False), ("f32", True)])
 def test_large_m_gemm_modes(mode, out, resid, tile_m):
-    # M >= 1024 takes the 256-column kernel at every tile height; ragged M
+    # M >= 128 takes the 256-column kernel at every tile height; ragged M
     # and N, every scale mode, both output types, with and without the
     # fused residual.
     M, N, K = 1300, 400, 1024
@@ -713,6 +713,57 @@ def test_large_m_odd_chunk_counts(K, tile_m):
                          q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
     assert HK.last_kernel() == f"fp8_gemm_{tile_m}x256"
     assert np.array_equal(host_bf16(c), bf16_of(exact.astype(np.float32)))
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 2560, 4096), (256, 2560, 9728), (384, 1040, 4224)])
+@pytest.mark.parametrize("out,resid", [("bf16", False), ("bf16", True), ("f32", True)])
+def test_large_m_split_k(M, N, K, out, resid):
+    # With a q_ws of heph_fp8_linear_ws_bytes(M, N, K) bytes the large-M
+    # GEMM splits K over the CUs its few tiles leave idle; a second kernel
+    # sums the fp32 partials in split order. Random data against the oracle
+    # within the tolerance; the residual added before the one rounding; the
+    # codes in the workspace still bit-exact.
+    assert L.lib().heph_fp8_linear_ws_bytes(M, N, K) > M * K
+    x = O.gen_act_bf16(90 + M, M, K, outlier_p=1e-3)
+    qw, sw = O.gen_weight(91 + M, N, K)
+    dt = torch.bfloat16 if out == "bf16" else torch.float32
+    r = O.gen_normal(92 + M, M * N).reshape(M, N).astype(np.float32)
+    res_t = (dev(bf16_of(r)) if out == "bf16" else dev(r)) if resid else None
+    q_ws, s_ws = HK.workspace(M, K, n=N)
+    c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K, out=dt, residual=res_t, q_ws=q_ws, s_ws=s_ws)
+    assert HK.last_kernel().endswith("_splitk"), HK.last_kernel()
+    ref = O.quant_linear(x, qw, sw)
+    if resid:
+        ref = ref + (f32_of_bf16(bf16_of(r)) if out == "bf16" else r)
+    got = f32_of_bf16(host_bf16(c)) if out == "bf16" else c.cpu().numpy()
+    assert max_abs_rel(got, ref) <= TOL
+    qo, _ = O.quant_act(x, 128)
+    assert np.array_equal(q_ws[: M * K].cpu().numpy().reshape(M, K), qo)
+
+
+def test_large_m_split_k_exact_and_repeatable():
+    # Split and unsplit runs of the same exact-integer problem give the same
+    # bits (every partial sum is exact), and two split runs are identical.
+    M, N, K = 512, 2560, 4096
+    ia, qa = lattice(M, K, 7000)
+    iw, qw = lattice(N, K, 7001)
+    sa = np.full(M * (K // 128), 2.0 ** -3, np.float32)
+    sw = np.full((-(-N // 128), K // 128), 2.0 ** -2, np.float32)
+    exact = (ia.astype(np.float64) @ iw.astype(np.float64).T) * 0.0625 * 2.0 ** -5
+    q_big, s_big = HK.workspace(M, K, n=N)
+    q_big[: M * K].copy_(dev(qa.reshape(-1)))
+    s_big.copy_(dev(sa))
+    outs = []
+    for _ in range(2):
+        c, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, skip_quant=True, q_ws=q_big, s_ws=s_big)
+        assert HK.last_kernel().endswith("_splitk")
+        outs.append(host_bf16(c))
+    c1, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, skip_quant=True,
+                          q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
+    assert not HK.last_kernel().endswith("_splitk")
+    assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(outs[0], host_bf16(c1))
+    assert np.array_equal(outs[0], bf16_of(exact.astype(np.float32)))
 
 
 def test_large_m_tile_choice_fills_the_cus():
