@@ -169,9 +169,15 @@ int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
     }
 
     // M <= 32 takes the chunk-slot GEMV unless a kernel is forced; the
-    // skinny kernel serves FORCE_SKINNY (cross-kernel checks) only.
+    // skinny kernel serves FORCE_SKINNY (cross-kernel checks) only. At
+    // 16 < M <= 32 (two 16-row tiles in the GEMV) quantizer + K-split GEMM
+    // is faster on large weights when the caller's scratch allows the split
+    // (MI355X at 19456 x 2560: 19 vs 24-26 us at M = 24 and 32; at the
+    // smaller config shapes the two are within 10% and the GEMV stays).
     const bool skinny = flags & HEPH_FLAG_FORCE_SKINNY;
-    const bool gemv = !skinny && !(flags & HEPH_FLAG_FORCE_GEMM) && M <= HEPH_SKINNY_MAX_M;
+    const bool split_gemm = M > 16 && (long)N * K >= (32L << 20) && gemm_splits_ready(op);
+    const bool gemv = !skinny && !(flags & HEPH_FLAG_FORCE_GEMM) && M <= HEPH_SKINNY_MAX_M &&
+                      !split_gemm;
     const bool fuse_ok = !skip_quant && !(flags & HEPH_FLAG_NO_FUSE) && group_k == kChunk;
     const bool fused = fuse_ok && ((gemv && gemv_fuses(M, N, K)) || (skinny && M <= kFusedMaxM));
     LaunchTiming t = take_timing();
@@ -266,7 +272,8 @@ int heph_set_tuning(int knob, int value)
         gu = value;
         break;
     case HEPH_TUNE_GEMM_BM:
-        if (value != 0 && value != 128 && value != 192 && value != 256) return HEPH_ERR_FLAGS;
+        if (value != 0 && value != 1 && value != 128 && value != 192 && value != 256)
+            return HEPH_ERR_FLAGS;
         gemm_tune(value);
         return HEPH_OK;
     default: return HEPH_ERR_FLAGS;

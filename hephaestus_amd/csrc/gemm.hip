@@ -512,7 +512,12 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
                 for (int e = 0; e < 4; ++e) {
                     v[e] = acc[mi][ni][e];
                     if constexpr (SM == 2)
-                        v[e] = (v[e] * sa) * op.sw[min(n0 + c_lane + ni * 16 + e, N - 1)];
+                    {
+                        // reference association: acc*(sa*sw) at M = 1
+                        // (wmma_gfx12.mojo:711-712), (acc*sa)*sw otherwise (:848)
+                        const float sw = op.sw[min(n0 + c_lane + ni * 16 + e, N - 1)];
+                        v[e] = M == 1 ? v[e] * (sa * sw) : (v[e] * sa) * sw;
+                    }
                 }
                 const uint2 pk = make_uint2(pack_bf16_hw(v[0], v[1]), pack_bf16_hw(v[2], v[3]));
                 *reinterpret_cast<uint2*>(smem + (r_lane + mi * 16) * RB +
@@ -557,10 +562,11 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
             const f32x4 hi = *reinterpret_cast<const f32x4*>(&Cs[r * CST + c8 + 4]);
             float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             if constexpr (SM == 2) {
-                // reference association (acc * sa) * sw (M >= 128 here)
+                // reference association: acc*(sa*sw) at M = 1, else (acc*sa)*sw
                 const float sa = op.s[grow];
 #pragma unroll
-                for (int t = 0; t < 8; ++t) v[t] = (v[t] * sa) * op.sw[gcol + t];
+                for (int t = 0; t < 8; ++t)
+                    v[t] = M == 1 ? v[t] * (sa * op.sw[gcol + t]) : (v[t] * sa) * op.sw[gcol + t];
             }
             const size_t o = (size_t)grow * N + gcol;
             if (op.c_f32) {
@@ -676,7 +682,7 @@ hipError_t launch_big(const Fp8Operands& op, hipStream_t stream, const LaunchTim
 int gemm_tile_m(int M, int N)
 {
     const int forced = g_tune_bm.load(std::memory_order_relaxed);
-    if (forced) return forced;
+    if (forced >= 128) return forced;
     const long cus = cu_count();
     struct { int bm; long cycles; } const tiles_cost[] = {{256, 2990}, {192, 2480}, {128, 2240}};
     int best = 256;
@@ -704,7 +710,6 @@ void gemm_tune(int bm) { g_tune_bm.store(bm, std::memory_order_relaxed); }
 // and gate_up whole; M = 4096 never splits.
 int gemm_splits(int M, int N, int K)
 {
-    if (M < 128) return 1;
     const int bm = gemm_tile_m(M, N);
     const long tiles = (long)((M + bm - 1) / bm) * ((N + L_BN - 1) / L_BN);
     const long cus = cu_count();
@@ -725,6 +730,13 @@ int gemm_splits(int M, int N, int K)
     return best;
 }
 
+bool gemm_splits_ready(const Fp8Operands& op)
+{
+    if (!op.part || op.s_step == 0) return false;
+    const int s = gemm_splits(op.M, op.N, op.K);
+    return s > 1 && op.part_bytes >= (size_t)s * op.M * op.N * 4;
+}
+
 size_t gemm_split_bytes(int M, int N, int K)
 {
     const int s = gemm_splits(M, N, K);
@@ -734,21 +746,18 @@ size_t gemm_split_bytes(int M, int N, int K)
 hipError_t launch_fp8_gemm(const Fp8Operands& op, hipStream_t stream,
                            const LaunchTiming& t, const char** name)
 {
-    // M >= 128: the 256-column DMA kernel (N % 16 == 0 keeps every 8-wide
-    // output group inside the row; its 32-bit operand offsets need M*K and
-    // N*K below 2^31). It is as fast as the 128x128 kernel below M = 128
-    // and faster from there on (MI355X, the configs[3] shapes: 1.3-2x at
-    // M = 128..512). Otherwise the 128x128 kernel.
+    // The 256-column DMA kernel for every M (N % 16 == 0 keeps every 8-wide
+    // output group inside the row), splitting K when its tiles leave CUs
+    // idle; its 32-bit operand offsets need M*K and N*K below 2^31, else the
+    // 128x128 kernel. (Without splits the two run alike below M = 128; the
+    // 256-column kernel is 1.3-2x faster from there on, MI355X.)
     const bool small_offsets = (long)op.M * op.K < (1L << 31) && (long)op.N * op.K < (1L << 31);
-    if (op.M >= 128 && small_offsets) {
+    const bool force_128 = g_tune_bm.load(std::memory_order_relaxed) == 1;
+    if (small_offsets && !force_128) {
         // K splits when the caller's scratch holds their partials (block or
         // per-channel weights with per-chunk activation scales).
         Fp8Operands o = op;
-        o.splits = 1;
-        if (o.part && o.s_step != 0) {
-            const int s = gemm_splits(o.M, o.N, o.K);
-            if (s > 1 && o.part_bytes >= (size_t)s * o.M * o.N * 4) o.splits = s;
-        }
+        o.splits = gemm_splits_ready(o) ? gemm_splits(o.M, o.N, o.K) : 1;
         const bool sk = o.splits > 1;
         switch (gemm_tile_m(o.M, o.N)) {
         case 128:

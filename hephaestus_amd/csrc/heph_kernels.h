@@ -101,6 +101,9 @@ void gemm_tune(int bm);
 // none), and the scratch bytes that takes.
 int gemm_splits(int M, int N, int K);
 size_t gemm_split_bytes(int M, int N, int K);
+// Whether op's scratch (part) holds the partials of gemm_splits(M, N, K) > 1
+// splits.
+bool gemm_splits_ready(const Fp8Operands& op);
 
 // bf16 x [M,K] @ w [N,K]^T, f32 accumulation, M <= 32.
 hipError_t launch_bf16_skinny(void* c, bool c_f32, bool residual, const uint16_t* x,

@@ -167,7 +167,9 @@ const char* heph_last_kernel(void);
  *   HEPH_TUNE_GEMV_WAVES    its waves per workgroup: 0, 4, 8 or 16 (16 only
  *                           for 8 < M <= 16; 8 is used otherwise)
  *   HEPH_TUNE_GEMV_U        its steps per load batch: 0, 1, 2 (1 with 16 waves)
- *   HEPH_TUNE_GEMM_BM       tile height of the M >= 1024 GEMM: 0, 128, 192, 256
+ *   HEPH_TUNE_GEMM_BM       tile height of the 256-column GEMM: 0, 128, 192,
+ *                           256; 1 selects the 128x128 GEMM (otherwise only
+ *                           used when M*K or N*K reaches 2^31)
  */
 #define HEPH_TUNE_SKINNY_WAVES 1
 #define HEPH_TUNE_SKINNY_U     2

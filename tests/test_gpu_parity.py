@@ -715,6 +715,41 @@ def test_large_m_odd_chunk_counts(K, tile_m):
     assert np.array_equal(host_bf16(c), bf16_of(exact.astype(np.float32)))
 
 
+@pytest.mark.parametrize("mode", ["block", "channel_token", "channel_g128"])
+@pytest.mark.parametrize("M", [1, 33, 100, 129])
+def test_gemm_128x128_fallback(mode, M):
+    # The 128x128 GEMM serves operands past 32-bit offsets; forced here on
+    # small shapes: random data within the tolerance in every scale mode,
+    # exact-integer lattices bit for bit, residual and f32 output.
+    HK.set_tuning(L.TUNE_GEMM_BM, 1)
+    try:
+        N, K = 400, 1152
+        x = O.gen_act_bf16(110 + M, M, K, outlier_p=1e-3)
+        if mode == "block":
+            qw, sw = O.gen_weight(111 + M, N, K)
+            bn, bk, g = 128, 128, 128
+        else:
+            qw, sw = O.quant_weight(O.gen_normal(111 + M, N * K, 0.0, 0.02).reshape(N, K), 1, K)
+            bn, bk, g = 1, K, (K if mode == "channel_token" else 128)
+        r = O.gen_normal(112 + M, M * N).reshape(M, N).astype(np.float32)
+        c, _, _ = run_linear(qw, sw, x, M=M, N=N, K=K, group_k=g, out=torch.float32,
+                             residual=dev(r), flags=L.FLAG_FORCE_GEMM)
+        assert HK.last_kernel() == "fp8_gemm_128x128"
+        ref = O.quant_linear(x, qw, sw, group_k=g, bn=bn, bk=bk) + r
+        assert max_abs_rel(c.cpu().numpy(), ref) <= TOL
+        ia, qa = lattice(M, K, 8000 + M)
+        iw, qwl = lattice(N, K, 8001)
+        sa = np.full(M * (K // 128), 2.0 ** -3, np.float32)
+        swl = np.full((-(-N // 128), K // 128), 2.0 ** -2, np.float32)
+        exact = (ia.astype(np.float64) @ iw.astype(np.float64).T) * 0.0625 * 2.0 ** -5
+        c, _, _ = run_linear(qwl, swl, None, M=M, N=N, K=K, skip_quant=True, flags=L.FLAG_FORCE_GEMM,
+                             q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
+        assert HK.last_kernel() == "fp8_gemm_128x128"
+        assert np.array_equal(host_bf16(c), bf16_of(exact.astype(np.float32)))
+    finally:
+        HK.set_tuning(L.TUNE_GEMM_BM, 0)
+
+
 @pytest.mark.parametrize("M,N,K", [(512, 2560, 4096), (256, 2560, 9728), (384, 1040, 4224)])
 @pytest.mark.parametrize("out,resid", [("bf16", False), ("bf16", True), ("f32", True)])
 def test_large_m_split_k(M, N, K, out, resid):
@@ -737,6 +772,24 @@ def test_large_m_split_k(M, N, K, out, resid):
         ref = ref + (f32_of_bf16(bf16_of(r)) if out == "bf16" else r)
     got = f32_of_bf16(host_bf16(c)) if out == "bf16" else c.cpu().numpy()
     assert max_abs_rel(got, ref) <= TOL
+    qo, _ = O.quant_act(x, 128)
+    assert np.array_equal(q_ws[: M * K].cpu().numpy().reshape(M, K), qo)
+
+
+@pytest.mark.parametrize("M", [17, 24, 32])
+@pytest.mark.parametrize("name", ["qkv", "gate_up", "down", "o_proj"])
+def test_batched_decode_split_gemm_route(M, name):
+    # 16 < M <= 32 with a split-capable q_ws: weights of at least 32M
+    # elements (gate_up) take quantizer + K-split GEMM, the rest stays on the
+    # GEMV; both within the tolerance, codes bit-exact.
+    N, K = SHAPES[name]
+    x = O.gen_act_bf16(120 + M, M, K)
+    qw, sw = O.gen_weight(1000 + N + K, N, K)
+    q_ws, s_ws = HK.workspace(M, K, n=N)
+    c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K, q_ws=q_ws, s_ws=s_ws)
+    big = N * K >= 32 << 20
+    assert HK.last_kernel().endswith("_splitk") == big, HK.last_kernel()
+    check_close(host_bf16(c), O.quant_linear(x, qw, sw), f"{name} M={M}")
     qo, _ = O.quant_act(x, 128)
     assert np.array_equal(q_ws[: M * K].cpu().numpy().reshape(M, K), qo)
 
