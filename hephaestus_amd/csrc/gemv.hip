@@ -24,8 +24,9 @@
 //   * fused mode (1x128 groups) quantizes x inside the kernel:
 //     64/(KS*MR) lanes share an A row's 128-element group, its max (on the
 //     bf16 magnitude bits, two per packed 16-bit max, NaN skipped) is
-//     reduced with DPP, the scale is the reference's own division
-//     (amax/448, 1/s, both rounded to nearest even), and the codes reach
+//     reduced with DPP and lane swaps, the scale is the reference's
+//     (amax/448, 1/s, both rounded to nearest even) computed without a
+//     division (group_scale in heph_device.h), and the codes reach
 //     the MFMA A layout through a per-wave LDS tile. Workgroup 0 also
 //     writes q/s to the workspace so later SKIP_QUANT calls can reuse them;
 //   * each lane rescales its candidate C elements by sa[row, chunk] *
@@ -53,15 +54,6 @@ struct GemvArgs {
 enum GemvScale { kGemvBlock = 0, kGemvChannel = 1, kGemvConst = 2 };
 
 namespace {
-
-// The reference group scale (kernels.mojo:173-181): s = amax / 448, 1.0
-// below 1e-12, inv = 1 / s; both divisions IEEE round-to-nearest-even.
-__device__ __forceinline__ void group_scale_div(float amax, float& s, float& inv)
-{
-    s = __fdiv_rn(amax, kE4M3Max);
-    if (s < 1e-12f) s = 1.0f;
-    inv = __frcp_rn(s);
-}
 
 // E consecutive bf16 activations (E = 2, 4, 8, 16 or 32) as E/2 dwords.
 template <int E>
@@ -106,7 +98,10 @@ __device__ __forceinline__ void store_codes(uint8_t* p, const uint32_t* cd)
     }
 }
 
-// Max over each aligned run of LPR lanes, unsigned integers.
+// Max over each aligned run of LPR lanes, unsigned integers, left in every
+// lane of the run: DPP within each 16-lane row, then gfx950's lane swaps
+// (v_permlane16_swap pairs rows 0-1 and 2-3, v_permlane32_swap the two
+// halves), which stay in the VALU instead of going through LDS.
 template <int LPR>
 __device__ __forceinline__ uint32_t lanes_max_u(uint32_t m)
 {
@@ -117,10 +112,14 @@ __device__ __forceinline__ uint32_t lanes_max_u(uint32_t m)
     m = max(m, dpp(m, std::integral_constant<int, 0x4E>{}));
     if constexpr (LPR >= 8) m = max(m, dpp(m, std::integral_constant<int, 0x141>{}));
     if constexpr (LPR >= 16) m = max(m, dpp(m, std::integral_constant<int, 0x140>{}));
-    if constexpr (LPR >= 32) m = max(m, (uint32_t)__shfl_xor((int)m, 16));
-    if constexpr (LPR == 64)
-        m = max((uint32_t)__builtin_amdgcn_readlane((int)m, 0),
-                (uint32_t)__builtin_amdgcn_readlane((int)m, 32));
+    if constexpr (LPR >= 32) {
+        const auto r = __builtin_amdgcn_permlane16_swap(m, m, false, false);
+        m = max((uint32_t)r[0], (uint32_t)r[1]);
+    }
+    if constexpr (LPR == 64) {
+        const auto r = __builtin_amdgcn_permlane32_swap(m, m, false, false);
+        m = max((uint32_t)r[0], (uint32_t)r[1]);
+    }
     return m;
 }
 
@@ -182,7 +181,6 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
     __shared__ __attribute__((aligned(16))) uint8_t qlds[FUSED ? WAVES : 1][FUSED ? U : 1]
                                                         [FUSED ? MT : 1][R * kChunk];
     if (threadIdx.x == 0) arrive = 0;
-    __syncthreads();
 
     const int n = n0 + r16 % TW;
     const uint8_t* wrow = op.w + (size_t)n * K + g * 16;
@@ -277,12 +275,15 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
                     const XVec<E>& xv = b.xv[u][mt];
-                    uint32_t mb = lanes_max_u<LPR>(absmax_bits(xv.d));
-                    if (__builtin_amdgcn_ballot_w64(mb > 0x7F80u) != 0)
-                        mb = lanes_max_u<LPR>(absmax_bits_skip_nan(xv.d));
-                    const float m = bf16_bits_f32(mb);
+                    // a lane holding a NaN takes the NaN-skipping max of its
+                    // own elements before the cross-lane max (rare; a
+                    // divergent branch that no lane takes costs two scalar
+                    // instructions)
+                    uint32_t mb = absmax_bits(xv.d);
+                    if (mb > 0x7F80u) mb = absmax_bits_skip_nan(xv.d);
+                    mb = lanes_max_u<LPR>(mb);
                     float inv;
-                    group_scale_div(m, sc[u][mt], inv);
+                    group_scale(bf16_bits_f32(mb), sc[u][mt], inv);
                     uint32_t cd[(E + 3) / 4];
                     if constexpr (E == 2) {
                         cd[0] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
@@ -360,6 +361,10 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
     // current ones.
     Batch b0, b1;
     if (sb < se) issue(b0, sb);
+    // arrive = 0 is seen by every wave before any wave's increment; the
+    // barrier waits here, with the first loads in flight, rather than
+    // before them
+    __syncthreads();
     for (int s = sb; s < se; s += 2 * U) {
         if (s + U < se) issue(b1, s + U);
         consume(b0, s);

@@ -13,7 +13,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "scale_tables.h"
+#include "group_scale.h"
 
 namespace heph {
 
@@ -133,23 +133,29 @@ __device__ __forceinline__ uint2 quant8(const uint4& v, float inv)
 }
 
 // Group scale of the reference quantizer for a bf16 amax: s = RN(amax/448)
-// (1.0 when below 1e-12) and inv = RN(1/s), from the exact mantissa tables
-// of scale_tables.h plus one ldexp each (no division). amax must be the
-// magnitude of a bf16 value (low 16 bits zero); zero and subnormal amax
-// take the floor, an infinite amax gives s = inf, inv = 0 as the division
-// would.
-static __constant__ ScaleTables g_scale_tab = make_scale_tables();
-
+// (1.0 when below 1e-12) and inv = RN(1/s), division-free (group_scale.h):
+// mantissa parts from an FMA-corrected product and an FMA Newton step on
+// the hardware reciprocal, exponents by ldexp. amax must be the magnitude
+// of a bf16 value (low 16 bits zero); zero and subnormal amax take the
+// floor, an infinite amax gives s = inf, inv = 0 as the division would.
+// Branch-free: a short dependent chain, as it sits between an activation
+// load and the first MFMA that uses it.
 __device__ __forceinline__ void group_scale(float amax, float& s, float& inv)
 {
     const uint32_t u = __float_as_uint(amax);
     const int e = (int)(u >> 23);
-    const int m = (int)((u >> 16) & 0x7Fu);
-    if (e == 0) { s = 1.0f; inv = 1.0f; return; }
-    if (e == 255) { s = __builtin_inff(); inv = 0.0f; return; }
-    s = ldexpf(g_scale_tab.scale[m], e - 134);
-    inv = ldexpf(g_scale_tab.inv[m], 134 - e);
-    if (s < 1e-12f) { s = 1.0f; inv = 1.0f; }
+    const float q = scale_mant((float)(int)(128u + ((u >> 16) & 0x7Fu)));
+    const float y = inv_mant(q, __builtin_amdgcn_rcpf(q));
+    s = __builtin_amdgcn_ldexpf(q, e - 140);
+    inv = __builtin_amdgcn_ldexpf(y, 140 - e);
+    if (e == 255) {
+        s = __builtin_inff();
+        inv = 0.0f;
+    }
+    if (e == 0 || s < 1e-12f) {
+        s = 1.0f;
+        inv = 1.0f;
+    }
 }
 
 __device__ __forceinline__ i32x4 ldg16(const void* p)

@@ -527,22 +527,16 @@ def test_errors_raise():
 
 # --------------------------------------------- scales, weights, graphs ----
 
-def test_scale_tables_every_bf16_amax():
-    # One 128-group per positive finite bf16 value v: the group holds v at a
-    # position that moves with the group, and v/2, v/3 ... elsewhere, so
-    # every possible amax is met once; scales and codes must match the
-    # oracle bit for bit (the table path replaces a division).
-    vals = np.arange(0x0001, 0x7F80, dtype=np.uint32)          # +finite bf16
-    G = vals.size
-    v = O.bf16_to_f32(vals.astype(np.uint16))
-    frac = np.linspace(-0.99, 0.99, 128).astype(np.float32)
-    grp = (v[:, None] * frac[None, :]).astype(np.float32)
-    grp[np.arange(G), np.arange(G) % 128] = v
+def test_group_scale_every_bf16_amax():
+    # Every possible group amax (one group per positive finite bf16 value)
+    # through the row quantizer: scales and codes must match the oracle bit
+    # for bit (the division-free group scale replaces two divisions).
+    row = every_amax_row()
     K = 2560
-    rows = -(-G * 128 // K)
-    flat = np.zeros(rows * K, np.float32)
-    flat[: G * 128] = grp.reshape(-1)
-    x = bf16_of(flat).reshape(rows, K)
+    rows = -(-row.shape[1] // K)
+    flat = np.zeros(rows * K, np.uint16)
+    flat[: row.shape[1]] = row.reshape(-1)
+    x = flat.reshape(rows, K)
     q = torch.zeros(rows * K, dtype=torch.uint8, device="cuda")
     s = torch.zeros(rows * (K // 128), dtype=torch.float32, device="cuda")
     HK.quantize_act_rows_fp8(q, s, dev(x), rows, K, group_k=128)
@@ -550,6 +544,43 @@ def test_scale_tables_every_bf16_amax():
     qo, so = O.quant_act(x, 128)
     assert np.array_equal(s.cpu().numpy().reshape(so.shape), so)
     assert np.array_equal(q.cpu().numpy().reshape(qo.shape), qo)
+
+
+def every_amax_row():
+    """One bf16 row of 128-groups, one per positive finite bf16 value v: v
+    sits at a position that moves with the group, v*f (|f| < 1) elsewhere,
+    so every possible group amax is met once."""
+    vals = np.arange(0x0001, 0x7F80, dtype=np.uint32)
+    G = vals.size
+    v = O.bf16_to_f32(vals.astype(np.uint16))
+    frac = np.linspace(-0.99, 0.99, 128).astype(np.float32)
+    grp = (v[:, None] * frac[None, :]).astype(np.float32)
+    grp[np.arange(G), np.arange(G) % 128] = v
+    return bf16_of(grp.reshape(1, -1))
+
+
+def test_fused_gemv_every_bf16_amax():
+    # The fused M = 1 GEMV quantizes inside the kernel with the division-free
+    # group scale and, per chunk-slot count, 64/32/16/8-lane amax groups
+    # (lane swaps for 64 and 32): codes and scales must match the oracle bit
+    # for bit for every possible amax.
+    x = every_amax_row()
+    K = x.shape[1]
+    N = 16
+    qo, so = O.quant_act(x, 128)
+    qw = np.zeros((N, K), np.uint8)
+    sw = np.ones((1, K // 128), np.float32)
+    try:
+        for ks in (1, 2, 4, 8):
+            HK.set_tuning(L.TUNE_GEMV_KS, ks)
+            _, q_ws, s_ws = run_linear(qw, sw, x, M=1, N=N, K=K)
+            assert HK.last_kernel() == "fp8_gemv_fused_m1", HK.last_kernel()
+            sg = s_ws.cpu().numpy().reshape(so.shape)
+            bad = np.flatnonzero(sg.view(np.uint32) != so.view(np.uint32))
+            assert bad.size == 0, (ks, bad[:4], sg.reshape(-1)[bad[:4]], so.reshape(-1)[bad[:4]])
+            assert np.array_equal(q_ws.cpu().numpy().reshape(qo.shape), qo), ks
+    finally:
+        HK.set_tuning(L.TUNE_GEMV_KS, 0)
 
 
 @pytest.mark.parametrize("N,K", [(256, 384), (300, 2560), (19456, 2560)])
