@@ -71,7 +71,8 @@ SIGNATURES = {
     "heph_attention_ws_bytes": (_sz, [_i, _i]),
     "heph_attention_fp8kv": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "heph_silu_mul": (_i, [_vp, _vp, _vp, _i, _vp]),
-    "heph_argmax_bf16": (_i, [_vp, _vp, _i, _vp]),
+    "heph_argmax_ws_bytes": (_sz, [_i]),
+    "heph_argmax_bf16": (_i, [_vp, _vp, _i, _vp, _sz, _vp]),
 }
 
 ATTN_MAX_KEYS = 262144

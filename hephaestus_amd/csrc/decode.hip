@@ -65,6 +65,13 @@ __device__ __forceinline__ float wave_sum64(float v)
     return __shfl(v, 0, 64);
 }
 
+// Max over the 64 lanes of a wave (exact in any order), in every lane.
+__device__ __forceinline__ float wave_max64(float v)
+{
+    for (int h = 32; h > 0; h >>= 1) v = fmaxf(v, __shfl_xor(v, h, 64));
+    return v;
+}
+
 // A token id outside [0, vocab) gives a zero row instead of a read past
 // the table (the host cannot see device-side ids).
 __global__ __launch_bounds__(256) void embed_fp8_kernel(uint16_t* x, const uint8_t* emb,
@@ -85,49 +92,68 @@ __global__ __launch_bounds__(256) void embed_fp8_kernel(uint16_t* x, const uint8
 }
 
 // One workgroup of 256 threads per row; thread t owns elements t, t + 256,
-// ... Rows up to kNormMax elements are loaded into registers, x and gamma
-// together, every load issued before the first use (one memory round
-// trip); longer rows loop.
-constexpr int kNormPer = 40;
-constexpr int kNormMax = 256 * kNormPer;
+// ... and sums their squares in that order (fma); the 256 sums are folded
+// as s[t] += s[t + h] for h = 128, 64, ..., 1. The first two levels are read
+// by wave 0 from LDS as (s[t] + s[t+128]) + (s[t+64] + s[t+192]), the rest
+// move between its lanes: two barriers in all. Rows up to 256 * PER
+// elements hold x and gamma in registers, every load issued before the
+// first use; longer rows loop.
+__device__ __forceinline__ float fold256_wave0(float v, float* red, float* out)
+{
+    const int t = threadIdx.x;
+    red[t] = v;
+    __syncthreads();
+    if (t < 64) {
+        float a = (red[t] + red[t + 128]) + (red[t + 64] + red[t + 192]);
+        for (int h = 32; h > 0; h >>= 1) a += __shfl_down(a, h, 64);
+        if (t == 0) *out = a;
+    }
+    __syncthreads();
+    return *out;
+}
 
+__device__ __forceinline__ float rms_inv(float ss, int cols, float eps)
+{
+    return __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)cols) + eps));
+}
+
+template <int PER>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* out, const uint16_t* in,
                                                       const uint16_t* gamma, int cols, float eps)
 {
     __shared__ float red[256];
+    __shared__ float res;
     const uint16_t* x = in + (size_t)blockIdx.x * cols;
     uint16_t* y = out + (size_t)blockIdx.x * cols;
     const int t = threadIdx.x;
-    if (cols <= kNormMax) {
-        float v[kNormPer], g[kNormPer];
+    if constexpr (PER > 0) {
+        float v[PER], g[PER];
 #pragma unroll
-        for (int e = 0; e < kNormPer; ++e) {
+        for (int e = 0; e < PER; ++e) {
             const int i = t + e * 256;
             v[e] = i < cols ? f32_of_bf16(x[i]) : 0.0f;
             g[e] = i < cols ? f32_of_bf16(gamma[i]) : 0.0f;
         }
         float ss = 0.0f;
 #pragma unroll
-        for (int e = 0; e < kNormPer; ++e)
+        for (int e = 0; e < PER; ++e)
             if (t + e * 256 < cols) ss = __builtin_fmaf(v[e], v[e], ss);
-        ss = block_sum256(ss, red);
-        const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)cols) + eps));
+        const float r = rms_inv(fold256_wave0(ss, red, &res), cols, eps);
 #pragma unroll
-        for (int e = 0; e < kNormPer; ++e) {
+        for (int e = 0; e < PER; ++e) {
             const int i = t + e * 256;
             if (i < cols) y[i] = f32_to_bf16(g[e] * round_bf16(v[e] * r));
         }
-        return;
+    } else {
+        float ss = 0.0f;
+        for (int i = t; i < cols; i += 256) {
+            const float v = f32_of_bf16(x[i]);
+            ss = __builtin_fmaf(v, v, ss);
+        }
+        const float r = rms_inv(fold256_wave0(ss, red, &res), cols, eps);
+        for (int i = t; i < cols; i += 256)
+            y[i] = f32_to_bf16(f32_of_bf16(gamma[i]) * round_bf16(f32_of_bf16(x[i]) * r));
     }
-    float ss = 0.0f;
-    for (int i = t; i < cols; i += 256) {
-        const float v = f32_of_bf16(x[i]);
-        ss = __builtin_fmaf(v, v, ss);
-    }
-    ss = block_sum256(ss, red);
-    const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)cols) + eps));
-    for (int i = t; i < cols; i += 256)
-        y[i] = f32_to_bf16(f32_of_bf16(gamma[i]) * round_bf16(f32_of_bf16(x[i]) * r));
 }
 
 // RoPE angle for pair p of a D-wide head at position pos, and its bf16 cos
@@ -199,148 +225,264 @@ __device__ __forceinline__ void decode16(const uint4& w, float* f)
     }
 }
 
-// Attention over the E4M3 cache runs as three kernels over splits of
-// kAttnSplit keys, with scores and per-split sums in a caller workspace:
-//   A  scores:  s_j = (sum_d q_d * k_jd, d in order) * sk / sqrt(128)
-//   B  softmax: m = max s; sum of e_j = exp(s_j - m) as per-thread sums over
-//      j = t, t + 256, ... in order folded across the 256 threads; p_j =
-//      bf16(e_j * (1/sum)); then this split's PV: per-thread sums over its
-//      keys j = t, t + 256 (in order) folded across threads -> r_split[d]
+// Attention over the E4M3 cache: three kernels over splits of kAttnSplit
+// keys, one workgroup per (kv head, split) serving all G query heads that
+// share the kv head, so every K and V byte is read once:
+//   A  scores: thread t of a workgroup holds dims 16c .. 16c+15 (c = t & 7)
+//      of keys j = 128*split + (t >> 3) + 32i (i < 4), one 16-byte load
+//      each (eight lanes read a key's 128-byte row). Per head g:
+//        part_c = sum over those 16 dims in order (fma), then
+//        s_j = (((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7))) * (sk * f32(1/sqrt(128)))
+//      written to the workspace, with the split's max m_s and
+//        l_s = slots4 over ks of (sum over i in order of exp(s_j - m_s)),
+//      j = 128*split + ks + 32i, where slots4 sums 32 slot values as
+//      ((a0+a1)+(a2+a3)) + ((a4+a5)+(a6+a7)) per wave (8 slots) and the
+//      four waves in order
+//   B  values: m = max over splits of m_s; sum = fold over 64 slots
+//      (v[l] += v[l + h], h = 32 .. 1) of the per-slot fma sums (slot l:
+//      splits l, l+64, ... in order) of l_s * exp(m_s - m);
+//      p_j = bf16(exp(s_j - m) * (1/sum)) (the
+//      reference's probability, kernels.mojo:1003-1019, global max and sum);
+//      per (head, dim): a_ks = sum over i in order of p_j * v_j (fma), then
+//      slots4 over ks -> r_split
 //   C  out_d = bf16((sum over splits of r_split[d], in split order) * sv)
-// The order is fixed by kAttnSplit, not by the launch, and the CPU
-// restatement repeats it. Workgroups are numbered so that the query heads
-// sharing a kv head and a split land on the same XCD (shared L2).
-constexpr int kAttnSplit = 512;
+// The same block index maps to the same (kv head, split) in A and B, so a
+// split's scores are read back on the XCD (L2) that wrote them. The CPU
+// restatement repeats every order above.
+constexpr int kAttnSplit = 128;
 
-struct AttnMap {
-    int h, split;
+struct AttnWs {
+    float* scores;   // [n_heads][n_keys]
+    float* smax;     // [n_heads][n_splits]
+    float* ssum;     // [n_heads][n_splits]
+    float* partial;  // [n_heads][n_splits][128]
 };
 
-__device__ __forceinline__ AttnMap attn_map(int b, int n_heads, int n_kv, int n_splits)
+__device__ __forceinline__ AttnWs attn_ws(float* ws, int n_heads, int n_keys, int n_splits)
 {
-    const int F = n_kv * n_splits;      // (kv head, split) pairs
-    const int qi = b / F, f = b % F;
-    return {(f / n_splits) * (n_heads / n_kv) + qi, f % n_splits};
+    AttnWs w;
+    w.scores = ws;
+    w.smax = w.scores + (size_t)n_heads * n_keys;
+    w.ssum = w.smax + (size_t)n_heads * n_splits;
+    w.partial = w.ssum + (size_t)n_heads * n_splits;
+    return w;
 }
 
+// x + (the value of lane l ^ 1, l ^ 2 or l ^ 4 within each 8-lane group),
+// i.e. one level of the 8-lane butterfly (quad_perm [1,0,3,2], [2,3,0,1],
+// row_half_mirror: lane l pairs with 7 - l, the other quad).
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x)
+{
+    return x + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+// Over the 8 key slots of a wave (lanes 8k + c, k < 8): the max, or the
+// sum ((a0+a1)+(a2+a3)) + ((a4+a5)+(a6+a7)); the result in every lane.
+// Pairs k^1 by row_ror:8, then rows 0-1 / 2-3 by v_permlane16_swap, then
+// the two halves by v_permlane32_swap (each pair's sum is the same value
+// in both lanes, as float addition commutes).
+template <bool MAX>
+__device__ __forceinline__ float slots_reduce(float x)
+{
+    const float y = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xf, 0xf, false));
+    x = MAX ? fmaxf(x, y) : x + y;
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                      false);
+    x = MAX ? fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]))
+            : __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                      false);
+    return MAX ? fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]))
+               : __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
+template <int G>
 __global__ __launch_bounds__(256) void attn_scores_kernel(
-    float* scores, const uint16_t* q, const uint8_t* kc, const float* kv_scale, int n_heads,
-    int n_kv, int n_keys, int n_splits)
+    float* ws, const uint16_t* q, const uint8_t* kc, const float* kv_scale, int n_kv,
+    int n_keys, int n_splits)
 {
     constexpr int D = 128;
-    const AttnMap m = attn_map(blockIdx.x, n_heads, n_kv, n_splits);
-    const int t = threadIdx.x, kh = m.h / (n_heads / n_kv);
+    const int kh = blockIdx.x % n_kv, split = blockIdx.x / n_kv;
+    const int t = threadIdx.x, ks = t >> 3, c = t & 7;
+    const AttnWs w = attn_ws(ws, n_kv * G, n_keys, n_splits);
     const size_t row = (size_t)n_kv * D;
-    float qv[D];
+    const int j0 = split * kAttnSplit + ks;
+    uint4 kv[4];
 #pragma unroll
-    for (int c = 0; c < D / 8; ++c) {
-        const uint4 w = ldg16u(q + (size_t)m.h * D + c * 8);
-        qv[8 * c] = bf16lo(w.x); qv[8 * c + 1] = bf16hi(w.x);
-        qv[8 * c + 2] = bf16lo(w.y); qv[8 * c + 3] = bf16hi(w.y);
-        qv[8 * c + 4] = bf16lo(w.z); qv[8 * c + 5] = bf16hi(w.z);
-        qv[8 * c + 6] = bf16lo(w.w); qv[8 * c + 7] = bf16hi(w.w);
+    for (int i = 0; i < 4; ++i)
+        kv[i] = ldg16u(kc + (size_t)min(j0 + 32 * i, n_keys - 1) * row + kh * D + 16 * c);
+    float qv[G][16];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const uint16_t* qp = q + (size_t)(kh * G + g) * D + 16 * c;
+        const uint4 a = ldg16u(qp), b = ldg16u(qp + 8);
+        const uint32_t d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            qv[g][2 * e] = bf16lo(d[e]);
+            qv[g][2 * e + 1] = bf16hi(d[e]);
+        }
     }
     const float qk_scale = kv_scale[kh] * 0.08838834764831845f;   // sk * f32(1/sqrt(128))
-    const int j0 = m.split * kAttnSplit + t;
-    uint4 w[2][8];
+    float sc[4][G];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int j = min(j0 + u * 256, n_keys - 1);
-        const uint4* kp = reinterpret_cast<const uint4*>(kc + j * row + kh * D);
+    for (int i = 0; i < 4; ++i) {
+        float k16[16];
+        decode16(kv[i], k16);
 #pragma unroll
-        for (int c = 0; c < 8; ++c) w[u][c] = kp[c];
-    }
+        for (int g = 0; g < G; ++g) {
+            float part = 0.0f;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int j = j0 + u * 256;
-        float dot = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            float k16[16];
-            decode16(w[u][c], k16);
-#pragma unroll
-            for (int k = 0; k < 16; ++k) dot = __builtin_fmaf(qv[16 * c + k], k16[k], dot);
+            for (int e = 0; e < 16; ++e) part = __builtin_fmaf(qv[g][e], k16[e], part);
+            part = dpp_add<0xB1>(part);
+            part = dpp_add<0x4E>(part);
+            part = dpp_add<0x141>(part);
+            sc[i][g] = part * qk_scale;
         }
-        if (j < n_keys) scores[(size_t)m.h * n_keys + j] = dot * qk_scale;
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int j = j0 + 32 * i;
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+            if (c == g && j < n_keys) w.scores[(size_t)(kh * G + g) * n_keys + j] = sc[i][g];
+    }
+    // split max and sum of exp(s - m_s): within a wave over its 8 key slots
+    // (all 8 lanes of a slot hold its scores), then over the 4 waves in LDS
+    __shared__ float wst[2][4][G];
+    const int wave = t >> 6;
+    float mw[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float m = -3.4e38f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (j0 + 32 * i < n_keys) m = fmaxf(m, sc[i][g]);
+        mw[g] = slots_reduce<true>(m);
+    }
+    if ((t & 63) == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) wst[0][wave][g] = mw[g];
+    }
+    __syncthreads();
+    float aw[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float m = fmaxf(fmaxf(wst[0][0][g], wst[0][1][g]), fmaxf(wst[0][2][g], wst[0][3][g]));
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (j0 + 32 * i < n_keys) a += expf(sc[i][g] - m);
+        aw[g] = slots_reduce<false>(a);
+        if (t == g) w.smax[(size_t)(kh * G + g) * n_splits + split] = m;
+    }
+    if ((t & 63) == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) wst[1][wave][g] = aw[g];
+    }
+    __syncthreads();
+    if (t < G)
+        w.ssum[(size_t)(kh * G + t) * n_splits + split] =
+            ((wst[1][0][t] + wst[1][1][t]) + wst[1][2][t]) + wst[1][3][t];
 }
 
-__global__ __launch_bounds__(256) void attn_pv_kernel(
-    float* partial, const float* scores, const uint8_t* vc, int n_heads, int n_kv, int n_keys,
-    int n_splits)
+template <int G>
+__global__ __launch_bounds__(256) void attn_pv_kernel(float* ws, const uint8_t* vc, int n_kv,
+                                                      int n_keys, int n_splits)
 {
-    constexpr int D = 128, FOLD = 32, PAD = FOLD + 1;
-    __shared__ float red[256 * PAD];
-    const AttnMap m = attn_map(blockIdx.x, n_heads, n_kv, n_splits);
-    const int t = threadIdx.x, kh = m.h / (n_heads / n_kv);
+    constexpr int D = 128;
+    const int kh = blockIdx.x % n_kv, split = blockIdx.x / n_kv;
+    const int t = threadIdx.x, ks = t >> 3, c = t & 7, wave = t >> 6;
+    const AttnWs w = attn_ws(ws, n_kv * G, n_keys, n_splits);
     const size_t row = (size_t)n_kv * D;
-    const float* sc = scores + (size_t)m.h * n_keys;
+    const int j0 = split * kAttnSplit + ks;
 
-    // V rows of this thread's two keys go out first
-    const int j0 = m.split * kAttnSplit + t;
-    uint4 w[2][8];
+    // this thread's V rows and scores go out first
+    uint4 vv[4];
+    float sj[4][G];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int j = min(j0 + u * 256, n_keys - 1);
-        const uint4* vp = reinterpret_cast<const uint4*>(vc + j * row + kh * D);
+    for (int i = 0; i < 4; ++i) {
+        const int j = min(j0 + 32 * i, n_keys - 1);
+        vv[i] = ldg16u(vc + (size_t)j * row + kh * D + 16 * c);
 #pragma unroll
-        for (int c = 0; c < 8; ++c) w[u][c] = vp[c];
+        for (int g = 0; g < G; ++g) sj[i][g] = w.scores[(size_t)(kh * G + g) * n_keys + j];
     }
-    float mx = -3.4e38f;
-    for (int j = t; j < n_keys; j += 256) mx = fmaxf(mx, sc[j]);
-    red[t] = mx;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if (t < s) red[t] = fmaxf(red[t], red[t + s]);
-        __syncthreads();
-    }
-    mx = red[0];
-    __syncthreads();
-    float se = 0.0f;
-    for (int j = t; j < n_keys; j += 256) se += expf(sc[j] - mx);
-    se = block_sum256(se, red);
-    const float inv = __fdiv_rn(1.0f, se);
 
-    float acc[D];
+    // global max and sum per head from the split statistics, computed by
+    // every wave on its own (no barrier): lane l takes splits l, l + 64, ...
+    // (sum: fma in that order), the max over all lanes, the sum folded as
+    // v[l] += v[l + h], h = 32 .. 1
+    float mloc[G], inv[G];
 #pragma unroll
-    for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+    for (int g = 0; g < G; ++g) {
+        const size_t base = (size_t)(kh * G + g) * n_splits;
+        const int l = t & 63;
+        float m = -3.4e38f;
+        for (int s = l; s < n_splits; s += 64) m = fmaxf(m, w.smax[base + s]);
+        m = wave_max64(m);
+        float a = 0.0f;
+        for (int s = l; s < n_splits; s += 64)
+            a = __builtin_fmaf(w.ssum[base + s], expf(w.smax[base + s] - m), a);
+        mloc[g] = m;
+        inv[g] = __fdiv_rn(1.0f, wave_sum64(a));
+    }
+
+    // p for this thread's keys, then its value sums (G heads x 16 dims)
+    float acc[G][16];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int j = j0 + u * 256;
-        const float pj = j < n_keys ? round_bf16(expf(sc[j] - mx) * inv) : 0.0f;
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            float v16[16];
-            decode16(w[u][c], v16);
+        for (int e = 0; e < 16; ++e) acc[g][e] = 0.0f;
 #pragma unroll
-            for (int k = 0; k < 16; ++k) acc[16 * c + k] = __builtin_fmaf(pj, v16[k], acc[16 * c + k]);
+    for (int i = 0; i < 4; ++i) {
+        float v16[16];
+        decode16(vv[i], v16);
+        const bool live = j0 + 32 * i < n_keys;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float pj = live ? round_bf16(expf(sj[i][g] - mloc[g]) * inv[g]) : 0.0f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[g][e] = __builtin_fmaf(pj, v16[e], acc[g][e]);
         }
     }
-    float* dst = partial + ((size_t)m.h * n_splits + m.split) * D;
+    // sum over the wave's 8 key slots
 #pragma unroll
-    for (int d0 = 0; d0 < D; d0 += FOLD) {
-        __syncthreads();
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int i = 0; i < FOLD; ++i) red[t * PAD + i] = acc[d0 + i];
-        __syncthreads();
-        for (int s = 128; s > 0; s >>= 1) {
-            for (int k = t; k < s * FOLD; k += 256) {
-                const int r = k / FOLD, i = k % FOLD;
-                red[r * PAD + i] += red[(r + s) * PAD + i];
-            }
-            __syncthreads();
-        }
-        if (t < FOLD) dst[d0 + t] = red[t];
+        for (int e = 0; e < 16; ++e) acc[g][e] = slots_reduce<false>(acc[g][e]);
+    __shared__ float wsum[4][G][D];
+    if ((t & 63) < 8) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) wsum[wave][g][16 * c + e] = acc[g][e];
+    }
+    __syncthreads();
+    for (int o = t; o < G * D; o += 256) {
+        const int g = o / D, d = o % D;
+        const float r = ((wsum[0][g][d] + wsum[1][g][d]) + wsum[2][g][d]) + wsum[3][g][d];
+        w.partial[((size_t)(kh * G + g) * n_splits + split) * D + d] = r;
     }
 }
 
-__global__ __launch_bounds__(128) void attn_combine_kernel(
-    uint16_t* out, const float* partial, const float* kv_scale, int n_heads, int n_kv, int n_splits)
+__global__ __launch_bounds__(128) void attn_combine_kernel(uint16_t* out, const float* ws,
+                                                           const float* kv_scale, int n_heads,
+                                                           int n_kv, int n_keys, int n_splits)
 {
     const int h = blockIdx.x, d = threadIdx.x;
-    const float* p = partial + (size_t)h * n_splits * 128 + d;
+    const AttnWs w = attn_ws(const_cast<float*>(ws), n_heads, n_keys, n_splits);
+    const float* p = w.partial + (size_t)h * n_splits * 128 + d;
     float v = 0.0f;
-    for (int s = 0; s < n_splits; ++s) v += p[s * 128];
+    int s = 0;
+    for (; s + 8 <= n_splits; s += 8) {      // eight loads in flight, summed in order
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = p[(s + u) * 128];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v += x[u];
+    }
+    for (; s < n_splits; ++s) v += p[s * 128];
     out[(size_t)h * 128 + d] = f32_to_bf16(v * kv_scale[n_kv + h / (n_heads / n_kv)]);
 }
 
@@ -354,38 +496,79 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(uint16_t* out, const uint
     out[i] = f32_to_bf16(s * f32_of_bf16(up[i]));
 }
 
-// One workgroup of 1024 threads: thread t scans i = t, t + 1024, ... keeping
-// the first maximum; then a tree keeps the larger value, or on a tie the
-// lower index.
-__global__ __launch_bounds__(1024) void argmax_bf16_kernel(int32_t* out, const float* logits, int n)
+// argmax over bf16-rounded logits, lowest index on ties, in two kernels:
+// workgroup b of the first takes the kArgChunk logits from b * kArgChunk
+// (thread t: b * kArgChunk + t + 256k, k < 8, in order, keeping the first
+// maximum) and leaves its (value, index) in the workspace; the second
+// reduces those. A pair beats another with a larger value, or an equal one
+// and a lower index (index -1: nothing found, e.g. all NaN); the rule is
+// associative and commutative, so any reduction order gives the same pair.
+constexpr int kArgChunk = 2048;
+
+struct ArgPair {
+    float v;
+    int i;
+};
+
+__device__ __forceinline__ ArgPair arg_better(ArgPair a, ArgPair b)
 {
-    __shared__ float bv[1024];
-    __shared__ int bi[1024];
+    if (b.v > a.v || (b.v == a.v && b.i >= 0 && (a.i < 0 || b.i < a.i))) return b;
+    return a;
+}
+
+__device__ __forceinline__ ArgPair arg_block256(ArgPair p, ArgPair* lds)
+{
+    for (int h = 32; h > 0; h >>= 1) {
+        ArgPair o;
+        o.v = __shfl_xor(p.v, h, 64);
+        o.i = __shfl_xor(p.i, h, 64);
+        p = arg_better(p, o);
+    }
     const int t = threadIdx.x;
-    float best = -3.4e38f;
-    int idx = -1;
-    for (int i = t; i < n; i += 1024) {
-        const float v = round_bf16(logits[i]);
-        if (v > best) { best = v; idx = i; }
-    }
-    bv[t] = best;
-    bi[t] = idx;
+    if ((t & 63) == 0) lds[t >> 6] = p;
     __syncthreads();
-    for (int h = 512; h > 0; h >>= 1) {
-        if (t < h) {
-            const float ov = bv[t + h];
-            const int oi = bi[t + h];
-            if (ov > bv[t] || (ov == bv[t] && oi >= 0 && (bi[t] < 0 || oi < bi[t]))) {
-                bv[t] = ov;
-                bi[t] = oi;
-            }
-        }
-        __syncthreads();
+    return arg_better(arg_better(lds[0], lds[1]), arg_better(lds[2], lds[3]));
+}
+
+__global__ __launch_bounds__(256) void argmax_part_kernel(ArgPair* part, const float* logits, int n)
+{
+    __shared__ ArgPair lds[4];
+    const int base = blockIdx.x * kArgChunk + threadIdx.x;
+    float x[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) x[k] = logits[min(base + 256 * k, n - 1)];
+    ArgPair p{-3.4e38f, -1};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float v = round_bf16(x[k]);
+        if (base + 256 * k < n && v > p.v) p = ArgPair{v, base + 256 * k};
     }
-    if (t == 0) out[0] = bi[0];
+    p = arg_block256(p, lds);
+    if (threadIdx.x == 0) part[blockIdx.x] = p;
+}
+
+__global__ __launch_bounds__(256) void argmax_final_kernel(int32_t* out, const ArgPair* part, int nb)
+{
+    __shared__ ArgPair lds[4];
+    ArgPair p{-3.4e38f, -1};
+    for (int b = threadIdx.x; b < nb; b += 256) p = arg_better(p, part[b]);
+    p = arg_block256(p, lds);
+    if (threadIdx.x == 0) out[0] = p.i;
 }
 
 int status_of(hipError_t e) { return e == hipSuccess ? HEPH_OK : HEPH_ERR_LAUNCH; }
+
+template <int G>
+hipError_t launch_attention(uint16_t* out, const uint16_t* q, const uint8_t* kc, const uint8_t* vc,
+                            const float* kv_scale, int n_kv, int n_keys, float* ws, hipStream_t s)
+{
+    const int splits = (n_keys + kAttnSplit - 1) / kAttnSplit;
+    const int blocks = n_kv * splits;
+    attn_scores_kernel<G><<<blocks, 256, 0, s>>>(ws, q, kc, kv_scale, n_kv, n_keys, splits);
+    attn_pv_kernel<G><<<blocks, 256, 0, s>>>(ws, vc, n_kv, n_keys, splits);
+    attn_combine_kernel<<<n_kv * G, 128, 0, s>>>(out, ws, kv_scale, n_kv * G, n_kv, n_keys, splits);
+    return hipGetLastError();
+}
 
 }  // namespace
 }  // namespace heph
@@ -412,9 +595,18 @@ int heph_rmsnorm(void* out_bf16, const void* in_bf16, const void* gamma_bf16, in
     if (!out_bf16 || !in_bf16 || !gamma_bf16) return HEPH_ERR_NULL;
     if (rows < 1 || cols < 1) return HEPH_ERR_SHAPE;
     if (int st = check_device()) return st;
-    rmsnorm_kernel<<<rows, 256, 0, static_cast<hipStream_t>(stream)>>>(
-        static_cast<uint16_t*>(out_bf16), static_cast<const uint16_t*>(in_bf16),
-        static_cast<const uint16_t*>(gamma_bf16), cols, eps);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint16_t* o = static_cast<uint16_t*>(out_bf16);
+    const uint16_t* x = static_cast<const uint16_t*>(in_bf16);
+    const uint16_t* g = static_cast<const uint16_t*>(gamma_bf16);
+    const int per = (cols + 255) / 256;      // elements per thread
+    if (per <= 1) rmsnorm_kernel<1><<<rows, 256, 0, s>>>(o, x, g, cols, eps);
+    else if (per <= 2) rmsnorm_kernel<2><<<rows, 256, 0, s>>>(o, x, g, cols, eps);
+    else if (per <= 4) rmsnorm_kernel<4><<<rows, 256, 0, s>>>(o, x, g, cols, eps);
+    else if (per <= 10) rmsnorm_kernel<10><<<rows, 256, 0, s>>>(o, x, g, cols, eps);
+    else if (per <= 16) rmsnorm_kernel<16><<<rows, 256, 0, s>>>(o, x, g, cols, eps);
+    else if (per <= 40) rmsnorm_kernel<40><<<rows, 256, 0, s>>>(o, x, g, cols, eps);
+    else rmsnorm_kernel<0><<<rows, 256, 0, s>>>(o, x, g, cols, eps);
     return status_of(hipGetLastError());
 }
 
@@ -440,8 +632,9 @@ size_t heph_attention_ws_bytes(int n_heads, int n_keys)
 {
     if (n_heads < 1 || n_keys < 1) return 0;
     const size_t splits = (size_t)(n_keys + kAttnSplit - 1) / kAttnSplit;
-    return 4 * (size_t)n_heads * ((size_t)n_keys + splits * 128);
+    return 4 * (size_t)n_heads * ((size_t)n_keys + splits * (2 + 128));
 }
+
 
 int heph_attention_fp8kv(void* out_bf16, const void* q_bf16, const uint8_t* k_cache,
                          const uint8_t* v_cache, const float* kv_scale, int n_heads,
@@ -452,24 +645,25 @@ int heph_attention_fp8kv(void* out_bf16, const void* q_bf16, const uint8_t* k_ca
     if (head_dim != 128 || n_kv_heads < 1 || n_heads < n_kv_heads || n_heads % n_kv_heads ||
         n_keys < 1 || n_keys > HEPH_ATTN_MAX_KEYS)
         return HEPH_ERR_SHAPE;
+    const int G = n_heads / n_kv_heads;
+    if (G != 1 && G != 2 && G != 4 && G != 8) return HEPH_ERR_SHAPE;
     if (ws_bytes < heph_attention_ws_bytes(n_heads, n_keys)) return HEPH_ERR_WORKSPACE;
     if (reinterpret_cast<uintptr_t>(k_cache) % 16 || reinterpret_cast<uintptr_t>(v_cache) % 16 ||
         reinterpret_cast<uintptr_t>(q_bf16) % 16 || reinterpret_cast<uintptr_t>(ws) % 16)
         return HEPH_ERR_ALIGN;
     if (int st = check_device()) return st;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const int splits = (n_keys + kAttnSplit - 1) / kAttnSplit;
-    float* scores = static_cast<float*>(ws);
-    float* partial = scores + (size_t)n_heads * n_keys;
-    const int blocks = n_heads * splits;
-    attn_scores_kernel<<<blocks, 256, 0, s>>>(scores, static_cast<const uint16_t*>(q_bf16),
-                                              k_cache, kv_scale, n_heads, n_kv_heads, n_keys,
-                                              splits);
-    attn_pv_kernel<<<blocks, 256, 0, s>>>(partial, scores, v_cache, n_heads, n_kv_heads, n_keys,
-                                          splits);
-    attn_combine_kernel<<<n_heads, 128, 0, s>>>(static_cast<uint16_t*>(out_bf16), partial,
-                                                kv_scale, n_heads, n_kv_heads, splits);
-    return status_of(hipGetLastError());
+    uint16_t* out = static_cast<uint16_t*>(out_bf16);
+    const uint16_t* q = static_cast<const uint16_t*>(q_bf16);
+    float* w = static_cast<float*>(ws);
+    hipError_t e;
+    switch (G) {
+    case 1: e = launch_attention<1>(out, q, k_cache, v_cache, kv_scale, n_kv_heads, n_keys, w, s); break;
+    case 2: e = launch_attention<2>(out, q, k_cache, v_cache, kv_scale, n_kv_heads, n_keys, w, s); break;
+    case 4: e = launch_attention<4>(out, q, k_cache, v_cache, kv_scale, n_kv_heads, n_keys, w, s); break;
+    default: e = launch_attention<8>(out, q, k_cache, v_cache, kv_scale, n_kv_heads, n_keys, w, s); break;
+    }
+    return status_of(e);
 }
 
 int heph_silu_mul(void* out_bf16, const void* gate_bf16, const void* up_bf16, int n, void* stream)
@@ -483,12 +677,25 @@ int heph_silu_mul(void* out_bf16, const void* gate_bf16, const void* up_bf16, in
     return status_of(hipGetLastError());
 }
 
-int heph_argmax_bf16(int32_t* out_idx, const float* logits, int n, void* stream)
+size_t heph_argmax_ws_bytes(int n)
 {
-    if (!out_idx || !logits) return HEPH_ERR_NULL;
+    if (n < 1) return 0;
+    return sizeof(ArgPair) * (size_t)((n + kArgChunk - 1) / kArgChunk);
+}
+
+int heph_argmax_bf16(int32_t* out_idx, const float* logits, int n, void* ws, size_t ws_bytes,
+                     void* stream)
+{
+    if (!out_idx || !logits || !ws) return HEPH_ERR_NULL;
     if (n < 1) return HEPH_ERR_SHAPE;
+    if (ws_bytes < heph_argmax_ws_bytes(n)) return HEPH_ERR_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(ws) % 8) return HEPH_ERR_ALIGN;
     if (int st = check_device()) return st;
-    argmax_bf16_kernel<<<1, 1024, 0, static_cast<hipStream_t>(stream)>>>(out_idx, logits, n);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int nb = (n + kArgChunk - 1) / kArgChunk;
+    ArgPair* part = static_cast<ArgPair*>(ws);
+    argmax_part_kernel<<<nb, 256, 0, s>>>(part, logits, n);
+    argmax_final_kernel<<<1, 256, 0, s>>>(out_idx, part, nb);
     return status_of(hipGetLastError());
 }
 

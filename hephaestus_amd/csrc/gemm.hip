@@ -346,6 +346,9 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     // DMA instruction `part` (0..8) of this wave for chunk j into stage
     // buf: parts 0-3 move A rows, 4-7 B rows, 8 the row scales.
     constexpr int kParts = 9;
+    // DMA parts per row tile (MI355X: 2 over the first five of 8 row tiles,
+    // 3 over the first three of 6 or 4, fewest cycles per chunk)
+    constexpr int kPer = L_MT >= 8 ? 2 : 3;
     auto issue_part = [&](int j, auto bufc, int part) {
         constexpr int buf = decltype(bufc)::value;
         uint8_t* st = smem + buf * L_STAGE;
@@ -409,9 +412,11 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     };
 
     // One 128-wide chunk j held in stage buf (a compile-time constant). The
-    // wave's nine DMA instructions for chunk j + 1 are spread over the row
-    // tiles: issued together right after the barrier, the DMAs of all eight
-    // waves stall every wave's instruction issue.
+    // wave's nine DMA instructions for chunk j + 1 go out kPer per row tile
+    // from the first tile on: issued together right after the barrier, the
+    // DMAs of all eight waves stall every wave's instruction issue; spread
+    // to the last tile, the late ones are still in flight at the next
+    // chunk's wait (MI355X: ~350 of ~3100 cycles a chunk).
     auto chunk = [&](auto bufc, int j) {
         constexpr int buf = decltype(bufc)::value;
         wait_dma();
@@ -444,7 +449,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
             if (more) {
 #pragma unroll
                 for (int part = 0; part < kParts; ++part)
-                    if (part * L_MT / kParts == mi) issue_part(j + 1, ic<buf ^ 1>{}, part);
+                    if (part / kPer == mi) issue_part(j + 1, ic<buf ^ 1>{}, part);
             }
             if constexpr (SM == 2) {
 #pragma unroll
@@ -673,21 +678,33 @@ hipError_t launch_big(const Fp8Operands& op, hipStream_t stream, const LaunchTim
 
 }  // namespace
 
+// Measured cost of one 128-wide chunk per tile height (MI355X shader
+// cycles per wave and chunk at M = 4096, random E4M3 data): a taller tile
+// does more MFMA work per chunk, a shorter one fills the CUs in finer steps.
+struct TileCost {
+    int bm;
+    long cycles;
+};
+constexpr TileCost kTileCost[] = {{256, 2980}, {192, 2400}, {128, 2150}};
+
+long chunk_cycles(int bm)
+{
+    for (const auto& tc : kTileCost)
+        if (tc.bm == bm) return tc.cycles;
+    return kTileCost[0].cycles;
+}
+
 // Tile height of the large-M kernel: the one with the least estimated time,
 // rounds of tiles over the CUs (one 512-thread workgroup per CU) times the
-// measured cost of one 128-wide chunk at that height (MI355X shader cycles
-// per chunk at M = 4096: 2990 for 256 rows, 2480 for 192, 2240 for 128 --
-// a taller tile does more MFMA work per chunk, a shorter one fills the CUs
-// in finer steps). The taller tile wins a tie.
+// chunk cost at that height. The taller tile wins a tie.
 int gemm_tile_m(int M, int N)
 {
     const int forced = g_tune_bm.load(std::memory_order_relaxed);
     if (forced >= 128) return forced;
     const long cus = cu_count();
-    struct { int bm; long cycles; } const tiles_cost[] = {{256, 2990}, {192, 2480}, {128, 2240}};
     int best = 256;
     long best_t = -1;
-    for (const auto& tc : tiles_cost) {
+    for (const auto& tc : kTileCost) {
         const long tiles = (long)((M + tc.bm - 1) / tc.bm) * ((N + L_BN - 1) / L_BN);
         const long t = (tiles + cus - 1) / cus * tc.cycles;
         if (best_t < 0 || t < best_t) {
@@ -702,8 +719,8 @@ void gemm_tune(int bm) { g_tune_bm.store(bm, std::memory_order_relaxed); }
 
 // K splits of the large-M GEMM: the count with the least estimated time,
 // rounds of (tile, split) workgroups over the CUs times the chunks of a
-// split times the per-chunk cost of the tile height (MI355X: about 1.2 us
-// at 128 rows), plus, when split, the reduction: about 8 us of extra
+// split times the per-chunk cost of the tile height (at ~1.9 GHz: about
+// 1.1 us at 128 rows), plus, when split, the reduction: about 8 us of extra
 // launch and per-workgroup set-up, and the partials (M*N*4 bytes a split)
 // read back at about 5 TB/s. At most 8 splits of at least 4 chunks. So M =
 // 512 splits o_proj and down (N = 2560: 40 tiles) 6 ways and leaves qkv
@@ -714,7 +731,7 @@ int gemm_splits(int M, int N, int K)
     const long tiles = (long)((M + bm - 1) / bm) * ((N + L_BN - 1) / L_BN);
     const long cus = cu_count();
     const int KC = K / kChunk;
-    const double chunk_us = (bm == 256 ? 2990.0 : bm == 192 ? 2480.0 : 2240.0) / 1900.0;
+    const double chunk_us = (double)chunk_cycles(bm) / 1900.0;
     int best = 1;
     double best_t = 0.0;
     for (int s = 1; s <= 8; ++s) {

@@ -82,8 +82,16 @@ def silu_mul(out, gate, up, n: int) -> None:
     _call("heph_silu_mul", _ptr(out), _ptr(gate), _ptr(up), n, _stream())
 
 
-def argmax_bf16(out_idx, logits) -> None:
-    _call("heph_argmax_bf16", _ptr(out_idx), _ptr(logits), logits.numel(), _stream())
+def argmax_ws(n: int, device="cuda") -> torch.Tensor:
+    """Scratch for argmax_bf16 over n logits."""
+    return torch.empty(max(L.lib().heph_argmax_ws_bytes(n), 16), dtype=torch.uint8, device=device)
+
+
+def argmax_bf16(out_idx, logits, ws: torch.Tensor | None = None) -> None:
+    if ws is None:
+        ws = argmax_ws(logits.numel(), device=logits.device)
+    _call("heph_argmax_bf16", _ptr(out_idx), _ptr(logits), logits.numel(), _ptr(ws), ws.numel(),
+          _stream())
 
 
 # ---------------------------------------------------------------- weights ----
@@ -180,6 +188,7 @@ class Qwen3Decoder:
         self.token = torch.zeros(1, dtype=torch.int32, device=dev)
         self.q_ws, self.s_ws = HK.workspace(1, max(H, Q, I), device=dev)
         self.attn_ws = attention_ws(cfg.n_heads, kv.max_ctx, device=dev)
+        self.arg_ws = argmax_ws(cfg.vocab, device=dev)
 
     def _linear(self, c, a, fw: Fp8Weight, K: int, residual: bool = False):
         fn = HK.linear_add_residual_fp8 if residual else HK.linear_fp8
@@ -238,7 +247,7 @@ class Qwen3Decoder:
         rec(-1, "final_norm", self.xn)
         self._linear(self.logits, self.xn, w.embed, H)
         rec(-1, "logits", self.logits)
-        argmax_bf16(self.next_token, self.logits)
+        argmax_bf16(self.next_token, self.logits, self.arg_ws)
         rec(-1, "argmax", self.next_token)
         return self.next_token
 

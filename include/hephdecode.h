@@ -57,9 +57,11 @@ int heph_qk_norm_rope_kv(void* qkv_bf16, const void* q_gamma, const void* k_gamm
  * One query token over n_keys cached keys: out[h] = sum_j p_j * v_j with
  * p = bf16(softmax(q.k_j * sk / sqrt(128))), K and V E4M3 codes
  * [n_keys, n_kv_heads, 128] scaled by kv_scale (K entries, then V).
+ * n_heads / n_kv_heads (query heads per kv head) must be 1, 2, 4 or 8.
  * ws: device scratch of heph_attention_ws_bytes(n_heads, n_keys) bytes
- * (scores and per-split sums), 16-byte aligned. Replaces attention
- * (src/hephaestus/kernels.mojo:923-1035, :1183-1240).
+ * (scores, and per 128-key split the max, sum and value sums), 16-byte
+ * aligned. Replaces attention (src/hephaestus/kernels.mojo:923-1035,
+ * :1183-1240).
  */
 size_t heph_attention_ws_bytes(int n_heads, int n_keys);
 int heph_attention_fp8kv(void* out_bf16, const void* q_bf16, const uint8_t* k_cache,
@@ -75,10 +77,14 @@ int heph_silu_mul(void* out_bf16, const void* gate_bf16, const void* up_bf16, in
                   void* stream);
 
 /*
- * out_idx[0] = argmax_i bf16(logits[i]), lowest index on ties. Replaces
- * argmax_logits (src/hephaestus/kernels.mojo:1376-1463).
+ * out_idx[0] = argmax_i bf16(logits[i]), lowest index on ties (-1 when no
+ * logit compares above -3.4e38, e.g. all NaN). ws: device scratch of
+ * heph_argmax_ws_bytes(n) bytes, 8-byte aligned (one (value, index) pair per
+ * 2048 logits). Replaces argmax_logits (src/hephaestus/kernels.mojo:1376-1463).
  */
-int heph_argmax_bf16(int32_t* out_idx, const float* logits, int n, void* stream);
+size_t heph_argmax_ws_bytes(int n);
+int heph_argmax_bf16(int32_t* out_idx, const float* logits, int n, void* ws, size_t ws_bytes,
+                     void* stream);
 
 #ifdef __cplusplus
 }

@@ -11,8 +11,10 @@
  *   embed          src/hephaestus/kernels.mojo:530-548
  *   rmsnorm        HF Qwen3RMSNorm as the engine calls it, forward.mojo:45-81
  *   qk_norm_rope   forward.mojo:474-500, rope kernels.mojo:709-762
- *   attention      kernels.mojo:923-1035 (fp32 scores, bf16 probabilities),
- *                  value sums in splits of 512 keys as decode.hip runs them
+ *   attention      kernels.mojo:923-1035 (fp32 scores, bf16 probabilities
+ *                  from the global max and sum), reductions split over
+ *                  128-key blocks as decode.hip runs them (the sum of
+ *                  exponentials as split sums rescaled to the global max)
  *   silu_mul       kernels.mojo:1243-1255
  *   argmax         kernels.mojo:1376-1433 (bf16 logits, lowest index on ties)
  */
@@ -129,63 +131,103 @@ void heph_oracle_qk_norm_rope_kv(uint16_t* qkv, const uint16_t* q_gamma, const u
     }
 }
 
+/* 32 key-slot values a[ks] summed as the attention kernels do: per group
+ * of 8 slots ((a0+a1)+(a2+a3)) + ((a4+a5)+(a6+a7)), the four groups in order. */
+static float slots4(const float* a)
+{
+    float wv[4];
+    for (int w = 0; w < 4; ++w) {
+        const float* b = a + 8 * w;
+        wv[w] = ((b[0] + b[1]) + (b[2] + b[3])) + ((b[4] + b[5]) + (b[6] + b[7]));
+    }
+    return ((wv[0] + wv[1]) + wv[2]) + wv[3];
+}
+
 int heph_oracle_attention_fp8kv(uint16_t* out, const uint16_t* q, const uint8_t* kc,
                                 const uint8_t* vc, const float* kv_scale, int n_heads, int n_kv,
                                 int n_keys)
 {
-    enum { D = 128 };
-    float* p = malloc(sizeof(float) * (size_t)n_keys);
-    float* pv = malloc(sizeof(float) * 256 * D);
-    if (!p || !pv) {
-        free(p);
-        free(pv);
+    /* Splits of 128 keys; key j = 128*split + ks + 32*i (key slot ks < 32,
+     * i < 4). Orders (decode.hip runs the same):
+     *   score: per 16-dim chunk c an fma chain over its dims, then
+     *          ((c0+c1)+(c2+c3)) + ((c4+c5)+(c6+c7)), times sk/sqrt(128)
+     *   split: m_s = max; l_s = slots4 over ks of (sum over i of exp(s - m_s))
+     *   total: m = max m_s; sum = fold64 of per-slot fma sums of
+     *          l_s * exp(m_s - m) (slot = split mod 64); p = bf16(exp(s - m)/sum)
+     *   values: per split and dim, a_ks = fma chain over i, slots4 over ks;
+     *          splits summed in order; times sv, bf16 */
+    enum { D = 128, SPLIT = 128 };
+    const int NS = (n_keys + SPLIT - 1) / SPLIT;
+    float* sc = malloc(sizeof(float) * (size_t)n_keys);
+    float* ms = malloc(sizeof(float) * (size_t)NS);
+    float* ls = malloc(sizeof(float) * (size_t)NS);
+    if (!sc || !ms || !ls) {
+        free(sc);
+        free(ms);
+        free(ls);
         return -1;
     }
     float dec[256];
     for (int c = 0; c < 256; ++c) dec[c] = heph_oracle_e4m3_decode((uint8_t)c);
     const size_t row = (size_t)n_kv * D;
+    const int G = n_heads / n_kv;
     for (int h = 0; h < n_heads; ++h) {
-        const int kh = h / (n_heads / n_kv);
+        const int kh = h / G;
         float qs[D];
         for (int d = 0; d < D; ++d) qs[d] = bf(q[(size_t)h * D + d]);
         const float qk_scale = kv_scale[kh] * 0.08838834764831845f;
-        float mx = -3.4e38f;
         for (int j = 0; j < n_keys; ++j) {
             const uint8_t* k = kc + j * row + kh * D;
-            float dot = 0.0f;
-            for (int d = 0; d < D; ++d) dot = fmaf(qs[d], dec[k[d]], dot);
-            p[j] = dot * qk_scale;
-            if (p[j] > mx) mx = p[j];
+            float pc[8];
+            for (int c = 0; c < 8; ++c) {
+                float part = 0.0f;
+                for (int e = 0; e < 16; ++e) part = fmaf(qs[16 * c + e], dec[k[16 * c + e]], part);
+                pc[c] = part;
+            }
+            const float s = ((pc[0] + pc[1]) + (pc[2] + pc[3])) + ((pc[4] + pc[5]) + (pc[6] + pc[7]));
+            sc[j] = s * qk_scale;
         }
-        float part[256];
-        for (int t = 0; t < 256; ++t) part[t] = 0.0f;
-        for (int j = 0; j < n_keys; ++j) {
-            p[j] = expf(p[j] - mx);
-            part[j & 255] += p[j];
+        float m = -3.4e38f;
+        for (int sp = 0; sp < NS; ++sp) {
+            float mx = -3.4e38f;
+            for (int j = sp * SPLIT; j < n_keys && j < (sp + 1) * SPLIT; ++j) mx = fmaxf(mx, sc[j]);
+            float a[32];
+            for (int ks = 0; ks < 32; ++ks) {
+                a[ks] = 0.0f;
+                for (int i = 0; i < 4; ++i) {
+                    const int j = sp * SPLIT + ks + 32 * i;
+                    if (j < n_keys) a[ks] += expf(sc[j] - mx);
+                }
+            }
+            ms[sp] = mx;
+            ls[sp] = slots4(a);
+            m = fmaxf(m, mx);
         }
-        const float inv = 1.0f / fold(part, 256);
-        for (int j = 0; j < n_keys; ++j) p[j] = rb(p[j] * inv);
-        /* PV over splits of 512 keys: per split, per-thread sums over the
-         * split's keys j = t, t + 256 (in order) folded across the 256
-         * threads; then the split results summed in split order */
+        float part[64];
+        for (int t = 0; t < 64; ++t) part[t] = 0.0f;
+        for (int sp = 0; sp < NS; ++sp) part[sp & 63] = fmaf(ls[sp], expf(ms[sp] - m), part[sp & 63]);
+        const float inv = 1.0f / fold(part, 64);
+        for (int j = 0; j < n_keys; ++j) sc[j] = rb(expf(sc[j] - m) * inv);
         float tot[D];
         for (int d = 0; d < D; ++d) tot[d] = 0.0f;
-        for (int j0 = 0; j0 < n_keys; j0 += 512) {
-            memset(pv, 0, sizeof(float) * 256 * D);
-            for (int j = j0; j < n_keys && j < j0 + 512; ++j) {
-                const uint8_t* v = vc + j * row + kh * D;
-                float* acc = pv + (size_t)((j - j0) & 255) * D;
-                for (int d = 0; d < D; ++d) acc[d] = fmaf(p[j], dec[v[d]], acc[d]);
-            }
+        for (int sp = 0; sp < NS; ++sp) {
             for (int d = 0; d < D; ++d) {
-                for (int t = 0; t < 256; ++t) part[t] = pv[(size_t)t * D + d];
-                tot[d] += fold(part, 256);
+                float a[32];
+                for (int ks = 0; ks < 32; ++ks) {
+                    a[ks] = 0.0f;
+                    for (int i = 0; i < 4; ++i) {
+                        const int j = sp * SPLIT + ks + 32 * i;
+                        if (j < n_keys) a[ks] = fmaf(sc[j], dec[vc[j * row + kh * D + d]], a[ks]);
+                    }
+                }
+                tot[d] += slots4(a);
             }
         }
         for (int d = 0; d < D; ++d) out[(size_t)h * D + d] = tob(tot[d] * kv_scale[n_kv + kh]);
     }
-    free(p);
-    free(pv);
+    free(sc);
+    free(ms);
+    free(ls);
     return 0;
 }
 

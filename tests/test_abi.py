@@ -162,7 +162,11 @@ def test_decode_ops_reject(lib):
     assert q(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 30, 8, 128, 0, 1e6, 1e-6, None) == L.HEPH_ERR_SHAPE
     a = lib.heph_attention_fp8kv
     ws = lib.heph_attention_ws_bytes(32, 4097)
-    assert ws == 4 * 32 * (4097 + 9 * 128)
+    # scores, then per 128-key split: max, sum and 128 value sums per head
+    assert ws == 4 * 32 * (4097 + 33 * (2 + 128))
+    # query heads per kv head: 1, 2, 4 or 8
+    assert a(FAKE, FAKE, FAKE, FAKE, FAKE, 24, 8, 128, 10, FAKE, ws, None) == L.HEPH_ERR_SHAPE
+    assert a(FAKE, FAKE, FAKE, FAKE, FAKE, 32, 2, 128, 10, FAKE, ws, None) == L.HEPH_ERR_SHAPE
     assert a(FAKE, FAKE, FAKE, FAKE, FAKE, 32, 8, 128, L.ATTN_MAX_KEYS + 1, FAKE, 1 << 40,
              None) == L.HEPH_ERR_SHAPE
     assert a(FAKE, FAKE, FAKE, FAKE, FAKE, 32, 8, 128, 0, FAKE, ws, None) == L.HEPH_ERR_SHAPE
@@ -171,4 +175,9 @@ def test_decode_ops_reject(lib):
         L.HEPH_ERR_WORKSPACE
     assert a(FAKE, FAKE, ODD, FAKE, FAKE, 32, 8, 128, 10, FAKE, ws, None) == L.HEPH_ERR_ALIGN
     assert lib.heph_silu_mul(FAKE, FAKE, FAKE, 0, None) == L.HEPH_ERR_SHAPE
-    assert lib.heph_argmax_bf16(None, FAKE, 10, None) == L.HEPH_ERR_NULL
+    aw = lib.heph_argmax_ws_bytes(151936)
+    assert aw == 8 * 75                              # one (value, index) per 2048 logits
+    assert lib.heph_argmax_bf16(None, FAKE, 10, FAKE, aw, None) == L.HEPH_ERR_NULL
+    assert lib.heph_argmax_bf16(FAKE, FAKE, 10, None, aw, None) == L.HEPH_ERR_NULL
+    assert lib.heph_argmax_bf16(FAKE, FAKE, 0, FAKE, aw, None) == L.HEPH_ERR_SHAPE
+    assert lib.heph_argmax_bf16(FAKE, FAKE, 151936, FAKE, aw - 8, None) == L.HEPH_ERR_WORKSPACE
