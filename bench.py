@@ -84,6 +84,9 @@ def parse():
     ap.add_argument("--prefill-pass", action="store_true",
                     help="only run the configs[3] M = 4096 prefill launches eagerly (quant + "
                          "GEMM, 10 per shape, for rocprofv3 traces); prints no JSON")
+    ap.add_argument("--decode-pass", action="store_true",
+                    help="only run configs[4] decode steps eagerly (random-init Qwen3-4B, "
+                         "4096 cached tokens; for rocprofv3 traces); prints no JSON")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="only run the M = 1 launches eagerly plus a 256 MiB device "
                          "copy (for rocprofv3 --pmc traffic counts); prints no JSON")
@@ -109,6 +112,25 @@ def prefill_pass(steps):
         print(f"prefill-pass {name} M={M} N={N} K={K} kernel={HK.last_kernel()} "
               f"launches={100 + steps} (the last {steps} are the measured ones)", flush=True)
         del lin
+
+
+def decode_pass(steps):
+    """`steps` eager decode steps at position 4096 after two
+    warm-up steps, each step ending in a device synchronization."""
+    import torch
+    from hephaestus_amd import decode as DEC
+    from hephaestus_amd.loader import Qwen3Config
+    torch.cuda.set_device(0)
+    cfg = Qwen3Config()
+    w = DEC.random_init(cfg, seed=4)
+    kv = DEC.KVCache(cfg, 4097)
+    kv.fill_synthetic(4096, seed=5)
+    dec = DEC.Qwen3Decoder(w, kv)
+    for i in range(2 + steps):
+        dec.step(12345, 4096)
+        torch.cuda.synchronize()
+    print(f"decode-pass steps={2 + steps} (the last {steps} are the measured ones) "
+          f"argmax={int(dec.next_token.item())}", flush=True)
 
 
 def pmc_pass(steps):
@@ -193,6 +215,9 @@ def main():
         return
     if args.prefill_pass:
         prefill_pass(max(1, min(args.steps, 20)))
+        return
+    if args.decode_pass:
+        decode_pass(max(1, min(args.steps, 20)))
         return
     import torch
     from hephaestus_amd import kernels as HK
