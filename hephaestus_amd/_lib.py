@@ -44,6 +44,7 @@ TUNE_GEMV_KS = 3
 TUNE_GEMV_WAVES = 4
 TUNE_GEMV_U = 5
 TUNE_GEMM_BM = 6
+TUNE_BATCH_SPLIT = 7
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int

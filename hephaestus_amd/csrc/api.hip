@@ -81,7 +81,9 @@ size_t heph_fp8_linear_ws_bytes(int M, int N, int K)
     if (M < 1 || N < 1 || K < 1) return 0;
     const size_t q = ((size_t)M * (size_t)K + 255) & ~(size_t)255;
     if (check_device() != HEPH_OK) return q;
-    return q + gemm_split_bytes(M, N, K);
+    const size_t g = gemm_split_bytes(M, N, K);
+    const size_t b = M <= HEPH_SKINNY_MAX_M ? gemv_split_bytes(M, N, K) : 0;
+    return q + (g > b ? g : b);
 }
 
 size_t heph_fp8_s_ws_floats(int M, int K, int group_k)
@@ -169,17 +171,24 @@ int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
     }
 
     // M <= 32 takes the chunk-slot GEMV unless a kernel is forced; the
-    // skinny kernel serves FORCE_SKINNY (cross-kernel checks) only. At
-    // 16 < M <= 32 (two 16-row tiles in the GEMV) quantizer + K-split GEMM
-    // is faster on large weights when the caller's scratch allows the split
-    // (MI355X at 19456 x 2560: 19 vs 24-26 us at M = 24 and 32; at the
-    // smaller config shapes the two are within 10% and the GEMV stays).
+    // skinny kernel serves FORCE_SKINNY (cross-kernel checks) only. Batched
+    // decode (gemv_split_routes: larger M, 1x128 groups) takes quantizer +
+    // the 64-column K-split kernel when the caller's scratch holds its
+    // partials; otherwise, at 16 < M <= 32 (two 16-row tiles in the GEMV),
+    // quantizer + K-split GEMM on large weights when scratch allows.
     const bool skinny = flags & HEPH_FLAG_FORCE_SKINNY;
-    const bool split_gemm = M > 16 && (long)N * K >= (32L << 20) && gemm_splits_ready(op);
-    const bool gemv = !skinny && !(flags & HEPH_FLAG_FORCE_GEMM) && M <= HEPH_SKINNY_MAX_M &&
-                      !split_gemm;
+    const bool forced_gemm = flags & HEPH_FLAG_FORCE_GEMM;
+    const int bmode = gemv_split_mode();
+    const bool batch_split = !skinny && !forced_gemm && M <= HEPH_SKINNY_MAX_M &&
+                             group_k == kChunk && bmode >= 0 &&
+                             (bmode > 0 || gemv_split_routes(M, N, K)) && gemv_split_ready(op);
+    const bool split_gemm = !batch_split && M > 16 && (long)N * K >= (32L << 20) &&
+                            gemm_splits_ready(op);
+    const bool gemv = !skinny && !forced_gemm && M <= HEPH_SKINNY_MAX_M && !split_gemm &&
+                      !batch_split;
     const bool fuse_ok = !skip_quant && !(flags & HEPH_FLAG_NO_FUSE) && group_k == kChunk;
-    const bool fused = fuse_ok && ((gemv && gemv_fuses(M, N, K)) || (skinny && M <= kFusedMaxM));
+    const bool fused = fuse_ok && (batch_split || (gemv && gemv_fuses(M, N, K)) ||
+                                   (skinny && M <= kFusedMaxM));
     LaunchTiming t = take_timing();
     if (!skip_quant && !fused) {
         // A timed call spans both kernels: the quantizer carries the start
@@ -190,7 +199,8 @@ int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
         t.start = nullptr;
     }
     hipError_t e;
-    if (gemv) e = launch_fp8_gemv(op, fused, s, t, &g_last_kernel);
+    if (batch_split) e = launch_fp8_gemv_split(op, fused, s, t, &g_last_kernel);
+    else if (gemv) e = launch_fp8_gemv(op, fused, s, t, &g_last_kernel);
     else if (skinny) e = launch_fp8_skinny(op, fused, s, t, &g_last_kernel);
     else e = launch_fp8_gemm(op, s, t, &g_last_kernel);
     return launch_status(e);
@@ -275,6 +285,10 @@ int heph_set_tuning(int knob, int value)
         if (value != 0 && value != 1 && value != 128 && value != 192 && value != 256)
             return HEPH_ERR_FLAGS;
         gemm_tune(value);
+        return HEPH_OK;
+    case HEPH_TUNE_BATCH_SPLIT:
+        if (value < -1 || value > 64) return HEPH_ERR_FLAGS;
+        gemv_split_tune(value);
         return HEPH_OK;
     default: return HEPH_ERR_FLAGS;
     }

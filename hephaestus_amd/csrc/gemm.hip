@@ -630,6 +630,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(Fp8Operands op)
     }
 }
 
+hipError_t launch_splitk_reduce(const Fp8Operands& op, hipStream_t stream, const LaunchTiming& t)
+{
+    const size_t n4 = (size_t)op.M * op.N / 4;
+    const int blocks = (int)std::min<size_t>((n4 + 255) / 256, 4096);
+    return launch(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, t, op);
+}
+
 namespace {
 
 std::atomic<int> g_tune_bm{0};
@@ -664,10 +671,7 @@ hipError_t launch_big(const Fp8Operands& op, hipStream_t stream, const LaunchTim
             e = launch(fp8_gemm256_kernel<1, BM>, grid, dim3(512), 0, stream,
                        LaunchTiming{t.start, nullptr}, op);
         if (e != hipSuccess) return e;
-        const size_t n4 = (size_t)op.M * op.N / 4;
-        const int blocks = (int)std::min<size_t>((n4 + 255) / 256, 4096);
-        return launch(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream,
-                      LaunchTiming{nullptr, t.stop}, op);
+        return launch_splitk_reduce(op, stream, LaunchTiming{nullptr, t.stop});
     }
     if (op.w_block)
         return launch(fp8_gemm256_kernel<0, BM>, grid, dim3(512), 0, stream, t, op);

@@ -1,0 +1,299 @@
+// gemv_split.hip - W8A8 FP8 linear for batched decode (12 <= M <= 32) as a
+// 64-column K-split kernel.
+//
+// Replaces the reference's small-M kernel (src/hephaestus/wmma_gfx12.mojo:
+// 900-1019, reached through linear_fp8, kernels.mojo:410-470) at the batch
+// sizes where the chunk-slot GEMV's 16-column workgroups re-read the whole
+// activation matrix for every 16 output columns: at M = 32 that is four
+// times the weight bytes each workgroup streams. Here a workgroup covers 64
+// columns and at most 8 K chunks, so the activation bytes it reads are a
+// fraction of its weight bytes, and the K splits supply the workgroups that
+// a 64-column grid alone would not (N = 2560: 40 tiles).
+//   * workgroup b takes column tile b % tiles_n and chunks [s*KC/S,
+//     (s+1)*KC/S) of split s = b / tiles_n; wave w its 16 columns
+//     n0 + 16w .. +15, whose weight fragments for every chunk of the split
+//     are loaded first (two 16-byte loads per lane and chunk, all in
+//     flight at once);
+//   * meanwhile the workgroup stages its activation slice in LDS: fused,
+//     eight lanes per 1x128 group load 16 bf16 each, take the group amax
+//     (bf16 magnitude bits, NaN skipped, DPP across the 8 lanes) and the
+//     division-free group scale, and write one 16-byte code piece each;
+//     column tile 0 also writes the codes and scales to the workspace.
+//     Otherwise the codes and scales are copied from the workspace. Rows of
+//     128 bytes, piece index XORed with the row's low bits;
+//   * per chunk and 16-row tile one v_mfma_f32_16x16x128_f8f6f4 with the
+//     weights as the first operand: lane (r, g) (r = lane & 15,
+//     g = lane >> 4) holds C[column 4g+e][activation row r], so it needs
+//     one activation scale per tile and chunk; acc += p * (sa * sw), the
+//     association of the other kernels of this library;
+//   * one split: bf16/f32 output (plus the residual) directly, four
+//     columns per lane; S splits: fp32 partials [split][M][N] in the
+//     caller's scratch, summed in split order by the large-M GEMM's
+//     reduction kernel.
+#include <atomic>
+
+#include "heph_kernels.h"
+
+namespace heph {
+
+namespace {
+
+constexpr int kSplitCols = 64;     // output columns per workgroup (4 waves x 16)
+constexpr int kSplitMaxKB = 8;     // chunks per split at most
+
+std::atomic<int> g_tune_split{0};
+}  // namespace
+
+// Max over each aligned run of 8 lanes (unsigned), left in all 8.
+__device__ __forceinline__ uint32_t max8_lanes(uint32_t m)
+{
+    m = max(m, (uint32_t)__builtin_amdgcn_mov_dpp((int)m, 0xB1, 0xf, 0xf, false));   // l ^ 1
+    m = max(m, (uint32_t)__builtin_amdgcn_mov_dpp((int)m, 0x4E, 0xf, 0xf, false));   // l ^ 2
+    m = max(m, (uint32_t)__builtin_amdgcn_mov_dpp((int)m, 0x141, 0xf, 0xf, false));  // 7 - l
+    return m;
+}
+
+// Byte offset of 16-byte piece p (0..7) of activation row r (0..31) of
+// chunk c in the LDS code tile: rows of 128 bytes, the piece index XORed
+// with r & 7 so that the 16 rows a fragment read touches fall in
+// different banks.
+__device__ __forceinline__ int code_off(int c, int r, int p)
+{
+    return ((c * 32 + r) * 8 + (p ^ (r & 7))) * 16;
+}
+
+// MT: 16-row tiles (1: M <= 16, 2: M <= 32). SM: 0 = 128x128 weight
+// blocks, 1 = per-channel weights (both with per-chunk activation scales).
+// FUSED: quantize the bf16 activations of the workgroup's chunks into LDS
+// (workgroups of column tile 0 also write the codes and scales to the
+// workspace); otherwise copy the codes and scales from the workspace.
+template <int MT, int SM, bool FUSED>
+__global__ __launch_bounds__(256) void fp8_gemv_split_kernel(Fp8Operands op)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t codes[kSplitMaxKB * 32 * kChunk];
+    __shared__ float sa_lds[kSplitMaxKB][32];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int M = op.M, N = op.N, K = op.K, KC = K >> 7;
+    const int tiles_n = (N + kSplitCols - 1) / kSplitCols;
+    const int S = op.splits;
+    const int tn = blockIdx.x % tiles_n, split = blockIdx.x / tiles_n;
+    const int jb = split * KC / S, je = (split + 1) * KC / S, KB = je - jb;   // 1 <= KB <= 8
+    const int n0 = tn * kSplitCols + wave * 16;                   // this wave's 16 columns
+
+    // 1. this wave's weight fragments for all KB chunks (rows past N re-read
+    //    row N-1 and are never stored; chunks past KB re-read the last one)
+    const uint8_t* wrow = op.w + (size_t)min(n0 + r16, N - 1) * K + (size_t)jb * kChunk + g * 16;
+    i32x4 wlo[kSplitMaxKB], whi[kSplitMaxKB];
+#pragma unroll
+    for (int c = 0; c < kSplitMaxKB; ++c) {
+        const size_t ko = (size_t)min(c, KB - 1) * kChunk;
+        wlo[c] = ldg16(wrow + ko);
+        whi[c] = ldg16(wrow + ko + 64);
+    }
+
+    // 2. the activation tile: rows 0..MT*16-1 (zero past M) x KB chunks,
+    //    one 128-group per 8 lanes, 16 elements (one code piece) a lane;
+    //    every pass's loads go out before the first is used
+    const int li = tid & 7;
+    constexpr int kGroupsPerPass = 32;
+    constexpr int kPasses = MT * 16 * kSplitMaxKB / kGroupsPerPass;
+    const int groups = MT * 16 * KB;
+    uint4 xa[kPasses], xb[kPasses];
+    float sc_in[kPasses];
+#pragma unroll
+    for (int ps = 0; ps < kPasses; ++ps) {
+        const int gi = ps * kGroupsPerPass + (tid >> 3);
+        const int r = gi % (MT * 16), c = gi / (MT * 16);
+        const bool live = gi < groups && r < M;
+        xa[ps] = make_uint4(0, 0, 0, 0);
+        xb[ps] = make_uint4(0, 0, 0, 0);
+        sc_in[ps] = 1.0f;
+        if (live) {
+            const int jx = jb + c;
+            if constexpr (FUSED) {
+                const uint16_t* xp = op.x + (size_t)r * K + (size_t)jx * kChunk + li * 16;
+                xa[ps] = ldg16u(xp);
+                xb[ps] = ldg16u(xp + 8);
+            } else {
+                xa[ps] = ldg16u(op.q + (size_t)r * K + (size_t)jx * kChunk + li * 16);
+                sc_in[ps] = op.s[(size_t)r * op.s_ld + jx];
+            }
+        }
+    }
+#pragma unroll
+    for (int ps = 0; ps < kPasses; ++ps) {
+        const int gi = ps * kGroupsPerPass + (tid >> 3);
+        if (ps * kGroupsPerPass >= groups) break;      // uniform: no group of this pass is live
+        const int r = gi % (MT * 16), c = gi / (MT * 16);
+        i32x4 piece;
+        float sc = sc_in[ps];
+        if constexpr (FUSED) {
+            const uint32_t d[8] = {xa[ps].x, xa[ps].y, xa[ps].z, xa[ps].w,
+                                   xb[ps].x, xb[ps].y, xb[ps].z, xb[ps].w};
+            uint32_t mb = absmax_bits(d);
+            if (mb > 0x7F80u) mb = absmax_bits_skip_nan(d);
+            mb = max8_lanes(mb);
+            float inv;
+            group_scale(bf16_bits_f32(mb), sc, inv);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                piece[q] = (int)pack4_e4m3(bf16lo(d[2 * q]) * inv, bf16hi(d[2 * q]) * inv,
+                                           bf16lo(d[2 * q + 1]) * inv, bf16hi(d[2 * q + 1]) * inv);
+            if (tn == 0 && gi < groups && r < M) {
+                const int jx = jb + c;
+                *reinterpret_cast<i32x4*>(op.q + (size_t)r * K + (size_t)jx * kChunk + li * 16) = piece;
+                if (li == 0) op.s[(size_t)r * op.s_ld + jx] = sc;
+            }
+        } else {
+            piece = i32x4{(int)xa[ps].x, (int)xa[ps].y, (int)xa[ps].z, (int)xa[ps].w};
+        }
+        if (gi < groups) {
+            *reinterpret_cast<i32x4*>(codes + code_off(c, r, li)) = piece;
+            if (li == 0) sa_lds[c][r] = sc;
+        }
+    }
+    __syncthreads();
+
+    // 3. per chunk and 16-row tile one MFMA, weights as the first operand:
+    //    lane (r16, g) holds C[column 4g+e][activation row r16]
+    typedef const __attribute__((address_space(4))) float* cf32p;
+    const cf32p swb = (cf32p)(op.sw + (size_t)(min(n0, N - 1) >> 7) * op.sw_ld + jb);
+    float swc[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) swc[e] = SM == 1 ? op.sw[min(n0 + 4 * g + e, N - 1)] : 0.0f;
+    f32x4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < kSplitMaxKB; ++c) {
+        if (c >= KB) break;
+        const i32x8 wf = join(wlo[c], whi[c]);
+        const float swj = SM == 0 ? swb[c] : 1.0f;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int r = mt * 16 + r16;
+            const i32x8 af = join(*reinterpret_cast<const i32x4*>(codes + code_off(c, r, g)),
+                                  *reinterpret_cast<const i32x4*>(codes + code_off(c, r, g + 4)));
+            const float sa = sa_lds[c][r];
+            const f32x4 p = mfma_e4m3(wf, af, f32x4{0, 0, 0, 0});
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[mt][e] += p[e] * (sa * (SM == 0 ? swj : swc[e]));
+        }
+    }
+
+    // 4. columns n0 + 4g .. +3 of rows mt*16 + r16 (N % 16 == 0: a wave's
+    //    columns lie all before N or all past it)
+    if (n0 >= N) return;
+    const int col = n0 + 4 * g;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int m = mt * 16 + r16;
+        if (m >= M) continue;
+        const size_t o = (size_t)m * N + col;
+        if (S > 1) {
+            *reinterpret_cast<f32x4*>(op.part + (size_t)split * M * N + o) = acc[mt];
+            continue;
+        }
+        float v[4] = {acc[mt][0], acc[mt][1], acc[mt][2], acc[mt][3]};
+        if (op.c_f32) {
+            float* cp = static_cast<float*>(op.c) + o;
+            if (op.residual) {
+                const f32x4 rv = *reinterpret_cast<const f32x4*>(cp);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] += rv[e];
+            }
+            *reinterpret_cast<f32x4*>(cp) = f32x4{v[0], v[1], v[2], v[3]};
+        } else {
+            uint16_t* cp = static_cast<uint16_t*>(op.c) + o;
+            if (op.residual) {
+                const uint2 rv = *reinterpret_cast<const uint2*>(cp);
+                v[0] += bf16lo(rv.x);
+                v[1] += bf16hi(rv.x);
+                v[2] += bf16lo(rv.y);
+                v[3] += bf16hi(rv.y);
+            }
+            *reinterpret_cast<uint2*>(cp) =
+                make_uint2(f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
+                           f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16));
+        }
+    }
+}
+
+// K splits for M x N x K: the fewest that keep every split at 8 chunks or
+// less (the LDS code tile and the weight registers). More splits only add
+// fp32 partials (S*M*N*4 bytes, written and read back) and per-workgroup
+// staging: on MI355X every config shape at M = 8..32 ran fastest at the
+// minimum. An override n > 0 is raised to that minimum and capped at one
+// chunk a split.
+int gemv_split_count(int M, int N, int K)
+{
+    (void)M;
+    (void)N;
+    const int forced = g_tune_split.load(std::memory_order_relaxed);
+    const int KC = K / kChunk;
+    const int s_min = (KC + kSplitMaxKB - 1) / kSplitMaxKB;
+    const int s = forced > s_min ? forced : s_min;
+    return s < KC ? s : KC;
+}
+
+size_t gemv_split_bytes(int M, int N, int K)
+{
+    const int s = gemv_split_count(M, N, K);
+    return s > 1 ? (size_t)s * M * N * 4 : 0;
+}
+
+void gemv_split_tune(int splits) { g_tune_split.store(splits, std::memory_order_relaxed); }
+
+int gemv_split_mode() { return g_tune_split.load(std::memory_order_relaxed); }
+
+// Where the fused split path beats the chunk-slot GEMV (quantization
+// included, HIP-graph replay on MI355X over the config shapes): from
+// M = 24 on weights below 32M elements (qkv -9%, o_proj -4..-9%, down
+// -10..-21% at M = 24, 32), and from M = 12 on long rows (down, K = 9728:
+// -14..-23% at M = 12, 16). Larger weights at 16 < M <= 32 (gate_up) keep
+// the quantizer + K-split GEMM, up to 5% faster there.
+bool gemv_split_routes(int M, int N, int K)
+{
+    if (M > 32) return false;
+    if (M >= 12 && K >= 8192) return true;
+    return M >= 24 && (long)N * K < (32L << 20);
+}
+
+bool gemv_split_ready(const Fp8Operands& op)
+{
+    if (op.M > 32 || op.s_step == 0) return false;
+    const int s = gemv_split_count(op.M, op.N, op.K);
+    return s == 1 || (op.part && op.part_bytes >= (size_t)s * op.M * op.N * 4);
+}
+
+hipError_t launch_fp8_gemv_split(const Fp8Operands& op, bool fused, hipStream_t stream,
+                                 const LaunchTiming& t, const char** name)
+{
+    Fp8Operands o = op;
+    o.splits = gemv_split_count(op.M, op.N, op.K);
+    const int tiles = (op.N + kSplitCols - 1) / kSplitCols;
+    const dim3 grid(tiles * o.splits), block(256);
+    *name = o.splits > 1 ? (fused ? "fp8_gemv_split64_fused_splitk" : "fp8_gemv_split64_splitk")
+                         : (fused ? "fp8_gemv_split64_fused" : "fp8_gemv_split64");
+    const LaunchTiming tk{t.start, o.splits > 1 ? nullptr : t.stop};
+    auto go = [&](auto kernel) { return launch(kernel, grid, block, 0, stream, tk, o); };
+    const int v = (op.M > 16 ? 1 : 0) + (op.w_block ? 0 : 2) + (fused ? 4 : 0);
+    hipError_t e;
+    switch (v) {
+    case 0: e = go(fp8_gemv_split_kernel<1, 0, false>); break;
+    case 1: e = go(fp8_gemv_split_kernel<2, 0, false>); break;
+    case 2: e = go(fp8_gemv_split_kernel<1, 1, false>); break;
+    case 3: e = go(fp8_gemv_split_kernel<2, 1, false>); break;
+    case 4: e = go(fp8_gemv_split_kernel<1, 0, true>); break;
+    case 5: e = go(fp8_gemv_split_kernel<2, 0, true>); break;
+    case 6: e = go(fp8_gemv_split_kernel<1, 1, true>); break;
+    default: e = go(fp8_gemv_split_kernel<2, 1, true>); break;
+    }
+    if (e != hipSuccess || o.splits == 1) return e;
+    return launch_splitk_reduce(o, stream, LaunchTiming{nullptr, t.stop});
+}
+
+}  // namespace heph

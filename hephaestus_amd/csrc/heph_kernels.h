@@ -105,6 +105,26 @@ size_t gemm_split_bytes(int M, int N, int K);
 // splits.
 bool gemm_splits_ready(const Fp8Operands& op);
 
+// Sums op.splits fp32 partials [split][M][N] at op.part in split order, adds
+// the residual and stores bf16 or f32 (M*N % 4 == 0).
+hipError_t launch_splitk_reduce(const Fp8Operands& op, hipStream_t stream, const LaunchTiming& t);
+
+// Batched decode (M <= 32, per-chunk activation scales): 64-column
+// workgroups over K splits, reading q/s from the workspace; partials in
+// op.part when it splits. Split count for M x N x K (override: n > 0
+// forces n), its scratch bytes, and whether op's scratch holds them.
+// fused: quantize x inside (group 128); column tile 0 writes q/s.
+hipError_t launch_fp8_gemv_split(const Fp8Operands& op, bool fused, hipStream_t stream,
+                                 const LaunchTiming& t, const char** name);
+int gemv_split_count(int M, int N, int K);
+size_t gemv_split_bytes(int M, int N, int K);
+bool gemv_split_ready(const Fp8Operands& op);
+// Whether M x N x K takes it by default; routing override: 0 automatic,
+// -1 never, n > 0 always (M <= 32, 1x128 groups) with n splits.
+bool gemv_split_routes(int M, int N, int K);
+void gemv_split_tune(int splits);
+int gemv_split_mode();
+
 // bf16 x [M,K] @ w [N,K]^T, f32 accumulation, M <= 32.
 hipError_t launch_bf16_skinny(void* c, bool c_f32, bool residual, const uint16_t* x,
                               const uint16_t* w, int M, int N, int K,

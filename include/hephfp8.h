@@ -170,6 +170,9 @@ const char* heph_last_kernel(void);
  *   HEPH_TUNE_GEMM_BM       tile height of the 256-column GEMM: 0, 128, 192,
  *                           256; 1 selects the 128x128 GEMM (otherwise only
  *                           used when M*K or N*K reaches 2^31)
+ *   HEPH_TUNE_BATCH_SPLIT   the 64-column K-split kernel for M <= 32 with
+ *                           1x128 groups: 0 automatic, -1 never, n in 1..64
+ *                           always with n K splits
  */
 #define HEPH_TUNE_SKINNY_WAVES 1
 #define HEPH_TUNE_SKINNY_U     2
@@ -177,6 +180,7 @@ const char* heph_last_kernel(void);
 #define HEPH_TUNE_GEMV_WAVES   4
 #define HEPH_TUNE_GEMV_U       5
 #define HEPH_TUNE_GEMM_BM      6
+#define HEPH_TUNE_BATCH_SPLIT  7
 int heph_set_tuning(int knob, int value);
 
 #ifdef __cplusplus

@@ -42,6 +42,15 @@ def check_close(got_bf16: np.ndarray, ref_f32: np.ndarray, what: str):
     return r
 
 
+@pytest.fixture
+def gemv_only():
+    """Route M <= 32 to the chunk-slot GEMV (the 64-column K-split kernel
+    off) for tests that target the GEMV itself."""
+    HK.set_tuning(L.TUNE_BATCH_SPLIT, -1)
+    yield
+    HK.set_tuning(L.TUNE_BATCH_SPLIT, 0)
+
+
 # ---------------------------------------------------------------- KATs ----
 
 def test_device_is_gfx950():
@@ -115,6 +124,7 @@ def test_quant_codes_bit_exact_oracle(M, K):
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 9, 16, 17, 32])
+@pytest.mark.usefixtures("gemv_only")
 def test_fused_quant_writes_workspace(M):
     N, K = 256, 4096
     x = O.gen_act_bf16(40 + M, M, K)
@@ -157,6 +167,7 @@ def codes_match(got, want):
 
 
 @pytest.mark.parametrize("M", [1, 3, 4, 16, 32])
+@pytest.mark.usefixtures("gemv_only")
 def test_quant_nan_and_inf_groups(M):
     # NaN is skipped by the amax (the reference's `v > local` test,
     # kernels.mojo:153-160); an infinite amax gives s = inf, inv = 0 and so
@@ -334,6 +345,7 @@ def gemv_shapes(M):
 
 @pytest.mark.parametrize("M", [2, 3, 4, 5, 8, 9, 16, 17, 32])
 @pytest.mark.parametrize("N,K", [(48, 384), (2560, 1152)])
+@pytest.mark.usefixtures("gemv_only")
 def test_gemv_rows_every_launch_shape(M, N, K):
     # The chunk-slot kernel at M rows (KS slots of MR rows, or two 16-row
     # tiles past M = 16) at every launch shape, with ragged step counts
@@ -401,6 +413,7 @@ def test_config_shapes_m1(name):
 
 @pytest.mark.parametrize("M", [2, 4, 8, 16, 32])
 @pytest.mark.parametrize("name", ["qkv", "down"])
+@pytest.mark.usefixtures("gemv_only")
 def test_small_m(M, name):
     N, K = SHAPES[name]
     x = O.gen_act_bf16(100 + M, M, K)
@@ -810,19 +823,109 @@ def test_large_m_split_k(M, N, K, out, resid):
 @pytest.mark.parametrize("M", [17, 24, 32])
 @pytest.mark.parametrize("name", ["qkv", "gate_up", "down", "o_proj"])
 def test_batched_decode_split_gemm_route(M, name):
-    # 16 < M <= 32 with a split-capable q_ws: weights of at least 32M
-    # elements (gate_up) take quantizer + K-split GEMM, the rest stays on the
-    # GEMV; both within the tolerance, codes bit-exact.
+    # With the 64-column split kernel switched off, 16 < M <= 32 with a
+    # split-capable q_ws: weights of at least 32M elements (gate_up) take
+    # quantizer + K-split GEMM, the rest the GEMV; by default the split
+    # kernel where it routes (M >= 24 below 32M weights, K >= 8192); all
+    # within the tolerance, codes bit-exact.
     N, K = SHAPES[name]
     x = O.gen_act_bf16(120 + M, M, K)
     qw, sw = O.gen_weight(1000 + N + K, N, K)
+    ref = O.quant_linear(x, qw, sw)
+    qo, _ = O.quant_act(x, 128)
     q_ws, s_ws = HK.workspace(M, K, n=N)
+    try:
+        HK.set_tuning(L.TUNE_BATCH_SPLIT, -1)
+        c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K, q_ws=q_ws, s_ws=s_ws)
+        big = N * K >= 32 << 20
+        assert HK.last_kernel().startswith("fp8_gemm") == big, HK.last_kernel()
+        check_close(host_bf16(c), ref, f"{name} M={M}")
+        assert np.array_equal(q_ws[: M * K].cpu().numpy().reshape(M, K), qo)
+    finally:
+        HK.set_tuning(L.TUNE_BATCH_SPLIT, 0)
     c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K, q_ws=q_ws, s_ws=s_ws)
-    big = N * K >= 32 << 20
-    assert HK.last_kernel().endswith("_splitk") == big, HK.last_kernel()
-    check_close(host_bf16(c), O.quant_linear(x, qw, sw), f"{name} M={M}")
+    routed = (M >= 24 and N * K < 32 << 20) or K >= 8192
+    assert HK.last_kernel().startswith("fp8_gemv_split64") == routed, HK.last_kernel()
+    check_close(host_bf16(c), ref, f"{name} M={M} default route")
+    assert np.array_equal(q_ws[: M * K].cpu().numpy().reshape(M, K), qo)
+
+
+@pytest.mark.parametrize("M", [9, 12, 16, 17, 24, 32])
+@pytest.mark.parametrize("name", ["qkv", "o_proj", "down"])
+def test_batch_split_kernel_config_shapes(M, name):
+    # The fused 64-column K-split kernel (partials summed in split order)
+    # where it routes by default (M >= 24, or M >= 12 at K = 9728), forced
+    # elsewhere: within the tolerance of the oracle, codes bit-exact, two
+    # runs bitwise identical.
+    N, K = SHAPES[name]
+    x = O.gen_act_bf16(130 + M, M, K)
+    qw, sw = O.gen_weight(1000 + N + K, N, K)
+    q_ws, s_ws = HK.workspace(M, K, n=N)
+    routed = M >= 24 or (M >= 12 and K >= 8192)
+    outs = []
+    try:
+        HK.set_tuning(L.TUNE_BATCH_SPLIT, 0 if routed else 1)
+        if not routed:
+            q_ws = torch.zeros(((M * K + 255) // 256) * 256 + 64 * M * N * 4, dtype=torch.uint8,
+                               device="cuda")
+        for _ in range(2):
+            c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K, q_ws=q_ws, s_ws=s_ws)
+            assert HK.last_kernel().startswith("fp8_gemv_split64_fused"), HK.last_kernel()
+            outs.append(host_bf16(c))
+    finally:
+        HK.set_tuning(L.TUNE_BATCH_SPLIT, 0)
+    assert np.array_equal(outs[0], outs[1])
+    check_close(outs[0], O.quant_linear(x, qw, sw), f"{name} M={M}")
     qo, _ = O.quant_act(x, 128)
     assert np.array_equal(q_ws[: M * K].cpu().numpy().reshape(M, K), qo)
+
+
+@pytest.mark.parametrize("kc,splits", [(7, 1), (7, 2), (7, 7), (21, 1), (21, 3), (21, 5),
+                                         (21, 21)])
+@pytest.mark.parametrize("M", [1, 5, 16, 32])
+def test_batch_split_kernel_forced_splits_ragged(M, kc, splits):
+    # N not a multiple of 64 (a ragged last column tile), odd chunk counts
+    # (splits of unequal length; a forced count is raised to the 8-chunk
+    # limit, so 21 chunks always split), forced split counts from 1 (direct
+    # store) to one chunk per split; f32 output with a residual and
+    # per-channel weights too; codes written to the workspace.
+    N, K = 2576, kc * 128
+    eff = min(max(splits, -(-kc // 8)), kc)
+    x = O.gen_act_bf16(140 + M, M, K)
+    qw, sw = O.gen_weight(2000 + splits, N, K)
+    ref = O.quant_linear(x, qw, sw)
+    try:
+        HK.set_tuning(L.TUNE_BATCH_SPLIT, splits)
+        q_ws, s_ws = HK.workspace(M, K, n=N)
+        need = eff * M * N * 4 + (-(-M * K // 256)) * 256
+        if q_ws.numel() < need:
+            q_ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+        c, _, _ = run_linear(qw, sw, x, M=M, N=N, K=K, q_ws=q_ws, s_ws=s_ws)
+        assert HK.last_kernel().startswith("fp8_gemv_split64_fused"), HK.last_kernel()
+        assert HK.last_kernel().endswith("_splitk") == (eff > 1), HK.last_kernel()
+        check_close(host_bf16(c), ref, f"M={M} splits={splits}")
+        qo, so = O.quant_act(x, 128)
+        assert np.array_equal(q_ws[: M * K].cpu().numpy().reshape(M, K), qo)
+        assert np.array_equal(s_ws.cpu().numpy().reshape(M, K // 128), so)
+        # codes from the workspace (SKIP_QUANT) give the same bits
+        c2, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, q_ws=q_ws, s_ws=s_ws, skip_quant=True)
+        assert HK.last_kernel().startswith("fp8_gemv_split64") and "fused" not in HK.last_kernel()
+        assert np.array_equal(host_bf16(c2), host_bf16(c))
+        res = bf16_of(O.gen_normal(7, M * N, 0.0, 1.0)).reshape(M, N)
+        r32 = torch.tensor(f32_of_bf16(res), device="cuda")
+        c, _, _ = run_linear(qw, sw, x, M=M, N=N, K=K, q_ws=q_ws, s_ws=s_ws, residual=r32)
+        assert HK.last_kernel().startswith("fp8_gemv_split64"), HK.last_kernel()
+        got = c.cpu().numpy()
+        want = ref + f32_of_bf16(res).astype(np.float64)
+        assert max_abs_rel(got, want) <= TOL, (M, splits)
+        # per-channel weights with 1x128 activation groups
+        swc = np.abs(O.gen_normal(9, N, 0.01, 0.002)).astype(np.float32).reshape(N, 1)
+        c, _, _ = run_linear(qw, swc, x, M=M, N=N, K=K, q_ws=q_ws, s_ws=s_ws)
+        assert HK.last_kernel().startswith("fp8_gemv_split64"), HK.last_kernel()
+        check_close(host_bf16(c), O.quant_linear(x, qw, swc, bn=1, bk=K),
+                    f"per-channel M={M} splits={splits}")
+    finally:
+        HK.set_tuning(L.TUNE_BATCH_SPLIT, 0)
 
 
 def test_large_m_split_k_exact_and_repeatable():
