@@ -282,7 +282,8 @@ int heph_set_tuning(int knob, int value)
         gu = value;
         break;
     case HEPH_TUNE_GEMM_BM:
-        if (value != 0 && value != 1 && value != 128 && value != 192 && value != 256)
+        if (value != 0 && value != 1 && value != 64 && value != 128 && value != 192 &&
+            value != 256)
             return HEPH_ERR_FLAGS;
         gemm_tune(value);
         return HEPH_OK;

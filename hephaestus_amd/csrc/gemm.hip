@@ -241,13 +241,13 @@ namespace {
 constexpr int L_BN = 256, L_WN = 64, L_NT = L_WN / 16;
 constexpr int L_STAGE_B = L_BN * kChunk;
 
-// Tile height BM in {128, 192, 256}: the 8 waves form a 2 x 4 grid of
+// Tile height BM in {64, 128, 192, 256}: the 8 waves form a 2 x 4 grid of
 // (BM/2) x 64 wave tiles. A smaller BM trades MFMA work per chunk for a
 // tile count that fills the CUs (e.g. 220 tiles of 192 x 256 instead of
 // 160 of 256 x 256 at M = 4096, N = 2560).
 template <int BM>
 struct BigTile {
-    static_assert(BM == 128 || BM == 192 || BM == 256, "tile height");
+    static_assert(BM == 64 || BM == 128 || BM == 192 || BM == 256, "tile height");
     static constexpr int WM = BM / 2, MT = WM / 16;
     static constexpr int STAGE_A = BM * kChunk, STAGE_S = BM * 4;
     static constexpr int STAGE = STAGE_A + L_STAGE_B + STAGE_S;
@@ -347,8 +347,10 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     // buf: parts 0-3 move A rows, 4-7 B rows, 8 the row scales.
     constexpr int kParts = 9;
     // DMA parts per row tile (MI355X: 2 over the first five of 8 row tiles,
-    // 3 over the first three of 6 or 4, fewest cycles per chunk)
-    constexpr int kPer = L_MT >= 8 ? 2 : 3;
+    // 3 over the first three of 6 or 4, fewest cycles per chunk; 5 and 4
+    // over the 2 row tiles of BM = 64, so that every part goes out)
+    constexpr int kPer = L_MT >= 8 ? 2 : L_MT >= 4 ? 3 : (kParts + L_MT - 1) / L_MT;
+    static_assert(kPer * L_MT >= kParts, "every DMA part is issued");
     auto issue_part = [&](int j, auto bufc, int part) {
         constexpr int buf = decltype(bufc)::value;
         uint8_t* st = smem + buf * L_STAGE;
@@ -445,6 +447,16 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
             if (mi + 1 < L_MT) {
                 a_[prv] = frag(a_row + (mi + 1) * 16 * kChunk);
                 sa_[prv] = *reinterpret_cast<const float*>(st + s_row + (mi + 1) * 64);
+            }
+            // Waves 4-7 (the second wave of each SIMD) win instruction issue
+            // over the first half of the row tiles. Left to the oldest-first
+            // arbiter, waves 0-3 finish every chunk ~600 cycles early and the
+            // late waves then run alone up to the barrier, with no MFMA of
+            // the other wave to hide their VALU work (MI355X: 1.5-3.5 % per
+            // shape at M = 4096).
+            if (wave >= 4) {
+                if (mi == 0) __builtin_amdgcn_s_setprio(1);
+                if (mi == L_MT / 2) __builtin_amdgcn_s_setprio(0);
             }
             if (more) {
 #pragma unroll
@@ -683,37 +695,56 @@ hipError_t launch_big(const Fp8Operands& op, hipStream_t stream, const LaunchTim
 }  // namespace
 
 // Measured cost of one 128-wide chunk per tile height (MI355X shader
-// cycles per wave and chunk at M = 4096, random E4M3 data): a taller tile
-// does more MFMA work per chunk, a shorter one fills the CUs in finer steps.
+// cycles per wave and chunk, random E4M3 data): a taller tile does more MFMA
+// work per chunk, a shorter one fills the CUs in finer steps. 256, 192 and
+// 128 rows from in-kernel stamps at M = 4096; 64 rows fitted to M = 512
+// timings (its 40 KB of operands a chunk for 2 MFMA row tiles per wave make
+// it bound by operand reads rather than MFMA).
 struct TileCost {
     int bm;
     long cycles;
 };
-constexpr TileCost kTileCost[] = {{256, 2980}, {192, 2400}, {128, 2150}};
+constexpr TileCost kTileCost[] = {{256, 2980}, {192, 2400}, {128, 2150}, {64, 1550}};
 
-long chunk_cycles(int bm)
+// Estimated time (us) of the large-M GEMM at tile height bm (chunk cost
+// `cycles`) with s K splits: rounds of (tile, split) workgroups over the
+// CUs (one 512-thread workgroup per CU) times the chunks of a split times
+// the chunk cost at ~1.9 GHz; a split adds the reduction: ~8 us of launch
+// and per-workgroup set-up, and the partials (M*N*4 bytes a split) read
+// back at ~5 TB/s.
+static double gemm_estimate(int M, int N, int K, int bm, long cycles, int s, long cus)
 {
-    for (const auto& tc : kTileCost)
-        if (tc.bm == bm) return tc.cycles;
-    return kTileCost[0].cycles;
+    const long tiles = (long)((M + bm - 1) / bm) * ((N + L_BN - 1) / L_BN);
+    const int KC = K / kChunk;
+    const long rounds = (tiles * s + cus - 1) / cus;
+    double t = (double)rounds * ((KC + s - 1) / s) * ((double)cycles / 1900.0);
+    if (s > 1) t += 8.0 + (double)s * M * N * 4.0 / 5.0e6;
+    return t;
 }
 
-// Tile height of the large-M kernel: the one with the least estimated time,
-// rounds of tiles over the CUs (one 512-thread workgroup per CU) times the
-// chunk cost at that height. The taller tile wins a tie.
-int gemm_tile_m(int M, int N)
+// Tile height and K splits of the large-M GEMM: the pair with the least
+// estimated time, splitting only when allowed, into at most 8 splits of at
+// least 4 chunks; ties go to the taller tile, then to fewer splits. A forced
+// tile height (HEPH_TUNE_GEMM_BM) fixes bm. So M = 4096 runs 256 rows for
+// N = 6144 and 19456 and 192 rows for N = 2560, all unsplit; M = 512 runs
+// qkv in 64 rows, o_proj in 64 rows and 3 splits, gate_up in 192 rows and
+// down in 128 rows and 6 splits.
+GemmPlan gemm_plan(int M, int N, int K, bool can_split)
 {
     const int forced = g_tune_bm.load(std::memory_order_relaxed);
-    if (forced >= 128) return forced;
     const long cus = cu_count();
-    int best = 256;
-    long best_t = -1;
+    const int KC = K / kChunk;
+    GemmPlan best{0, 1};
+    double best_t = -1.0;
     for (const auto& tc : kTileCost) {
-        const long tiles = (long)((M + tc.bm - 1) / tc.bm) * ((N + L_BN - 1) / L_BN);
-        const long t = (tiles + cus - 1) / cus * tc.cycles;
-        if (best_t < 0 || t < best_t) {
-            best_t = t;
-            best = tc.bm;
+        if (forced >= 64 && tc.bm != forced) continue;
+        for (int s = 1; s <= (can_split ? 8 : 1); ++s) {
+            if (s > 1 && KC / s < 4) break;
+            const double t = gemm_estimate(M, N, K, tc.bm, tc.cycles, s, cus);
+            if (best_t < 0.0 || t < best_t) {
+                best_t = t;
+                best = GemmPlan{tc.bm, s};
+            }
         }
     }
     return best;
@@ -721,46 +752,16 @@ int gemm_tile_m(int M, int N)
 
 void gemm_tune(int bm) { g_tune_bm.store(bm, std::memory_order_relaxed); }
 
-// K splits of the large-M GEMM: the count with the least estimated time,
-// rounds of (tile, split) workgroups over the CUs times the chunks of a
-// split times the per-chunk cost of the tile height (at ~1.9 GHz: about
-// 1.1 us at 128 rows), plus, when split, the reduction: about 8 us of extra
-// launch and per-workgroup set-up, and the partials (M*N*4 bytes a split)
-// read back at about 5 TB/s. At most 8 splits of at least 4 chunks. So M =
-// 512 splits o_proj and down (N = 2560: 40 tiles) 6 ways and leaves qkv
-// and gate_up whole; M = 4096 never splits.
-int gemm_splits(int M, int N, int K)
-{
-    const int bm = gemm_tile_m(M, N);
-    const long tiles = (long)((M + bm - 1) / bm) * ((N + L_BN - 1) / L_BN);
-    const long cus = cu_count();
-    const int KC = K / kChunk;
-    const double chunk_us = (double)chunk_cycles(bm) / 1900.0;
-    int best = 1;
-    double best_t = 0.0;
-    for (int s = 1; s <= 8; ++s) {
-        if (s > 1 && KC / s < 4) break;
-        const long rounds = (tiles * s + cus - 1) / cus;
-        double t = (double)rounds * ((KC + s - 1) / s) * chunk_us;
-        if (s > 1) t += 8.0 + (double)s * M * N * 4.0 / 5.0e6;
-        if (s == 1 || t < best_t) {
-            best_t = t;
-            best = s;
-        }
-    }
-    return best;
-}
-
 bool gemm_splits_ready(const Fp8Operands& op)
 {
     if (!op.part || op.s_step == 0) return false;
-    const int s = gemm_splits(op.M, op.N, op.K);
+    const int s = gemm_plan(op.M, op.N, op.K, true).splits;
     return s > 1 && op.part_bytes >= (size_t)s * op.M * op.N * 4;
 }
 
 size_t gemm_split_bytes(int M, int N, int K)
 {
-    const int s = gemm_splits(M, N, K);
+    const int s = gemm_plan(M, N, K, true).splits;
     return s > 1 ? (size_t)s * M * N * 4 : 0;
 }
 
@@ -778,9 +779,13 @@ hipError_t launch_fp8_gemm(const Fp8Operands& op, hipStream_t stream,
         // K splits when the caller's scratch holds their partials (block or
         // per-channel weights with per-chunk activation scales).
         Fp8Operands o = op;
-        o.splits = gemm_splits_ready(o) ? gemm_splits(o.M, o.N, o.K) : 1;
+        const GemmPlan plan = gemm_plan(o.M, o.N, o.K, gemm_splits_ready(o));
+        o.splits = plan.splits;
         const bool sk = o.splits > 1;
-        switch (gemm_tile_m(o.M, o.N)) {
+        switch (plan.bm) {
+        case 64:
+            *name = sk ? "fp8_gemm_64x256_splitk" : "fp8_gemm_64x256";
+            return launch_big<64>(o, stream, t);
         case 128:
             *name = sk ? "fp8_gemm_128x256_splitk" : "fp8_gemm_128x256";
             return launch_big<128>(o, stream, t);

@@ -93,16 +93,18 @@ void gemv_tune(int ks, int waves, int u);
 hipError_t launch_fp8_gemm(const Fp8Operands& op, hipStream_t stream,
                            const LaunchTiming& t, const char** name);
 
-// Tile height (128, 192 or 256) the large-M GEMM uses for M x N, and its
+// Tile height (64, 128, 192 or 256) and K splits (1 = none) of the
+// large-M GEMM for M x N x K, splits only if can_split; the tile height's
 // override (0 = automatic).
-int gemm_tile_m(int M, int N);
+struct GemmPlan {
+    int bm, splits;
+};
+GemmPlan gemm_plan(int M, int N, int K, bool can_split);
 void gemm_tune(int bm);
-// K splits the large-M GEMM uses for M x N x K when scratch allows (1 =
-// none), and the scratch bytes that takes.
-int gemm_splits(int M, int N, int K);
+// Scratch bytes for the partials of the split plan (0 when it does not
+// split), and whether op's scratch (part) holds them for a plan of more
+// than one split.
 size_t gemm_split_bytes(int M, int N, int K);
-// Whether op's scratch (part) holds the partials of gemm_splits(M, N, K) > 1
-// splits.
 bool gemm_splits_ready(const Fp8Operands& op);
 
 // Sums op.splits fp32 partials [split][M][N] at op.part in split order, adds

@@ -167,8 +167,8 @@ const char* heph_last_kernel(void);
  *   HEPH_TUNE_GEMV_WAVES    its waves per workgroup: 0, 4, 8 or 16 (16 only
  *                           for 8 < M <= 16; 8 is used otherwise)
  *   HEPH_TUNE_GEMV_U        its steps per load batch: 0, 1, 2 (1 with 16 waves)
- *   HEPH_TUNE_GEMM_BM       tile height of the 256-column GEMM: 0, 128, 192,
- *                           256; 1 selects the 128x128 GEMM (otherwise only
+ *   HEPH_TUNE_GEMM_BM       tile height of the 256-column GEMM: 0, 64, 128,
+ *                           192, 256; 1 selects the 128x128 GEMM (otherwise only
  *                           used when M*K or N*K reaches 2^31)
  *   HEPH_TUNE_BATCH_SPLIT   the 64-column K-split kernel for M <= 32 with
  *                           1x128 groups: 0 automatic, -1 never, n in 1..64

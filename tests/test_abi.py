@@ -119,9 +119,10 @@ def test_bf16_rejects(lib):
 def test_set_tuning_validates(lib):
     ok = [(L.TUNE_SKINNY_WAVES, 16), (L.TUNE_SKINNY_U, 4), (L.TUNE_GEMV_KS, 8),
           (L.TUNE_GEMV_WAVES, 4), (L.TUNE_GEMV_U, 2), (L.TUNE_GEMM_BM, 192),
+          (L.TUNE_GEMM_BM, 64),
           (L.TUNE_BATCH_SPLIT, -1), (L.TUNE_BATCH_SPLIT, 64)]
     bad = [(L.TUNE_SKINNY_WAVES, 3), (L.TUNE_SKINNY_U, 1), (L.TUNE_GEMV_KS, 16),
-           (L.TUNE_GEMV_WAVES, 2), (L.TUNE_GEMV_U, 4), (L.TUNE_GEMM_BM, 64),
+           (L.TUNE_GEMV_WAVES, 2), (L.TUNE_GEMV_U, 4), (L.TUNE_GEMM_BM, 96),
            (L.TUNE_BATCH_SPLIT, -2), (L.TUNE_BATCH_SPLIT, 65), (99, 0)]
     try:
         for knob, v in ok:

@@ -650,7 +650,7 @@ def test_graph_capture_replays_match_eager():
 
 # ------------------------------------------------ large-M GEMM variants ----
 
-@pytest.fixture(params=[128, 192, 256])
+@pytest.fixture(params=[64, 128, 192, 256])
 def tile_m(request):
     """Force the large-M kernel's tile height for one test."""
     HK.set_tuning(L.TUNE_GEMM_BM, request.param)
