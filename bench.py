@@ -23,8 +23,9 @@ kernel's own begin and end by HIP events (hipExtLaunchKernel) on the launch
 stream.
 "detail" adds per-shape figures, the bf16 lm_head, the batched-decode M
 sweep (configs[2], per call graph-replayed over rotated weights, as the
-M = 1 line) and the prefill GEMM at M = 512 and 4096 in
-TFLOP/s against the 5.0 PFLOP/s dense FP8 peak.
+M = 1 line) and the prefill GEMM at M = 512 and 4096 (configs[3], quant +
+GEMM per call, graph-replayed the same way) in TFLOP/s against the 5.0
+PFLOP/s dense FP8 peak.
 "cpu_baseline" times the CPU restatement of the same arithmetic
 (oracle/heph_oracle.c: quantize, dequantize, f32-accumulated matmul) on the
 host's cores over a bounded sample of the same workload.
@@ -95,19 +96,20 @@ def parse():
 
 
 def prefill_pass(steps):
-    """configs[3] at M = 4096: quantize + GEMM for each shape, eagerly; 100
-    launches per shape before the counted ones, so that every shape runs at
-    the clock sustained under FP8 MFMA load."""
+    """configs[3] at M = 4096: quantize + GEMM for each shape, eagerly, over
+    the rotated weight copies (as the detail sweep: weights come from HBM,
+    not the Infinity Cache); 100 launches per shape before the counted ones,
+    so that every shape runs at the clock sustained under FP8 MFMA load."""
     import torch
     from hephaestus_amd import kernels as HK
     torch.cuda.set_device(0)
     M = 4096
     for i, (name, N, K) in enumerate(SHAPES):
-        lin = Linear(name, N, K, M, seed=100 + i, rotate=False)
+        lin = Linear(name, N, K, M, seed=100 + i)
         x = act(M, K, seed=M + 1, outliers=True)
         c = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
-        w, s = lin.next()
         for _ in range(100 + steps):
+            w, s = lin.next()
             HK.linear_fp8(c, x, w, s, lin.q_ws, lin.s_ws, M, N, K)
         torch.cuda.synchronize()
         print(f"prefill-pass {name} M={M} N={N} K={K} kernel={HK.last_kernel()} "
@@ -410,7 +412,10 @@ def detail_sweeps(lins):
         small[f"M={M}"] = row
     out["small_m_GBs"] = small
 
-    # prefill GEMM, quant + GEMM path time, TFLOP/s
+    # prefill GEMM, quant + GEMM (+ K-split reduction) path time
+    # per call, graph-replayed over the rotated weight copies as the M = 1
+    # and configs[2] lines (timed eagerly, M = 512 calls are bound by the
+    # host's launch rate), TFLOP/s
     pre = {}
     for M in (512, 4096):
         row = {}
@@ -418,9 +423,9 @@ def detail_sweeps(lins):
             xm = act(M, lin.K, seed=M + 1, outliers=True)
             cm = torch.empty(M, lin.N, dtype=torch.bfloat16, device="cuda")
             q_ws, s_ws = HK.workspace(M, lin.K, n=lin.N)
-            w, s = lin.w[0], lin.s[0]
 
-            def run_p(lin=lin, xm=xm, cm=cm, M=M, q_ws=q_ws, s_ws=s_ws, w=w, s=s):
+            def run_p(lin=lin, xm=xm, cm=cm, M=M, q_ws=q_ws, s_ws=s_ws):
+                w, s = lin.next()
                 HK.linear_fp8(cm, xm, w, s, q_ws, s_ws, M, lin.N, lin.K)
             # ~20 ms of the same launches first: the shader clock settles
             # under sustained FP8 MFMA load, and a first shape timed from idle
@@ -430,8 +435,7 @@ def detail_sweeps(lins):
                 for _ in range(8):
                     run_p()
                 torch.cuda.synchronize()
-            n = 20
-            ms = time_calls(run_p, n, timer) / n
+            ms = graph_call_ms(run_p, 20)
             tf = 2.0 * M * lin.N * lin.K / (ms * 1e-3) / 1e12
             row[lin.name] = {"us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
                              "frac": round(tf / FP8_PEAK_TFLOPS, 4)}

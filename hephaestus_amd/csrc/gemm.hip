@@ -282,6 +282,24 @@ __device__ __forceinline__ void wait_dma()
     __builtin_amdgcn_s_waitcnt(0x0F70);
     asm volatile("" ::: "memory");
 }
+// The chunk-start wait of a three-stage ring: the wave's LDS reads and
+// scalar loads done (lgkmcnt(0)) and all its vector memory instructions
+// but the newest n (vmcnt(n), n = 9, 8, 4 or 0: the DMA of the next chunk
+// may stay in flight).
+__device__ __forceinline__ void wait_stage(int n)
+{
+    if (n == 9) __builtin_amdgcn_s_waitcnt(0x0079);
+    else if (n == 8) __builtin_amdgcn_s_waitcnt(0x0078);
+    else if (n == 4) __builtin_amdgcn_s_waitcnt(0x0074);
+    else __builtin_amdgcn_s_waitcnt(0x0070);
+    asm volatile("" ::: "memory");
+}
+// Workgroup barrier after wait_stage: every wave's DMA into the stage about
+// to be read has landed, and its reads of the stage about to be refilled
+// are done. No memory fence (the fence of __syncthreads waits for every
+// outstanding DMA, the next chunk's included); the clobber keeps the
+// compiler from moving LDS accesses across it.
+__device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
 // Keeps v where the program computes it: the scheduler may not sink the
 // rescale FMAs below the next row tile's MFMAs (their partials would then
 // all be live at once).
@@ -306,7 +324,15 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     using T = BigTile<BM>;
     constexpr int L_BM = BM, L_WM = T::WM, L_MT = T::MT;
     constexpr int L_STAGE_A = T::STAGE_A, L_STAGE = T::STAGE;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * L_STAGE];
+    // LDS stages: two at 192 and 256 rows (133 KB at 256), three at 128 and
+    // 64 rows, where they fit (149 KB at 128). With three, chunk j + 2's DMA
+    // goes out in chunk j, two chunks ahead: a short chunk (~0.8 us at 64
+    // rows) is well below the loaded HBM latency, and weights that are not
+    // in the Infinity Cache (each layer of a real prefill) otherwise left
+    // every chunk waiting on its DMA (MI355X: M = 512 qkv 16.4 us from the
+    // cache, 29.5 us from HBM).
+    constexpr int NS = L_BM <= 128 ? 3 : 2;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[NS * L_STAGE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -413,17 +439,26 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
         }
     };
 
+    // DMA instructions a wave issues per chunk (A rows, B rows, row scales).
+    const int n_parts = (wave * 32 < L_BM ? 4 : 0) + 4 + (SM != 2 && wave * 64 < L_BM ? 1 : 0);
+
     // One 128-wide chunk j held in stage buf (a compile-time constant). The
-    // wave's nine DMA instructions for chunk j + 1 go out kPer per row tile
-    // from the first tile on: issued together right after the barrier, the
-    // DMAs of all eight waves stall every wave's instruction issue; spread
-    // to the last tile, the late ones are still in flight at the next
-    // chunk's wait (MI355X: ~350 of ~3100 cycles a chunk).
+    // wave's nine DMA instructions for chunk j + NS - 1 go out kPer per row
+    // tile from the first tile on: issued together right after the barrier,
+    // the DMAs of all eight waves stall every wave's instruction issue;
+    // spread to the last tile, the late ones are still in flight at the
+    // next chunk's wait (MI355X: ~350 of ~3100 cycles a chunk).
     auto chunk = [&](auto bufc, int j) {
         constexpr int buf = decltype(bufc)::value;
-        wait_dma();
-        __syncthreads();
+        if constexpr (NS == 2) {
+            wait_dma();
+            __syncthreads();
+        } else {
+            wait_stage(j + 1 < je ? n_parts : 0);
+            stage_barrier();
+        }
         const bool more = j + 1 < je;
+        const bool more_dma = j + NS - 1 < je;
         if constexpr (SM == 0) {
             if (more) sw_nxt = swb[j + 1];
         }
@@ -458,10 +493,10 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
                 if (mi == 0) __builtin_amdgcn_s_setprio(1);
                 if (mi == L_MT / 2) __builtin_amdgcn_s_setprio(0);
             }
-            if (more) {
+            if (more_dma) {
 #pragma unroll
                 for (int part = 0; part < kParts; ++part)
-                    if (part / kPer == mi) issue_part(j + 1, ic<buf ^ 1>{}, part);
+                    if (part / kPer == mi) issue_part(j + NS - 1, ic<(buf + NS - 1) % NS>{}, part);
             }
             if constexpr (SM == 2) {
 #pragma unroll
@@ -482,11 +517,25 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
 #pragma unroll
     for (int part = 0; part < kParts; ++part) issue_part(jb, ic<0>{}, part);
     int j = jb;
-    for (; j + 1 < je; j += 2) {
-        chunk(ic<0>{}, j);
-        chunk(ic<1>{}, j + 1);
+    if constexpr (NS == 2) {
+        for (; j + 1 < je; j += 2) {
+            chunk(ic<0>{}, j);
+            chunk(ic<1>{}, j + 1);
+        }
+        if (j < je) chunk(ic<0>{}, j);
+    } else {
+        if (jb + 1 < je) {
+#pragma unroll
+            for (int part = 0; part < kParts; ++part) issue_part(jb + 1, ic<1>{}, part);
+        }
+        for (; j + 2 < je; j += 3) {
+            chunk(ic<0>{}, j);
+            chunk(ic<1>{}, j + 1);
+            chunk(ic<2>{}, j + 2);
+        }
+        if (j < je) chunk(ic<0>{}, j);
+        if (j + 1 < je) chunk(ic<1>{}, j + 1);
     }
-    if (j < je) chunk(ic<0>{}, j);
     if constexpr (SM != 2) rescale(L_MT - 1, (L_MT - 1) & 1);
 
     // ---- epilogue ----
@@ -516,7 +565,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
         // padded to 520 bytes (130 dwords: consecutive rows 2 banks apart),
         // each lane writing 8 bytes per block; then 16-byte coalesced stores.
         constexpr int RB = 520;
-        static_assert(L_BM * RB <= 2 * L_STAGE, "bf16 tile must fit the stage buffers");
+        static_assert(L_BM * RB <= NS * L_STAGE, "bf16 tile must fit the stage buffers");
         __syncthreads();
 #pragma unroll
         for (int mi = 0; mi < L_MT; ++mi) {
@@ -555,7 +604,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     // f32 output or residual: two passes of L_WM rows through LDS in f32
     // (the residual is added before the one rounding).
     constexpr int CST = L_BN + 4;
-    static_assert(L_WM * CST * 4 <= 2 * L_STAGE, "epilogue tile must fit the stage buffers");
+    static_assert(L_WM * CST * 4 <= NS * L_STAGE, "epilogue tile must fit the stage buffers");
     float* Cs = reinterpret_cast<float*>(smem);
     float* cw = Cs + r16 * CST + c_lane;
     for (int pass = 0; pass < 2; ++pass) {

@@ -686,6 +686,22 @@ def test_large_m_gemm_modes(mode, out, resid, tile_m):
     assert np.array_equal(q_ws.cpu().numpy().reshape(M, K), qo)
 
 
+@pytest.mark.parametrize("K", [128, 256, 384, 640])
+def test_large_m_short_k(K, tile_m):
+    # One to five K chunks: the three-stage ring of the 64- and 128-row
+    # tiles (the DMA two chunks ahead, its prologue and a tail of one or
+    # two chunks after the unrolled loop) and the two-stage ring of the
+    # taller tiles, ragged M and N, codes bit-exact.
+    M, N = 200, 272
+    x = O.gen_act_bf16(66 + K, M, K, outlier_p=1e-3)
+    qw, sw = O.gen_weight(67 + K, N, K)
+    c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K)
+    assert HK.last_kernel() == f"fp8_gemm_{tile_m}x256"
+    check_close(host_bf16(c), O.quant_linear(x, qw, sw), f"K={K} BM={tile_m}")
+    qo, _ = O.quant_act(x, 128)
+    assert np.array_equal(q_ws.cpu().numpy().reshape(M, K), qo)
+
+
 @pytest.mark.parametrize("mode", ["block", "channel_token", "channel_g128"])
 def test_large_m_bf16_is_rounded_f32(mode, tile_m):
     # The bf16 epilogue rounds with v_cvt_pk_bf16_f32; the f32 epilogue
