@@ -251,6 +251,26 @@ struct BigTile {
     static constexpr int WM = BM / 2, MT = WM / 16;
     static constexpr int STAGE_A = BM * kChunk, STAGE_S = BM * 4;
     static constexpr int STAGE = STAGE_A + L_STAGE_B + STAGE_S;
+    // LDS stages. A short chunk is below the loaded HBM latency, so where
+    // LDS allows, the DMA runs two chunks ahead: three whole stages at 64
+    // and 128 rows (149 KB at 128); at 192 rows two A/scale stages and
+    // three B stages (149 KB: the weights, streamed from HBM in a real
+    // prefill, get the extra chunk); at 256 rows two stages (133 KB).
+    static constexpr bool SPLIT_B = BM == 192;
+    static constexpr int NS = BM <= 128 ? 3 : 2;    // A and row-scale stages
+    static constexpr int NB = SPLIT_B ? 3 : NS;      // B stages
+    static constexpr int BYTES =
+        SPLIT_B ? 2 * STAGE_A + 2 * STAGE_S + 3 * L_STAGE_B : NS * STAGE;
+    // Byte offsets of A, B and row-scale stage k.
+    static constexpr int a_at(int k) { return SPLIT_B ? k * STAGE_A : k * STAGE; }
+    static constexpr int s_at(int k)
+    {
+        return SPLIT_B ? 2 * STAGE_A + k * STAGE_S : k * STAGE + STAGE_A + L_STAGE_B;
+    }
+    static constexpr int b_at(int k)
+    {
+        return SPLIT_B ? 2 * STAGE_A + 2 * STAGE_S + k * L_STAGE_B : k * STAGE + STAGE_A;
+    }
 };
 
 template <int V>
@@ -324,15 +344,14 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     using T = BigTile<BM>;
     constexpr int L_BM = BM, L_WM = T::WM, L_MT = T::MT;
     constexpr int L_STAGE_A = T::STAGE_A, L_STAGE = T::STAGE;
-    // LDS stages: two at 192 and 256 rows (133 KB at 256), three at 128 and
-    // 64 rows, where they fit (149 KB at 128). With three, chunk j + 2's DMA
-    // goes out in chunk j, two chunks ahead: a short chunk (~0.8 us at 64
-    // rows) is well below the loaded HBM latency, and weights that are not
-    // in the Infinity Cache (each layer of a real prefill) otherwise left
-    // every chunk waiting on its DMA (MI355X: M = 512 qkv 16.4 us from the
-    // cache, 29.5 us from HBM).
-    constexpr int NS = L_BM <= 128 ? 3 : 2;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[NS * L_STAGE];
+    // With three stages, chunk j + 2's DMA goes out in chunk j: a chunk
+    // (~0.8 us at 64 rows, ~1.3 us at 192) is below the loaded HBM latency,
+    // and weights that are not in the Infinity Cache (each layer of a real
+    // prefill) otherwise left every chunk waiting on its DMA (MI355X: M =
+    // 512 qkv 16.4 us from the cache, 29.5 us from HBM with two stages).
+    constexpr int NS = T::NS, NB = T::NB;
+    constexpr bool SPLIT_B = T::SPLIT_B;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[T::BYTES];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -369,24 +388,31 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     const uint32_t soff = (uint32_t)min(m0 + wave * 64 + lane, M - 1) * (uint32_t)op.s_ld * 4u;
     const uint32_t s_step = (uint32_t)op.s_step * 4u;
 
-    // DMA instruction `part` (0..8) of this wave for chunk j into stage
-    // buf: parts 0-3 move A rows, 4-7 B rows, 8 the row scales.
+    // DMA instruction `part` (0..8) of this wave: parts 0-3 move A rows of
+    // chunk ja into A stage abuf, then 4-7 B rows of chunk jw into B stage
+    // bbuf and 8 the row scales of chunk ja; with separate B stages the row
+    // scales come fourth (part 4) and the B rows last (5-8), so that the
+    // next chunk's wait can leave exactly the four B instructions in flight.
     constexpr int kParts = 9;
+    constexpr int kFirstB = SPLIT_B ? 5 : 4, kScalePart = SPLIT_B ? 4 : 8;
     // DMA parts per row tile (MI355X: 2 over the first five of 8 row tiles,
     // 3 over the first three of 6 or 4, fewest cycles per chunk; 5 and 4
     // over the 2 row tiles of BM = 64, so that every part goes out)
     constexpr int kPer = L_MT >= 8 ? 2 : L_MT >= 4 ? 3 : (kParts + L_MT - 1) / L_MT;
     static_assert(kPer * L_MT >= kParts, "every DMA part is issued");
-    auto issue_part = [&](int j, auto bufc, int part) {
-        constexpr int buf = decltype(bufc)::value;
-        uint8_t* st = smem + buf * L_STAGE;
-        const uint32_t ko = (uint32_t)j * kChunk;
+    auto issue_part = [&](int ja, int jw, auto abufc, int bbuf, int part) {
+        constexpr int abuf = decltype(abufc)::value;
         if (part < 4) {
-            if (wave * 32 < L_BM) dma16(rq, aoff[part], ko, st + (wave * 32 + part * 8) * kChunk);
-        } else if (part < 8) {
-            dma16(rw, boff[part - 4], ko, st + L_STAGE_A + (wave * 32 + (part - 4) * 8) * kChunk);
-        } else if (SM != 2 && wave * 64 < L_BM) {
-            dma4(rs, soff, (uint32_t)j * s_step, st + L_STAGE_A + L_STAGE_B + wave * 256);
+            if (wave * 32 < L_BM)
+                dma16(rq, aoff[part], (uint32_t)ja * kChunk,
+                      smem + T::a_at(abuf) + (wave * 32 + part * 8) * kChunk);
+        } else if (part == kScalePart) {
+            if (SM != 2 && wave * 64 < L_BM)
+                dma4(rs, soff, (uint32_t)ja * s_step, smem + T::s_at(abuf) + wave * 256);
+        } else {
+            const int q = part - kFirstB;
+            dma16(rw, boff[q], (uint32_t)jw * kChunk,
+                  smem + T::b_at(bbuf) + (wave * 32 + q * 8) * kChunk);
         }
     };
 
@@ -410,8 +436,8 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     // the two 16-byte slots this lane reads, and the row scale.
     const int sl0 = (slice ^ (r16 & 7)) * 16, sl1 = sl0 ^ 64;
     const int a_row = (wm * L_WM + r16) * kChunk;
-    const int b_row = L_STAGE_A + (wn * L_WN + r16) * kChunk;
-    const int s_row = L_STAGE_A + L_STAGE_B + (wm * L_WM + r16) * 4;
+    const int b_row = (wn * L_WN + r16) * kChunk;
+    const int s_row = (wm * L_WM + r16) * 4;
 
     f32x4 acc[L_MT][L_NT];
 #pragma unroll
@@ -442,46 +468,53 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     // DMA instructions a wave issues per chunk (A rows, B rows, row scales).
     const int n_parts = (wave * 32 < L_BM ? 4 : 0) + 4 + (SM != 2 && wave * 64 < L_BM ? 1 : 0);
 
-    // One 128-wide chunk j held in stage buf (a compile-time constant). The
-    // wave's nine DMA instructions for chunk j + NS - 1 go out kPer per row
+    // One 128-wide chunk j held in A stage buf (a compile-time constant)
+    // and B stage bst. The wave's nine DMA instructions (A rows and scales
+    // of chunk j + NS - 1, B rows of chunk j + NB - 1) go out kPer per row
     // tile from the first tile on: issued together right after the barrier,
     // the DMAs of all eight waves stall every wave's instruction issue;
     // spread to the last tile, the late ones are still in flight at the
     // next chunk's wait (MI355X: ~350 of ~3100 cycles a chunk).
-    auto chunk = [&](auto bufc, int j) {
+    auto chunk = [&](auto bufc, int j, int bst) {
         constexpr int buf = decltype(bufc)::value;
-        if constexpr (NS == 2) {
+        if constexpr (NB == 2) {
             wait_dma();
             __syncthreads();
         } else {
-            wait_stage(j + 1 < je ? n_parts : 0);
+            // the newest instructions, the next chunk's DMA (all nine parts
+            // with three whole stages, its four B parts with three B
+            // stages), may stay in flight
+            wait_stage(j + 1 < je ? (SPLIT_B ? 4 : n_parts) : 0);
             stage_barrier();
         }
         const bool more = j + 1 < je;
-        const bool more_dma = j + NS - 1 < je;
+        const int ja = j + NS - 1, jw = j + NB - 1;
+        const int bnext = SPLIT_B ? (bst == 0 ? 2 : bst - 1) : (buf + NB - 1) % NB;
         if constexpr (SM == 0) {
             if (more) sw_nxt = swb[j + 1];
         }
-        const uint8_t* st = smem + buf * L_STAGE;
-        auto frag = [&](int row_off) {
+        const uint8_t* sta = smem + T::a_at(buf);
+        const uint8_t* sts = smem + T::s_at(buf);
+        const uint8_t* stb = smem + T::b_at(bst);
+        auto frag = [&](const uint8_t* st, int row_off) {
             return join(*reinterpret_cast<const i32x4*>(st + row_off + sl0),
                         *reinterpret_cast<const i32x4*>(st + row_off + sl1));
         };
         i32x8 b[L_NT];
 #pragma unroll
-        for (int ni = 0; ni < L_NT; ++ni) b[ni] = frag(b_row + ni * 16 * kChunk);
+        for (int ni = 0; ni < L_NT; ++ni) b[ni] = frag(stb, b_row + ni * 16 * kChunk);
         const float swj = sw_cur;
         sw_cur = sw_nxt;
         i32x8 a_[2];
         float sa_[2];
-        a_[0] = frag(a_row);
-        sa_[0] = *reinterpret_cast<const float*>(st + s_row);
+        a_[0] = frag(sta, a_row);
+        sa_[0] = *reinterpret_cast<const float*>(sts + s_row);
 #pragma unroll
         for (int mi = 0; mi < L_MT; ++mi) {
             const int cur = mi & 1, prv = cur ^ 1;
             if (mi + 1 < L_MT) {
-                a_[prv] = frag(a_row + (mi + 1) * 16 * kChunk);
-                sa_[prv] = *reinterpret_cast<const float*>(st + s_row + (mi + 1) * 64);
+                a_[prv] = frag(sta, a_row + (mi + 1) * 16 * kChunk);
+                sa_[prv] = *reinterpret_cast<const float*>(sts + s_row + (mi + 1) * 64);
             }
             // Waves 4-7 (the second wave of each SIMD) win instruction issue
             // over the first half of the row tiles. Left to the oldest-first
@@ -493,10 +526,14 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
                 if (mi == 0) __builtin_amdgcn_s_setprio(1);
                 if (mi == L_MT / 2) __builtin_amdgcn_s_setprio(0);
             }
-            if (more_dma) {
 #pragma unroll
-                for (int part = 0; part < kParts; ++part)
-                    if (part / kPer == mi) issue_part(j + NS - 1, ic<(buf + NS - 1) % NS>{}, part);
+            for (int part = 0; part < kParts; ++part) {
+                if (part / kPer != mi) continue;
+                // the B parts stay behind the A and scale parts in issue
+                // order (the next chunk's wait relies on it)
+                if (SPLIT_B && part == kFirstB) __builtin_amdgcn_sched_barrier(0);
+                if ((part >= kFirstB && part != kScalePart ? jw : ja) < je)
+                    issue_part(ja, jw, ic<(buf + NS - 1) % NS>{}, bnext, part);
             }
             if constexpr (SM == 2) {
 #pragma unroll
@@ -515,26 +552,41 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     };
 
 #pragma unroll
-    for (int part = 0; part < kParts; ++part) issue_part(jb, ic<0>{}, part);
+    for (int part = 0; part < kParts; ++part) issue_part(jb, jb, ic<0>{}, 0, part);
     int j = jb;
-    if constexpr (NS == 2) {
+    if constexpr (NB == 2) {
         for (; j + 1 < je; j += 2) {
-            chunk(ic<0>{}, j);
-            chunk(ic<1>{}, j + 1);
+            chunk(ic<0>{}, j, 0);
+            chunk(ic<1>{}, j + 1, 1);
         }
-        if (j < je) chunk(ic<0>{}, j);
-    } else {
+        if (j < je) chunk(ic<0>{}, j, 0);
+    } else if constexpr (NS == 3) {
         if (jb + 1 < je) {
 #pragma unroll
-            for (int part = 0; part < kParts; ++part) issue_part(jb + 1, ic<1>{}, part);
+            for (int part = 0; part < kParts; ++part) issue_part(jb + 1, jb + 1, ic<1>{}, 1, part);
         }
         for (; j + 2 < je; j += 3) {
-            chunk(ic<0>{}, j);
-            chunk(ic<1>{}, j + 1);
-            chunk(ic<2>{}, j + 2);
+            chunk(ic<0>{}, j, 0);
+            chunk(ic<1>{}, j + 1, 1);
+            chunk(ic<2>{}, j + 2, 2);
         }
-        if (j < je) chunk(ic<0>{}, j);
-        if (j + 1 < je) chunk(ic<1>{}, j + 1);
+        if (j < je) chunk(ic<0>{}, j, 0);
+        if (j + 1 < je) chunk(ic<1>{}, j + 1, 1);
+    } else {
+        // two A stages, three B stages (the B stage index runs at run time)
+        if (jb + 1 < je) {
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) issue_part(jb, jb + 1, ic<0>{}, 1, kFirstB + q);
+        }
+        int bst = 0;
+        for (; j + 1 < je; j += 2) {
+            chunk(ic<0>{}, j, bst);
+            bst = bst == 2 ? 0 : bst + 1;
+            chunk(ic<1>{}, j + 1, bst);
+            bst = bst == 2 ? 0 : bst + 1;
+        }
+        if (j < je) chunk(ic<0>{}, j, bst);
     }
     if constexpr (SM != 2) rescale(L_MT - 1, (L_MT - 1) & 1);
 
@@ -565,7 +617,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
         // padded to 520 bytes (130 dwords: consecutive rows 2 banks apart),
         // each lane writing 8 bytes per block; then 16-byte coalesced stores.
         constexpr int RB = 520;
-        static_assert(L_BM * RB <= NS * L_STAGE, "bf16 tile must fit the stage buffers");
+        static_assert(L_BM * RB <= T::BYTES, "bf16 tile must fit the stage buffers");
         __syncthreads();
 #pragma unroll
         for (int mi = 0; mi < L_MT; ++mi) {
@@ -604,7 +656,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     // f32 output or residual: two passes of L_WM rows through LDS in f32
     // (the residual is added before the one rounding).
     constexpr int CST = L_BN + 4;
-    static_assert(L_WM * CST * 4 <= NS * L_STAGE, "epilogue tile must fit the stage buffers");
+    static_assert(L_WM * CST * 4 <= T::BYTES, "epilogue tile must fit the stage buffers");
     float* Cs = reinterpret_cast<float*>(smem);
     float* cw = Cs + r16 * CST + c_lane;
     for (int pass = 0; pass < 2; ++pass) {
