@@ -446,17 +446,55 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(float* ws, const uint8_t* 
             for (int e = 0; e < 16; ++e) acc[g][e] = __builtin_fmaf(pj, v16[e], acc[g][e]);
         }
     }
-    // sum over the wave's 8 key slots
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[g][e] = slots_reduce<false>(acc[g][e]);
+    // sum over the wave's 8 key slots (lanes 8k + c) by the tree of
+    // slots_reduce, ((k0+k1)+(k2+k3))+((k4+k5)+(k6+k7)), but scattering the
+    // results: pairs k^1 by row_ror:8 on all 16G values; pairs k^2 by one
+    // v_permlane16_swap per pair of values (even rows keep the first half,
+    // odd rows the second); pairs k^4 by one v_permlane32_swap per pair of
+    // the remaining 8G (the lower half keeps the first half). A lane then
+    // holds the 4G sums o = 8G * (row & 1) + 4G * (lane >= 32) + i, i < 4G,
+    // of the flattened (head, dim) index g * 16 + e: a third of the
+    // cross-lane work of reducing every value everywhere, same sums.
     __shared__ float wsum[4][G][D];
-    if ((t & 63) < 8) {
+    if constexpr (G >= 4) {
+        constexpr int V = 16 * G;
+        float* f = &acc[0][0];
+#pragma unroll
+        for (int i = 0; i < V; ++i) f[i] = dpp_add<0x128>(f[i]);
+        float h2[V / 2];
+#pragma unroll
+        for (int i = 0; i < V / 2; ++i) {
+            const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(f[i]),
+                                                            __float_as_uint(f[i + V / 2]), false, false);
+            h2[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
+        float h4[V / 4];
+#pragma unroll
+        for (int i = 0; i < V / 4; ++i) {
+            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(h2[i]),
+                                                            __float_as_uint(h2[i + V / 4]), false, false);
+            h4[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
+        const int lane = t & 63;
+        if ((lane & 8) == 0) {   // k even; its row partner k + 1 holds the same sums
+            const int o0 = (V / 2) * ((lane >> 4) & 1) + (V / 4) * (lane >> 5);
+#pragma unroll
+            for (int i = 0; i < V / 4; ++i) {
+                const int o = o0 + i;
+                wsum[wave][o >> 4][16 * c + (o & 15)] = h4[i];
+            }
+        }
+    } else {
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) wsum[wave][g][16 * c + e] = acc[g][e];
+            for (int e = 0; e < 16; ++e) acc[g][e] = slots_reduce<false>(acc[g][e]);
+        if ((t & 63) < 8) {
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) wsum[wave][g][16 * c + e] = acc[g][e];
+        }
     }
     __syncthreads();
     for (int o = t; o < G * D; o += 256) {
