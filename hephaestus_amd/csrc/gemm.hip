@@ -296,16 +296,10 @@ __device__ __forceinline__ void dma4(rsrc_t r, uint32_t voff, uint32_t soff, voi
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4,
                                              voff, soff, 0, 0);
 }
-__device__ __forceinline__ void wait_dma()
-{
-    // vmcnt(0), expcnt and lgkmcnt left at their maxima (no wait)
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    asm volatile("" ::: "memory");
-}
-// The chunk-start wait of a three-stage ring: the wave's LDS reads and
+// The chunk-start wait of the large-M kernel: the wave's LDS reads and
 // scalar loads done (lgkmcnt(0)) and all its vector memory instructions
-// but the newest n (vmcnt(n), n = 9, 8, 4 or 0: the DMA of the next chunk
-// may stay in flight).
+// but the newest n (vmcnt(n), n = 9, 8, 4 or 0: with three stages the DMA
+// of the next chunk may stay in flight).
 __device__ __forceinline__ void wait_stage(int n)
 {
     if (n == 9) __builtin_amdgcn_s_waitcnt(0x0079);
@@ -477,22 +471,14 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     // next chunk's wait (MI355X: ~350 of ~3100 cycles a chunk).
     auto chunk = [&](auto bufc, int j, int bst) {
         constexpr int buf = decltype(bufc)::value;
-        if constexpr (NB == 2) {
-            wait_dma();
-            __syncthreads();
-        } else {
-            // the newest instructions, the next chunk's DMA (all nine parts
-            // with three whole stages, its four B parts with three B
-            // stages), may stay in flight
-            wait_stage(j + 1 < je ? (SPLIT_B ? 4 : n_parts) : 0);
-            stage_barrier();
-        }
+        // with three stages the newest instructions, the next chunk's DMA
+        // (all nine parts, or its four B parts with three B stages), may
+        // stay in flight; with two, everything lands
+        wait_stage(NB == 3 && j + 1 < je ? (SPLIT_B ? 4 : n_parts) : 0);
+        stage_barrier();
         const bool more = j + 1 < je;
         const int ja = j + NS - 1, jw = j + NB - 1;
         const int bnext = SPLIT_B ? (bst == 0 ? 2 : bst - 1) : (buf + NB - 1) % NB;
-        if constexpr (SM == 0) {
-            if (more) sw_nxt = swb[j + 1];
-        }
         const uint8_t* sta = smem + T::a_at(buf);
         const uint8_t* sts = smem + T::s_at(buf);
         const uint8_t* stb = smem + T::b_at(bst);
@@ -504,11 +490,14 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
 #pragma unroll
         for (int ni = 0; ni < L_NT; ++ni) b[ni] = frag(stb, b_row + ni * 16 * kChunk);
         const float swj = sw_cur;
-        sw_cur = sw_nxt;
         i32x8 a_[2];
         float sa_[2];
         a_[0] = frag(sta, a_row);
         sa_[0] = *reinterpret_cast<const float*>(sts + s_row);
+        if constexpr (SM == 0) {
+            if (more) sw_nxt = swb[j + 1];
+        }
+        sw_cur = sw_nxt;
 #pragma unroll
         for (int mi = 0; mi < L_MT; ++mi) {
             const int cur = mi & 1, prv = cur ^ 1;
@@ -554,6 +543,14 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
 #pragma unroll
     for (int part = 0; part < kParts; ++part) issue_part(jb, jb, ic<0>{}, 0, part);
     int j = jb;
+    if constexpr (SPLIT_B) {
+        // chunk jb + 1's B rows, last in issue order
+        if (jb + 1 < je) {
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) issue_part(jb, jb + 1, ic<0>{}, 1, kFirstB + q);
+        }
+    }
     if constexpr (NB == 2) {
         for (; j + 1 < je; j += 2) {
             chunk(ic<0>{}, j, 0);
@@ -574,11 +571,6 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
         if (j + 1 < je) chunk(ic<1>{}, j + 1, 1);
     } else {
         // two A stages, three B stages (the B stage index runs at run time)
-        if (jb + 1 < je) {
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) issue_part(jb, jb + 1, ic<0>{}, 1, kFirstB + q);
-        }
         int bst = 0;
         for (; j + 1 < je; j += 2) {
             chunk(ic<0>{}, j, bst);
