@@ -944,6 +944,31 @@ def test_batch_split_kernel_forced_splits_ragged(M, kc, splits):
         HK.set_tuning(L.TUNE_BATCH_SPLIT, 0)
 
 
+@pytest.mark.parametrize("out,resid", [("bf16", False), ("f32", True)])
+def test_large_m_split_k_every_tile(out, resid, tile_m):
+    # Few tiles (M = 200, N = 272) and 17 chunks: every forced tile height
+    # splits K (ragged splits of 4 and 5 chunks) through its own stage
+    # layout: three whole stages at 64 and 128 rows, two A + three B
+    # stages at 192, two at 256. Random data against the oracle, residual
+    # added before the one rounding, codes bit-exact.
+    M, N, K = 200, 272, 2176
+    x = O.gen_act_bf16(95, M, K, outlier_p=1e-3)
+    qw, sw = O.gen_weight(96, N, K)
+    dt = torch.bfloat16 if out == "bf16" else torch.float32
+    r = O.gen_normal(97, M * N).reshape(M, N).astype(np.float32)
+    res_t = (dev(bf16_of(r)) if out == "bf16" else dev(r)) if resid else None
+    q_ws, s_ws = HK.workspace(M, K, n=N)
+    c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K, out=dt, residual=res_t, q_ws=q_ws, s_ws=s_ws)
+    assert HK.last_kernel() == f"fp8_gemm_{tile_m}x256_splitk", HK.last_kernel()
+    ref = O.quant_linear(x, qw, sw)
+    if resid:
+        ref = ref + (f32_of_bf16(bf16_of(r)) if out == "bf16" else r)
+    got = f32_of_bf16(host_bf16(c)) if out == "bf16" else c.cpu().numpy()
+    assert max_abs_rel(got, ref) <= TOL
+    qo, _ = O.quant_act(x, 128)
+    assert np.array_equal(q_ws[: M * K].cpu().numpy().reshape(M, K), qo)
+
+
 def test_large_m_split_k_exact_and_repeatable():
     # Split and unsplit runs of the same exact-integer problem give the same
     # bits (every partial sum is exact), and two split runs are identical.
