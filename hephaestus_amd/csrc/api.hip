@@ -174,15 +174,17 @@ int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
     // skinny kernel serves FORCE_SKINNY (cross-kernel checks) only. Batched
     // decode (gemv_split_routes: larger M, 1x128 groups) takes quantizer +
     // the 64-column K-split kernel when the caller's scratch holds its
-    // partials; otherwise, at 16 < M <= 32 (two 16-row tiles in the GEMV),
-    // quantizer + K-split GEMM on large weights when scratch allows.
+    // partials; otherwise, at 16 <= M <= 32, quantizer + K-split GEMM on
+    // large weights when scratch allows (MI355X, gate_up graph-replayed over
+    // HBM-streamed weights: M = 16 17.9 us against 19.8 for the GEMV; M = 8
+    // 17.1 against 15.0).
     const bool skinny = flags & HEPH_FLAG_FORCE_SKINNY;
     const bool forced_gemm = flags & HEPH_FLAG_FORCE_GEMM;
     const int bmode = gemv_split_mode();
     const bool batch_split = !skinny && !forced_gemm && M <= HEPH_SKINNY_MAX_M &&
                              group_k == kChunk && bmode >= 0 &&
                              (bmode > 0 || gemv_split_routes(M, N, K)) && gemv_split_ready(op);
-    const bool split_gemm = !batch_split && M > 16 && (long)N * K >= (32L << 20) &&
+    const bool split_gemm = !batch_split && M >= 16 && (long)N * K >= (32L << 20) &&
                             gemm_splits_ready(op);
     const bool gemv = !skinny && !forced_gemm && M <= HEPH_SKINNY_MAX_M && !split_gemm &&
                       !batch_split;

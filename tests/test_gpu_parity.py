@@ -836,10 +836,10 @@ def test_large_m_split_k(M, N, K, out, resid):
     assert np.array_equal(q_ws[: M * K].cpu().numpy().reshape(M, K), qo)
 
 
-@pytest.mark.parametrize("M", [17, 24, 32])
+@pytest.mark.parametrize("M", [16, 17, 24, 32])
 @pytest.mark.parametrize("name", ["qkv", "gate_up", "down", "o_proj"])
 def test_batched_decode_split_gemm_route(M, name):
-    # With the 64-column split kernel switched off, 16 < M <= 32 with a
+    # With the 64-column split kernel switched off, 16 <= M <= 32 with a
     # split-capable q_ws: weights of at least 32M elements (gate_up) take
     # quantizer + K-split GEMM, the rest the GEMV; by default the split
     # kernel where it routes (M >= 24 below 32M weights, K >= 8192); all
