@@ -2,7 +2,10 @@
 //
 // Replaces the reference's prefill kernel wmma_gemm_kernel_v3a_fp8
 // (src/hephaestus/wmma_gfx12.mojo:756-888: 64x64 tile, BK=16, single LDS
-// buffer, two barriers per 16-wide K step, rank-1 scale epilogue). Here:
+// buffer, two barriers per 16-wide K step, rank-1 scale epilogue). Two
+// kernels: the large-M BMx256 DMA kernel further down (every M while the
+// operands' byte offsets fit 32 bits), and first the 128x128 kernel for
+// larger operands:
 //   * 128x128 output tile per 256-thread workgroup, 2x2 waves of 64x64,
 //     each wave 4x4 v_mfma_f32_16x16x128_f8f6f4 per 128-wide K chunk;
 //   * K advances one 128-wide chunk per step, which is exactly one
@@ -220,19 +223,22 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8Operands op)
 // chunk, and four consecutive outputs to pack. Operand tiles reach LDS by
 // direct DMA (buffer_load_dwordx4 ... lds, 1 KB = 8 rows per instruction,
 // no VGPR staging); a 16-byte piece p of row r lands in slot p ^ (r & 7),
-// which spreads the fragment reads over the banks. Two stages of
-// A BM*128 B + B 32 KB + row scales BM*4 B; one barrier per 128-wide chunk:
+// which spreads the fragment reads over the banks. Stages of A BM*128 B,
+// B 32 KB and row scales BM*4 B (two, or three where LDS allows: see
+// BigTile); one barrier per 128-wide chunk:
 //   wait own DMA of chunk j -> barrier (chunk j visible everywhere, and
-//   every wave is done with the other buffer) -> DMA chunk j+1 into the
-//   other buffer -> contract chunk j.
-// The chunk loop is unrolled by two so that each stage's LDS addresses are
-// fixed registers plus instruction offsets, and the DMA advances through K
+//   every wave is done with the stage read in chunk j-1) -> DMA chunk j+1
+//   (j+2 with three stages) into that stage -> contract chunk j.
+// The chunk loop is unrolled by the stage count so that each stage's LDS
+// addresses are fixed registers plus instruction offsets (the B stage of
+// the 192-row tile, three against two A stages, is a run-time base), and
+// the DMA advances through K
 // with a scalar offset only: apart from the rescale (one FMA per
 // accumulator and chunk, one multiply per row tile) the loop holds almost
 // no VALU work, because a wave's VALU instructions do not overlap its own
 // MFMAs. The block scales come through the scalar cache.
 // The compiler does not model the DMA's LDS writes, so the waits are
-// explicit s_waitcnt vmcnt(0) plus compiler memory barriers.
+// explicit s_waitcnt vmcnt(n) plus compiler memory barriers.
 // Epilogue, bf16 output: the tile is rounded (v_cvt_pk_bf16_f32), written to
 // LDS once as bf16 (8 bytes per lane and block) and stored as coalesced
 // 16-byte row pieces. f32 output or a residual: staged in f32, BM/2 rows at
