@@ -114,10 +114,14 @@ int heph_fp8_quant_weight(const uint16_t* w_bf16, uint8_t* q, float* scale_inv, 
                                        static_cast<hipStream_t>(stream)));
 }
 
-int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t* w,
+namespace {
+
+// heph_fp8_linear, and with gamma (M = 1, group 128, fused GEMV only) the
+// RMSNorm of x folded into the GEMV's quantization prologue.
+int fp8_linear_impl(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t* w,
                     const float* w_scale, int w_block_n, int w_block_k, uint8_t* q_ws,
-                    size_t q_ws_bytes, float* s_ws, size_t s_ws_floats, int M, int N,
-                    int K, int group_k, int flags, void* stream)
+                    size_t q_ws_bytes, float* s_ws, size_t s_ws_floats, int M, int N, int K,
+                    int group_k, int flags, void* stream, const uint16_t* gamma, float eps)
 {
     const int known = HEPH_FLAG_ADD_RESIDUAL | HEPH_FLAG_SKIP_QUANT |
                       HEPH_FLAG_FORCE_SKINNY | HEPH_FLAG_FORCE_GEMM | HEPH_FLAG_NO_FUSE;
@@ -188,9 +192,11 @@ int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
                             gemm_splits_ready(op);
     const bool gemv = !skinny && !forced_gemm && M <= HEPH_SKINNY_MAX_M && !split_gemm &&
                       !batch_split;
+    if (gamma && !(gemv && M == 1 && group_k == kChunk)) return HEPH_ERR_SHAPE;
     const bool fuse_ok = !skip_quant && !(flags & HEPH_FLAG_NO_FUSE) && group_k == kChunk;
     const bool fused = fuse_ok && (batch_split || (gemv && gemv_fuses(M, N, K)) ||
                                    (skinny && M <= kFusedMaxM));
+    if (gamma && !fused) return HEPH_ERR_SHAPE;
     LaunchTiming t = take_timing();
     if (!skip_quant && !fused) {
         // A timed call spans both kernels: the quantizer carries the start
@@ -202,10 +208,35 @@ int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
     }
     hipError_t e;
     if (batch_split) e = launch_fp8_gemv_split(op, fused, s, t, &g_last_kernel);
-    else if (gemv) e = launch_fp8_gemv(op, fused, s, t, &g_last_kernel);
+    else if (gemv) e = launch_fp8_gemv(op, fused, s, t, &g_last_kernel, gamma, eps);
     else if (skinny) e = launch_fp8_skinny(op, fused, s, t, &g_last_kernel);
     else e = launch_fp8_gemm(op, s, t, &g_last_kernel);
     return launch_status(e);
+}
+
+}  // namespace
+
+int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t* w,
+                    const float* w_scale, int w_block_n, int w_block_k, uint8_t* q_ws,
+                    size_t q_ws_bytes, float* s_ws, size_t s_ws_floats, int M, int N,
+                    int K, int group_k, int flags, void* stream)
+{
+    return fp8_linear_impl(c, c_dtype, x_bf16, w, w_scale, w_block_n, w_block_k, q_ws,
+                           q_ws_bytes, s_ws, s_ws_floats, M, N, K, group_k, flags, stream,
+                           nullptr, 0.0f);
+}
+
+int heph_fp8_linear_rmsnorm(void* c, int c_dtype, const uint16_t* x_bf16,
+                            const uint16_t* gamma_bf16, float eps, const uint8_t* w,
+                            const float* w_scale, int w_block_n, int w_block_k, uint8_t* q_ws,
+                            size_t q_ws_bytes, float* s_ws, size_t s_ws_floats, int N, int K,
+                            int flags, void* stream)
+{
+    if (!gamma_bf16 || !x_bf16) return HEPH_ERR_NULL;
+    if (flags & ~HEPH_FLAG_ADD_RESIDUAL) return HEPH_ERR_FLAGS;
+    return fp8_linear_impl(c, c_dtype, x_bf16, w, w_scale, w_block_n, w_block_k, q_ws,
+                           q_ws_bytes, s_ws, s_ws_floats, 1, N, K, kChunk, flags, stream,
+                           gamma_bf16, eps);
 }
 
 int heph_bf16_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint16_t* w_bf16,

@@ -98,25 +98,6 @@ __global__ __launch_bounds__(256) void embed_fp8_kernel(uint16_t* x, const uint8
 // move between its lanes: two barriers in all. Rows up to 256 * PER
 // elements hold x and gamma in registers, every load issued before the
 // first use; longer rows loop.
-__device__ __forceinline__ float fold256_wave0(float v, float* red, float* out)
-{
-    const int t = threadIdx.x;
-    red[t] = v;
-    __syncthreads();
-    if (t < 64) {
-        float a = (red[t] + red[t + 128]) + (red[t + 64] + red[t + 192]);
-        for (int h = 32; h > 0; h >>= 1) a += __shfl_down(a, h, 64);
-        if (t == 0) *out = a;
-    }
-    __syncthreads();
-    return *out;
-}
-
-__device__ __forceinline__ float rms_inv(float ss, int cols, float eps)
-{
-    return __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)cols) + eps));
-}
-
 template <int PER>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* out, const uint16_t* in,
                                                       const uint16_t* gamma, int cols, float eps)

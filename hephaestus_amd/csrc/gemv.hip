@@ -49,6 +49,10 @@ namespace heph {
 struct GemvArgs {
     Fp8Operands op;
     bool write_ws;
+    // RMSNorm prologue (M = 1, fused): x is the un-normalized row, each
+    // activation becomes bf16(gamma * bf16(x * r)) before its quantization
+    const uint16_t* gamma;
+    float eps;
 };
 
 enum GemvScale { kGemvBlock = 0, kGemvChannel = 1, kGemvConst = 2 };
@@ -140,9 +144,11 @@ __device__ __forceinline__ float pick(const f32x4& p, int e)
 
 }  // namespace
 
-template <int WAVES, int KS, int MR, int MT, int U, bool FUSED, int SM>
+template <int WAVES, int KS, int MR, int MT, int U, bool FUSED, int SM, bool NORM = false>
 __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
 {
+    static_assert(!NORM || (FUSED && MR == 1 && MT == 1 && WAVES >= 4),
+                  "RMSNorm prologue: fused M = 1 with at least 256 threads");
     static_assert(KS == 1 || KS == 2 || KS == 4 || KS == 8, "chunk slots");
     static_assert(MR == 1 || MR == 2 || MR == 4 || MR == 8 || MR == 16, "rows per slot");
     static_assert(KS * MR <= 16, "slots x rows must fit the 16 MFMA rows");
@@ -191,6 +197,7 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
         i32x4 blo[U], bhi[U];
         i32x4 alo[FUSED ? 1 : U][MT], ahi[FUSED ? 1 : U][MT];
         XVec<E> xv[FUSED ? U : 1][MT];
+        XVec<E> gv[NORM ? U : 1];       // gamma at the same columns
         float sw[U];
         // MR = 1: the scale of this lane's candidate row; else the scale of
         // its own A row r16, passed to the candidate rows by ds_bpermute
@@ -218,6 +225,9 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
 #pragma unroll
                     for (int d = 0; d < E / 2; ++d) b.xv[u][mt].d[d] = live ? v.d[d] : 0u;
                 }
+                if constexpr (NORM)
+                    b.gv[u] = load_xvec<E>(args.gamma + (size_t)min(jx, KC - 1) * kChunk +
+                                           qpiece * E);
             } else {
                 const int ja = st * KS + ta;
 #pragma unroll
@@ -253,6 +263,7 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int i = 0; i < NE; ++i) acc[mt][i] = 0.0f;
+    float rn = 1.0f;    // RMSNorm factor (NORM)
 
     auto contract = [&](int mt, const i32x4& alo, const i32x4& ahi, const i32x4& blo,
                         const i32x4& bhi, const float* scl) {
@@ -274,7 +285,20 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
                 if (s + u >= se) break;
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
-                    const XVec<E>& xv = b.xv[u][mt];
+                    XVec<E>& xv = b.xv[u][mt];
+                    if constexpr (NORM) {
+                        // the RMSNorm output, as the standalone kernel
+                        // rounds it: bf16(gamma * bf16(x * r))
+#pragma unroll
+                        for (int d = 0; d < E / 2; ++d) {
+                            const uint32_t xd = xv.d[d], gd = b.gv[u].d[d];
+                            const float yl = bf16lo((uint32_t)f32_to_bf16(bf16lo(xd) * rn));
+                            const float yh = bf16lo((uint32_t)f32_to_bf16(bf16hi(xd) * rn));
+                            const uint32_t lo = f32_to_bf16(bf16lo(gd) * yl);
+                            const uint32_t hi = f32_to_bf16(bf16hi(gd) * yh);
+                            xv.d[d] = lo | (hi << 16);
+                        }
+                    }
                     // a lane holding a NaN takes the NaN-skipping max of its
                     // own elements before the cross-lane max (rare; a
                     // divergent branch that no lane takes costs two scalar
@@ -361,10 +385,33 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
     // current ones.
     Batch b0, b1;
     if (sb < se) issue(b0, sb);
-    // arrive = 0 is seen by every wave before any wave's increment; the
-    // barrier waits here, with the first loads in flight, rather than
-    // before them
-    __syncthreads();
+    if constexpr (NORM) {
+        // RMSNorm of the row, in the standalone kernel's order (threads
+        // t < 256 sum elements t, t + 256, ... by fma, 16 loads in flight,
+        // then fold256_wave0); its barriers also publish arrive = 0
+        __shared__ float nred[256];
+        __shared__ float nres;
+        float ss = 0.0f;
+        if (threadIdx.x < 256) {
+            for (int i0 = threadIdx.x; i0 < K; i0 += 256 * 16) {
+                float v[16];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int i = i0 + e * 256;
+                    v[e] = i < K ? bf16lo((uint32_t)op.x[i]) : 0.0f;
+                }
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    if (i0 + e * 256 < K) ss = __builtin_fmaf(v[e], v[e], ss);
+            }
+        }
+        rn = rms_inv(fold256_wave0(ss, nred, &nres), K, args.eps);
+    } else {
+        // arrive = 0 is seen by every wave before any wave's increment; the
+        // barrier waits here, with the first loads in flight, rather than
+        // before them
+        __syncthreads();
+    }
     for (int s = sb; s < se; s += 2 * U) {
         if (s + U < se) issue(b1, s + U);
         consume(b0, s);
@@ -428,6 +475,16 @@ hipError_t launch_ks(const GemvArgs& a, bool fused, hipStream_t stream, const La
 {
     const dim3 grid(a.op.N / (16 / KS));
     const dim3 block(WAVES * 64);
+    if (a.gamma) {
+        if constexpr (MR == 1 && MT == 1 && WAVES >= 4) {
+            if (a.op.w_block)
+                return launch(fp8_gemv_kernel<WAVES, KS, MR, MT, U, true, kGemvBlock, true>, grid,
+                              block, 0, stream, t, a);
+            return launch(fp8_gemv_kernel<WAVES, KS, MR, MT, U, true, kGemvChannel, true>, grid,
+                          block, 0, stream, t, a);
+        }
+        return hipErrorInvalidValue;
+    }
     if (fused) {
         if (a.op.w_block)
             return launch(fp8_gemv_kernel<WAVES, KS, MR, MT, U, true, kGemvBlock>, grid, block,
@@ -522,13 +579,14 @@ void gemv_shape(int M, int N, int K, int* ks, int* waves, int* u)
 }
 
 hipError_t launch_fp8_gemv(const Fp8Operands& op, bool fused, hipStream_t stream,
-                           const LaunchTiming& t, const char** name)
+                           const LaunchTiming& t, const char** name, const uint16_t* gamma,
+                           float eps)
 {
-    GemvArgs a{op, fused};
+    GemvArgs a{op, fused, gamma, eps};
     int ks, waves, u;
     gemv_shape(op.M, op.N, op.K, &ks, &waves, &u);
     const int mr = gemv_rows(op.M);
-    if (op.M == 1) *name = fused ? "fp8_gemv_fused_m1" : "fp8_gemv_m1";
+    if (op.M == 1) *name = gamma ? "fp8_gemv_rmsnorm_m1" : fused ? "fp8_gemv_fused_m1" : "fp8_gemv_m1";
     else if (op.M <= 16) *name = fused ? "fp8_gemv_fused_m16" : "fp8_gemv_m16";
     else *name = fused ? "fp8_gemv_fused_m32" : "fp8_gemv_m32";
     switch (waves) {

@@ -163,6 +163,31 @@ __device__ __forceinline__ i32x4 ldg16(const void* p)
     return *reinterpret_cast<const i32x4*>(p);
 }
 
+// RMSNorm's sum of squares over one row: thread t < 256 of the workgroup
+// brings v = its fma chain over elements t, t + 256, ...; the 256 sums are
+// folded as s[t] += s[t + h] for h = 128, 64, ..., 1, the first two levels
+// read by wave 0 from LDS as (s[t] + s[t+128]) + (s[t+64] + s[t+192]), the
+// rest moved between its lanes: two barriers (every thread of the
+// workgroup calls it). red holds 256 floats, out one.
+__device__ __forceinline__ float fold256_wave0(float v, float* red, float* out)
+{
+    const int t = threadIdx.x;
+    if (t < 256) red[t] = v;
+    __syncthreads();
+    if (t < 64) {
+        float a = (red[t] + red[t + 128]) + (red[t + 64] + red[t + 192]);
+        for (int h = 32; h > 0; h >>= 1) a += __shfl_down(a, h, 64);
+        if (t == 0) *out = a;
+    }
+    __syncthreads();
+    return *out;
+}
+
+__device__ __forceinline__ float rms_inv(float ss, int cols, float eps)
+{
+    return __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)cols) + eps));
+}
+
 __device__ __forceinline__ uint4 ldg16u(const void* p)
 {
     return *reinterpret_cast<const uint4*>(p);

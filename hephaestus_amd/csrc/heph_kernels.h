@@ -76,9 +76,12 @@ hipError_t launch_fp8_skinny(const Fp8Operands& op, bool fused, hipStream_t stre
 void skinny_tune(int waves, int u);
 
 // M <= 32 kernel with K-chunk slots in the MFMA rows. fused: quantize x
-// inside the kernel (group 128); workgroup 0 also writes q/s.
+// inside the kernel (group 128); workgroup 0 also writes q/s. gamma (fused,
+// M = 1 only): x is first RMS-normalized with gamma and eps, as
+// heph_rmsnorm_bf16 rounds it.
 hipError_t launch_fp8_gemv(const Fp8Operands& op, bool fused, hipStream_t stream,
-                           const LaunchTiming& t, const char** name);
+                           const LaunchTiming& t, const char** name,
+                           const uint16_t* gamma = nullptr, float eps = 0.0f);
 
 // Rows per chunk slot for M rows (M rounded up to a power of two, at most
 // 16), and the launch shape (chunk slots, waves, steps per batch) for

@@ -6,16 +6,15 @@ per (layer, kv head, K|V):
 
     x = embed(token)                                     heph_embed_fp8
     per layer:
-        xn  = rmsnorm(x, attn_norm)                      heph_rmsnorm
-        qkv = xn @ Wqkv^T          (fused quant)         heph_fp8_linear
+        qkv = rmsnorm(x, attn_norm) @ Wqkv^T             heph_fp8_linear_rmsnorm
+              (norm + quant inside the GEMV; = heph_rmsnorm then heph_fp8_linear)
         q, k, v: per-head q/k norm, RoPE, k/v -> cache   heph_qk_norm_rope_kv
         att = attention(q, K[:pos+1], V[:pos+1])         heph_attention_fp8kv
         x  += att @ Wo^T                                 heph_fp8_linear + ADD_RESIDUAL
-        xn  = rmsnorm(x, ffn_norm)
-        gu  = xn @ Wgate_up^T
+        gu  = rmsnorm(x, ffn_norm) @ Wgate_up^T          heph_fp8_linear_rmsnorm
         act = silu(gate) * up                            heph_silu_mul
         x  += act @ Wdown^T
-    logits = rmsnorm(x, norm) @ E^T   (f32, tied FP8 embedding)
+    logits = rmsnorm(x, norm) @ E^T   (f32, tied FP8 embedding; fused norm)
     token  = argmax(bf16(logits)), lowest index on ties  heph_argmax_bf16
 
 Every op is a HIP kernel of libhephfp8.so; torch only holds device memory.
@@ -194,6 +193,17 @@ class Qwen3Decoder:
         fn = HK.linear_add_residual_fp8 if residual else HK.linear_fp8
         fn(c, a, fw.w, fw.scale, self.q_ws, self.s_ws, 1, fw.N, K)
 
+    def _norm_linear(self, c, gamma, fw: Fp8Weight, K: int, eps: float, rec, li, op):
+        """c = rmsnorm(self.x, gamma) @ fw: the norm inside the fused GEMV
+        (heph_fp8_linear_rmsnorm, bit for bit heph_rmsnorm + the linear). A
+        traced step also writes the normalized row to self.xn, for the record
+        only."""
+        HK.linear_fp8_rmsnorm(c, self.x, gamma, eps, fw.w, fw.scale, self.q_ws, self.s_ws,
+                              fw.N, K)
+        if rec.tracing:
+            rmsnorm(self.xn, self.x, gamma, eps)
+            rec(li, op, self.xn)
+
     def step(self, token, pos: int, trace: list | None = None) -> torch.Tensor:
         """Decode `token` (int or int32 device tensor [1]) at position pos;
         the KV cache row pos is written. Returns the argmax token (int32
@@ -215,15 +225,14 @@ class Qwen3Decoder:
                 a = (t.view(torch.int16).cpu().numpy().view(np.uint16) if t.dtype == torch.bfloat16
                      else t.cpu().numpy())
                 trace.append((li, op, a.reshape(-1).copy()))
+        rec.tracing = trace is not None
 
         H, I, Q = cfg.hidden, cfg.inter, cfg.q_out
         NH, NKV, eps = cfg.n_heads, cfg.n_kv_heads, cfg.eps
         embed_fp8(self.x, w.embed.w, w.embed.scale, self.token)
         rec(-1, "embed", self.x)
         for li, lw in enumerate(w.layers):
-            rmsnorm(self.xn, self.x, lw.attn_norm, eps)
-            rec(li, "attn_norm", self.xn)
-            self._linear(self.qkv, self.xn, lw.qkv, H)
+            self._norm_linear(self.qkv, lw.attn_norm, lw.qkv, H, eps, rec, li, "attn_norm")
             rec(li, "qkv", self.qkv)
             qk_norm_rope_kv(self.qkv, lw.q_norm, lw.k_norm, kv.k[li, pos], kv.v[li, pos],
                             kv.inv[li], NH, NKV, pos, cfg.theta, eps)
@@ -235,17 +244,13 @@ class Qwen3Decoder:
             rec(li, "attention", self.att)
             self._linear(self.x, self.att, lw.o, Q, residual=True)
             rec(li, "o_residual", self.x)
-            rmsnorm(self.xn, self.x, lw.ffn_norm, eps)
-            rec(li, "ffn_norm", self.xn)
-            self._linear(self.gu, self.xn, lw.gate_up, H)
+            self._norm_linear(self.gu, lw.ffn_norm, lw.gate_up, H, eps, rec, li, "ffn_norm")
             rec(li, "gate_up", self.gu)
             silu_mul(self.act, self.gu, self.gu[:, I:], I)
             rec(li, "silu_mul", self.act)
             self._linear(self.x, self.act, lw.down, I, residual=True)
             rec(li, "down_residual", self.x)
-        rmsnorm(self.xn, self.x, w.final_norm, eps)
-        rec(-1, "final_norm", self.xn)
-        self._linear(self.logits, self.xn, w.embed, H)
+        self._norm_linear(self.logits, w.final_norm, w.embed, H, eps, rec, -1, "final_norm")
         rec(-1, "logits", self.logits)
         argmax_bf16(self.next_token, self.logits, self.arg_ws)
         rec(-1, "argmax", self.next_token)

@@ -121,6 +121,26 @@ def _linear_fp8(c, a, w, scale, a_fp8_ws, act_scale_ws, m, n, k, ctx, *,
     _check(s, where)
 
 
+def linear_fp8_rmsnorm(c, x, gamma, eps, w, scale, a_fp8_ws, act_scale_ws, n, k, ctx=None, *,
+                       add_residual=False):
+    """c = rmsnorm(x, gamma, eps) @ dequant(w)^T for one row (M = 1), the
+    norm computed inside the fused GEMV (bit for bit rmsnorm then linear_fp8);
+    the workspaces receive the normalized row's codes and scales."""
+    bn, bk = _weight_block(scale, n, k)
+    if c.dtype not in _OUT:
+        raise TypeError(f"linear_fp8_rmsnorm: output dtype {c.dtype} not supported")
+    if c.numel() < n or w.numel() < n * k or x.numel() < k or gamma.numel() < k:
+        raise HephError(L.HEPH_ERR_SHAPE, "linear_fp8_rmsnorm")
+    s = L.lib().heph_fp8_linear_rmsnorm(
+        _dev(c, "c", tuple(_OUT)), _OUT[c.dtype], _dev(x, "x", (torch.bfloat16,)),
+        _dev(gamma, "gamma", (torch.bfloat16,)), float(eps),
+        _dev(w, "w", _FP8), _dev(scale, "scale", (torch.float32,)), bn, bk,
+        _dev(a_fp8_ws, "a_fp8_ws", _FP8), a_fp8_ws.numel(),
+        _dev(act_scale_ws, "act_scale_ws", (torch.float32,)), act_scale_ws.numel(),
+        n, k, L.FLAG_ADD_RESIDUAL if add_residual else 0, _stream(ctx))
+    _check(s, "linear_fp8_rmsnorm")
+
+
 def linear_fp8(c, a, w, scale, a_fp8_ws, act_scale_ws, m, n, k, ctx=None, *,
                do_quantize=True, group_k=None, flags=0):
     """C = A @ W^T through the W8A8 FP8 path (quantize A, FP8 contraction,

@@ -111,6 +111,23 @@ int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16,
                     int group_k, int flags, void* stream);
 
 /*
+ * Decode-step linear on an RMS-normalized row (M = 1, group 128): c =
+ * rmsnorm(x, gamma, eps) @ dequant(w)^T, where the norm is
+ * bf16(gamma * bf16(x * r)) with r = 1/sqrt(mean(x^2) + eps) summed as
+ * heph_rmsnorm sums it, computed by every workgroup of the fused GEMV
+ * before its quantization, so the normalized row is never written. Bit for
+ * bit heph_rmsnorm followed by heph_fp8_linear; the workspaces hold the
+ * normalized row's codes and scales. Replaces the pair rms_norm + linear_fp8
+ * of the reference's decode step (src/hephaestus/forward.mojo:359-615,
+ * kernels.mojo:653-762). flags: HEPH_FLAG_ADD_RESIDUAL only.
+ */
+int heph_fp8_linear_rmsnorm(void* c, int c_dtype, const uint16_t* x_bf16,
+                            const uint16_t* gamma_bf16, float eps, const uint8_t* w,
+                            const float* w_scale, int w_block_n, int w_block_k,
+                            uint8_t* q_ws, size_t q_ws_bytes, float* s_ws,
+                            size_t s_ws_floats, int N, int K, int flags, void* stream);
+
+/*
  * Unquantized bf16 linear with f32 accumulation: c = x @ w^T.
  * Replaces `linear` for the lm_head (reference
  * src/hephaestus/kernels.mojo:89-121, which keeps F32 logits); accepts

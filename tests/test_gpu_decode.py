@@ -64,6 +64,40 @@ def test_embed_bit_exact():
     assert np.array_equal(host(x), O.embed_fp8(emb, sblk, True, toks))
 
 
+@pytest.mark.parametrize("N,K,scale,out", [(6144, 2560, 1.0, "bf16"), (19456, 2560, 40.0, "bf16"),
+                                           (2560, 4224, 1e-3, "f32"), (4096, 1152, 1.0, "f32")])
+def test_fused_rmsnorm_linear_bit_exact(N, K, scale, out):
+    # heph_fp8_linear_rmsnorm (the norm inside the fused M = 1 GEMV) gives
+    # the bits of heph_rmsnorm followed by heph_fp8_linear, leaves the same
+    # codes and scales in the workspaces, and adds the residual alike.
+    from hephaestus_amd import kernels as HK
+    x = rng_bf16(K + N, K, scale)
+    g = rng_bf16(8, K, 0.5)
+    qw, sw = O.gen_weight(K + 3, N, K)
+    dt = torch.bfloat16 if out == "bf16" else torch.float32
+    xd, gd, wd, sd = dev(x), dev(g), dev(qw), dev(sw)
+    res = (torch.randn(N, device="cuda") * 3).to(dt)
+    for resid in (False, True):
+        q1, s1 = HK.workspace(1, K)
+        q2, s2 = HK.workspace(1, K)
+        xn = torch.empty(K, dtype=torch.bfloat16, device="cuda")
+        c1, c2 = res.clone(), res.clone()
+        DEC.rmsnorm(xn, xd, gd)
+        fn = HK.linear_add_residual_fp8 if resid else HK.linear_fp8
+        fn(c1, xn, wd, sd, q1, s1, 1, N, K)
+        HK.linear_fp8_rmsnorm(c2, xd, gd, 1e-6, wd, sd, q2, s2, N, K, add_residual=resid)
+        assert HK.last_kernel() == "fp8_gemv_rmsnorm_m1"
+        torch.cuda.synchronize()
+        assert np.array_equal(host(c1).view(np.uint8), host(c2).view(np.uint8)), f"resid={resid}"
+        assert torch.equal(q1[:K], q2[:K]) and torch.equal(s1[:K // 128], s2[:K // 128])
+    # flags other than ADD_RESIDUAL are refused
+    st = L.lib().heph_fp8_linear_rmsnorm(
+        c2.data_ptr(), 0 if out == "bf16" else 1, xd.data_ptr(), gd.data_ptr(), 1e-6,
+        wd.data_ptr(), sd.data_ptr(), 128, 128, q2.data_ptr(), q2.numel(), s2.data_ptr(),
+        s2.numel(), N, K, L.FLAG_SKIP_QUANT, None)
+    assert st == L.HEPH_ERR_FLAGS
+
+
 @pytest.mark.parametrize("rows,cols,scale", [(3, 2560, 1.0), (1, 9728, 40.0), (2, 2560, 1e-4),
                                              (32, 128, 1.0), (2, 12288, 1.0)])
 def test_rmsnorm_bit_exact(rows, cols, scale):
