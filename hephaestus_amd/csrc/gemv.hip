@@ -384,16 +384,29 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
     // Two batches in flight: issue the next U steps before consuming the
     // current ones.
     Batch b0, b1;
+    // RMSNorm (NORM): threads t < 256 sum the squares of elements t, t + 256,
+    // ... by fma, the standalone kernel's order. The first 16 of those loads
+    // go out before the weight batch: a wave's loads return in order, and
+    // the norm's row should not wait behind the weights.
+    float nv[NORM ? 16 : 1];
+    if constexpr (NORM) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int i = (int)threadIdx.x + e * 256;
+            nv[e] = threadIdx.x < 256 && i < K ? bf16lo((uint32_t)op.x[i]) : 0.0f;
+        }
+    }
     if (sb < se) issue(b0, sb);
     if constexpr (NORM) {
-        // RMSNorm of the row, in the standalone kernel's order (threads
-        // t < 256 sum elements t, t + 256, ... by fma, 16 loads in flight,
-        // then fold256_wave0); its barriers also publish arrive = 0
+        // then the fold of the 256 sums, as fold256_wave0 (its one barrier
+        // also publishes arrive = 0)
         __shared__ float nred[256];
-        __shared__ float nres;
         float ss = 0.0f;
         if (threadIdx.x < 256) {
-            for (int i0 = threadIdx.x; i0 < K; i0 += 256 * 16) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                if ((int)threadIdx.x + e * 256 < K) ss = __builtin_fmaf(nv[e], nv[e], ss);
+            for (int i0 = threadIdx.x + 256 * 16; i0 < K; i0 += 256 * 16) {
                 float v[16];
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
@@ -405,7 +418,7 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
                     if (i0 + e * 256 < K) ss = __builtin_fmaf(v[e], v[e], ss);
             }
         }
-        rn = rms_inv(fold256_wave0(ss, nred, &nres), K, args.eps);
+        rn = rms_inv(fold256_every_wave(ss, nred), K, args.eps);
     } else {
         // arrive = 0 is seen by every wave before any wave's increment; the
         // barrier waits here, with the first loads in flight, rather than

@@ -183,6 +183,19 @@ __device__ __forceinline__ float fold256_wave0(float v, float* red, float* out)
     return *out;
 }
 
+// The same fold with its result in every wave and one barrier: after the
+// first level's barrier each wave repeats wave 0's part (same operands, same
+// order) and takes lane 0's sum.
+__device__ __forceinline__ float fold256_every_wave(float v, float* red)
+{
+    const int t = threadIdx.x, l = t & 63;
+    if (t < 256) red[t] = v;
+    __syncthreads();
+    float a = (red[l] + red[l + 128]) + (red[l + 64] + red[l + 192]);
+    for (int h = 32; h > 0; h >>= 1) a += __shfl_down(a, h, 64);
+    return __shfl(a, 0, 64);
+}
+
 __device__ __forceinline__ float rms_inv(float ss, int cols, float eps)
 {
     return __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)cols) + eps));
