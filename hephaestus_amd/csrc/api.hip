@@ -234,6 +234,7 @@ int heph_fp8_linear_rmsnorm(void* c, int c_dtype, const uint16_t* x_bf16,
 {
     if (!gamma_bf16 || !x_bf16) return HEPH_ERR_NULL;
     if (flags & ~HEPH_FLAG_ADD_RESIDUAL) return HEPH_ERR_FLAGS;
+    if (K > kNormMaxK) return HEPH_ERR_SHAPE;
     return fp8_linear_impl(c, c_dtype, x_bf16, w, w_scale, w_block_n, w_block_k, q_ws,
                            q_ws_bytes, s_ws, s_ws_floats, 1, N, K, kChunk, flags, stream,
                            gamma_bf16, eps);

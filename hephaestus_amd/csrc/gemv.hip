@@ -186,6 +186,9 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
     __shared__ int arrive;
     __shared__ __attribute__((aligned(16))) uint8_t qlds[FUSED ? WAVES : 1][FUSED ? U : 1]
                                                         [FUSED ? MT : 1][R * kChunk];
+    // NORM: the row and gamma (bf16)
+    __shared__ __attribute__((aligned(16))) uint16_t nrow[NORM ? kNormMaxK : 1];
+    __shared__ __attribute__((aligned(16))) uint16_t ngam[NORM ? kNormMaxK : 1];
     if (threadIdx.x == 0) arrive = 0;
 
     const int n = n0 + r16 % TW;
@@ -197,7 +200,6 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
         i32x4 blo[U], bhi[U];
         i32x4 alo[FUSED ? 1 : U][MT], ahi[FUSED ? 1 : U][MT];
         XVec<E> xv[FUSED ? U : 1][MT];
-        XVec<E> gv[NORM ? U : 1];       // gamma at the same columns
         float sw[U];
         // MR = 1: the scale of this lane's candidate row; else the scale of
         // its own A row r16, passed to the candidate rows by ds_bpermute
@@ -213,7 +215,9 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int st = min(s + u, se - 1);
-            if constexpr (FUSED) {
+            if constexpr (NORM) {
+                // the row and gamma come from LDS at quantization time
+            } else if constexpr (FUSED) {
                 const int jx = st * KS + tq;
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
@@ -225,9 +229,6 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
 #pragma unroll
                     for (int d = 0; d < E / 2; ++d) b.xv[u][mt].d[d] = live ? v.d[d] : 0u;
                 }
-                if constexpr (NORM)
-                    b.gv[u] = load_xvec<E>(args.gamma + (size_t)min(jx, KC - 1) * kChunk +
-                                           qpiece * E);
             } else {
                 const int ja = st * KS + ta;
 #pragma unroll
@@ -288,10 +289,18 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
                     XVec<E>& xv = b.xv[u][mt];
                     if constexpr (NORM) {
                         // the RMSNorm output, as the standalone kernel
-                        // rounds it: bf16(gamma * bf16(x * r))
+                        // rounds it: bf16(gamma * bf16(x * r)), from the row
+                        // and gamma the prologue left in LDS (zero past K)
+                        const int jx = (s + u) * KS + tq;
+                        const int k0 = jx * kChunk + qpiece * E;
+                        const bool live = jx < KC;
 #pragma unroll
                         for (int d = 0; d < E / 2; ++d) {
-                            const uint32_t xd = xv.d[d], gd = b.gv[u].d[d];
+                            const int k = k0 + 2 * d;
+                            const uint32_t xd =
+                                live ? (uint32_t)nrow[k] | ((uint32_t)nrow[k + 1] << 16) : 0u;
+                            const uint32_t gd =
+                                live ? (uint32_t)ngam[k] | ((uint32_t)ngam[k + 1] << 16) : 0u;
                             const float yl = bf16lo((uint32_t)f32_to_bf16(bf16lo(xd) * rn));
                             const float yh = bf16lo((uint32_t)f32_to_bf16(bf16hi(xd) * rn));
                             const uint32_t lo = f32_to_bf16(bf16lo(gd) * yl);
@@ -388,34 +397,51 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
     // ... by fma, the standalone kernel's order. The first 16 of those loads
     // go out before the weight batch: a wave's loads return in order, and
     // the norm's row should not wait behind the weights.
-    float nv[NORM ? 16 : 1];
+    // The row and gamma are read from global memory once per workgroup
+    // (coalesced, by every thread) into LDS; the quantizing lanes take their
+    // slices from there. K <= kNormMaxK.
+    uint16_t nv[NORM ? 16 : 1];
     if constexpr (NORM) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
             const int i = (int)threadIdx.x + e * 256;
-            nv[e] = threadIdx.x < 256 && i < K ? bf16lo((uint32_t)op.x[i]) : 0.0f;
+            nv[e] = threadIdx.x < 256 && i < K ? op.x[i] : (uint16_t)0;
         }
     }
     if (sb < se) issue(b0, sb);
     if constexpr (NORM) {
-        // then the fold of the 256 sums, as fold256_wave0 (its one barrier
-        // also publishes arrive = 0)
+        for (int i = threadIdx.x; i < K; i += WAVES * 64) ngam[i] = args.gamma[i];
+        // then the sum of squares and the fold of the 256 sums, as
+        // fold256_wave0 (its one barrier also publishes the row, gamma and
+        // arrive = 0)
         __shared__ float nred[256];
         float ss = 0.0f;
         if (threadIdx.x < 256) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-                if ((int)threadIdx.x + e * 256 < K) ss = __builtin_fmaf(nv[e], nv[e], ss);
+            for (int e = 0; e < 16; ++e) {
+                const int i = (int)threadIdx.x + e * 256;
+                if (i < K) {
+                    nrow[i] = nv[e];
+                    const float v = bf16lo((uint32_t)nv[e]);
+                    ss = __builtin_fmaf(v, v, ss);
+                }
+            }
             for (int i0 = threadIdx.x + 256 * 16; i0 < K; i0 += 256 * 16) {
-                float v[16];
+                uint16_t v[16];
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int i = i0 + e * 256;
-                    v[e] = i < K ? bf16lo((uint32_t)op.x[i]) : 0.0f;
+                    v[e] = i < K ? op.x[i] : (uint16_t)0;
                 }
 #pragma unroll
-                for (int e = 0; e < 16; ++e)
-                    if (i0 + e * 256 < K) ss = __builtin_fmaf(v[e], v[e], ss);
+                for (int e = 0; e < 16; ++e) {
+                    const int i = i0 + e * 256;
+                    if (i < K) {
+                        nrow[i] = v[e];
+                        const float f = bf16lo((uint32_t)v[e]);
+                        ss = __builtin_fmaf(f, f, ss);
+                    }
+                }
             }
         }
         rn = rms_inv(fold256_every_wave(ss, nred), K, args.eps);

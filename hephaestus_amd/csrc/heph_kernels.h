@@ -79,6 +79,8 @@ void skinny_tune(int waves, int u);
 // inside the kernel (group 128); workgroup 0 also writes q/s. gamma (fused,
 // M = 1 only): x is first RMS-normalized with gamma and eps, as
 // heph_rmsnorm_bf16 rounds it.
+// Longest row the GEMV's RMSNorm prologue holds in LDS (with gamma: 32 KB).
+constexpr int kNormMaxK = 8192;
 hipError_t launch_fp8_gemv(const Fp8Operands& op, bool fused, hipStream_t stream,
                            const LaunchTiming& t, const char** name,
                            const uint16_t* gamma = nullptr, float eps = 0.0f);
