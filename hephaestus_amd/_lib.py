@@ -26,25 +26,26 @@ HEPH_ERR_WORKSPACE = -6
 HEPH_ERR_FLAGS = -7
 HEPH_ERR_DEVICE = -8
 HEPH_ERR_LAUNCH = -9
+HEPH_ERR_UNSUPPORTED = -10
 
 HEPH_DTYPE_BF16 = 0
 HEPH_DTYPE_F32 = 1
 
 FLAG_ADD_RESIDUAL = 0x1
 FLAG_SKIP_QUANT = 0x2
-FLAG_FORCE_SKINNY = 0x4
 FLAG_FORCE_GEMM = 0x8
 FLAG_NO_FUSE = 0x10
 
 SKINNY_MAX_M = 32
 
-TUNE_SKINNY_WAVES = 1
-TUNE_SKINNY_U = 2
-TUNE_GEMV_KS = 3
-TUNE_GEMV_WAVES = 4
-TUNE_GEMV_U = 5
-TUNE_GEMM_BM = 6
-TUNE_BATCH_SPLIT = 7
+
+
+class LaunchOverrides(ctypes.Structure):
+    """heph_launch_overrides: per-call launch-shape overrides (0 = built-in)."""
+    _fields_ = [("gemv_ks", ctypes.c_int), ("gemv_waves", ctypes.c_int),
+                ("gemv_u", ctypes.c_int), ("gemm_bm", ctypes.c_int),
+                ("batch_split", ctypes.c_int)]
+
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
@@ -55,6 +56,8 @@ SIGNATURES = {
     "heph_fp8_quant_weight": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "heph_fp8_linear": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _vp, _sz, _vp, _sz,
                              _i, _i, _i, _i, _i, _vp]),
+    "heph_fp8_linear_with": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _vp, _sz, _vp, _sz,
+                                  _i, _i, _i, _i, _i, _vp, ctypes.POINTER(LaunchOverrides)]),
     "heph_fp8_linear_rmsnorm": (_i, [_vp, _i, _vp, _vp, ctypes.c_float, _vp, _vp, _i, _i, _vp,
                                      _sz, _vp, _sz, _i, _i, _i, _vp]),
     "heph_bf16_linear": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _i, _vp]),
@@ -65,7 +68,6 @@ SIGNATURES = {
     "heph_abi_version": (_i, []),
     "heph_profile_next_launch": (_i, [_vp, _vp]),
     "heph_last_kernel": (ctypes.c_char_p, []),
-    "heph_set_tuning": (_i, [_i, _i]),
     # hephdecode.h
     "heph_embed_fp8": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i, _i, _vp]),
     "heph_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, ctypes.c_float, _vp]),

@@ -1,7 +1,8 @@
 """Builds libhephfp8.so (gfx950 only) in-tree with hipcc.
 
 Each csrc/*.hip file is compiled to an object in parallel, then linked into
-hephaestus_amd/libhephfp8.so. Every HIP compile carries
+hephaestus_amd/libhephfp8.so; bench_csrc/hbm_read.hip (bench.py's plain-read
+measurement kernel) becomes hephaestus_amd/libhephbench.so. Every HIP compile carries
 `-Xclang -target-feature -Xclang -packed-fp32-ops`, which keeps the compiler
 from forming packed fp32 VALU instructions.
 """
@@ -16,6 +17,9 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libhephfp8.so")
+# measurement kernels for bench.py (a plain HBM read); not the product
+BENCH_SRC = os.path.join(PKG, "bench_csrc", "hbm_read.hip")
+BENCH_LIB = os.path.join(PKG, "libhephbench.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -50,8 +54,14 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    tmp = BENCH_LIB + ".tmp"
+    r = subprocess.run([HIPCC, *CFLAGS, "-shared", "-o", tmp, BENCH_SRC], capture_output=True,
+                       text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {BENCH_SRC}:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, BENCH_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {BENCH_LIB}")
     return LIB
 
 

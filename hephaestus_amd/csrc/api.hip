@@ -116,18 +116,40 @@ int heph_fp8_quant_weight(const uint16_t* w_bf16, uint8_t* q, float* scale_inv, 
 
 namespace {
 
+// Launch-shape overrides of one heph_fp8_linear_with call, checked and
+// copied into the operands (no state outlives the call).
+int take_overrides(const heph_launch_overrides* ov, Tuning* t)
+{
+    *t = Tuning{};
+    if (!ov) return HEPH_OK;
+    const int ks = ov->gemv_ks, w = ov->gemv_waves, u = ov->gemv_u, bm = ov->gemm_bm;
+    if (ks != 0 && ks != 1 && ks != 2 && ks != 4 && ks != 8) return HEPH_ERR_FLAGS;
+    if (w != 0 && w != 4 && w != 8 && w != 16) return HEPH_ERR_FLAGS;
+    if (u != 0 && u != 1 && u != 2) return HEPH_ERR_FLAGS;
+    if (bm != 0 && bm != 1 && bm != 64 && bm != 128 && bm != 192 && bm != 256)
+        return HEPH_ERR_FLAGS;
+    if (ov->batch_split < -1 || ov->batch_split > 64) return HEPH_ERR_FLAGS;
+    t->gemv_ks = ks;
+    t->gemv_waves = w;
+    t->gemv_u = u;
+    t->gemm_bm = bm;
+    t->batch_split = ov->batch_split;
+    return HEPH_OK;
+}
+
 // heph_fp8_linear, and with gamma (M = 1, group 128, fused GEMV only) the
 // RMSNorm of x folded into the GEMV's quantization prologue.
 int fp8_linear_impl(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t* w,
                     const float* w_scale, int w_block_n, int w_block_k, uint8_t* q_ws,
                     size_t q_ws_bytes, float* s_ws, size_t s_ws_floats, int M, int N, int K,
-                    int group_k, int flags, void* stream, const uint16_t* gamma, float eps)
+                    int group_k, int flags, void* stream, const uint16_t* gamma, float eps,
+                    const heph_launch_overrides* ov)
 {
-    const int known = HEPH_FLAG_ADD_RESIDUAL | HEPH_FLAG_SKIP_QUANT |
-                      HEPH_FLAG_FORCE_SKINNY | HEPH_FLAG_FORCE_GEMM | HEPH_FLAG_NO_FUSE;
+    const int known = HEPH_FLAG_ADD_RESIDUAL | HEPH_FLAG_SKIP_QUANT | HEPH_FLAG_FORCE_GEMM |
+                      HEPH_FLAG_NO_FUSE;
     if (flags & ~known) return HEPH_ERR_FLAGS;
-    if ((flags & HEPH_FLAG_FORCE_SKINNY) && (flags & HEPH_FLAG_FORCE_GEMM))
-        return HEPH_ERR_FLAGS;
+    Tuning tune;
+    if (take_overrides(ov, &tune) != HEPH_OK) return HEPH_ERR_FLAGS;
     const bool skip_quant = flags & HEPH_FLAG_SKIP_QUANT;
     if (!c || !w || !w_scale || !q_ws || !s_ws) return HEPH_ERR_NULL;
     if (!skip_quant && !x_bf16) return HEPH_ERR_NULL;
@@ -135,7 +157,6 @@ int fp8_linear_impl(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
     if (M < 1 || N < 16 || K < kChunk || N % 16 || K % kChunk) return HEPH_ERR_SHAPE;
     if ((long)M * K > (1L << 40) || (long)N * K > (1L << 40) || (long)M * N > (1L << 40))
         return HEPH_ERR_SHAPE;
-    if ((flags & HEPH_FLAG_FORCE_SKINNY) && M > HEPH_SKINNY_MAX_M) return HEPH_ERR_FLAGS;
     if (group_k != kChunk && group_k != K) return HEPH_ERR_GROUP;
     bool w_block;
     if (w_block_n == kChunk && w_block_k == kChunk) w_block = true;
@@ -166,6 +187,7 @@ int fp8_linear_impl(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
     op.M = M;
     op.N = N;
     op.K = K;
+    op.tune = tune;
     // The part of q_ws past the codes (from the next 256-byte boundary) is
     // scratch for the large-M GEMM's split-K partials.
     const size_t qb = ((size_t)M * (size_t)K + 255) & ~(size_t)255;
@@ -174,29 +196,25 @@ int fp8_linear_impl(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
         op.part_bytes = q_ws_bytes - qb;
     }
 
-    // M <= 32 takes the chunk-slot GEMV unless a kernel is forced; the
-    // skinny kernel serves FORCE_SKINNY (cross-kernel checks) only. Batched
+    // M <= 32 takes the chunk-slot GEMV unless the GEMM is forced. Batched
     // decode (gemv_split_routes: larger M, 1x128 groups) takes quantizer +
     // the 64-column K-split kernel when the caller's scratch holds its
     // partials; otherwise, at 16 <= M <= 32, quantizer + K-split GEMM on
     // large weights when scratch allows (MI355X, gate_up graph-replayed over
     // HBM-streamed weights: M = 16 17.9 us against 19.8 for the GEMV; M = 8
-    // 17.1 against 15.0).
-    const bool skinny = flags & HEPH_FLAG_FORCE_SKINNY;
+    // 17.1 against 15.0). The RMSNorm entry point always takes the GEMV.
     const bool forced_gemm = flags & HEPH_FLAG_FORCE_GEMM;
-    const int bmode = gemv_split_mode();
-    const bool batch_split = !skinny && !forced_gemm && M <= HEPH_SKINNY_MAX_M &&
-                             group_k == kChunk && bmode >= 0 &&
-                             (bmode > 0 || gemv_split_routes(M, N, K)) && gemv_split_ready(op);
-    const bool split_gemm = !batch_split && M >= 16 && (long)N * K >= (32L << 20) &&
+    const int bmode = gamma ? -1 : tune.batch_split;
+    const bool batch_split = !forced_gemm && M <= HEPH_SKINNY_MAX_M && group_k == kChunk &&
+                             bmode >= 0 && (bmode > 0 || gemv_split_routes(M, N, K)) &&
+                             gemv_split_ready(op);
+    const bool split_gemm = !gamma && !batch_split && M >= 16 && (long)N * K >= (32L << 20) &&
                             gemm_splits_ready(op);
-    const bool gemv = !skinny && !forced_gemm && M <= HEPH_SKINNY_MAX_M && !split_gemm &&
-                      !batch_split;
-    if (gamma && !(gemv && M == 1 && group_k == kChunk)) return HEPH_ERR_SHAPE;
+    const bool gemv = !forced_gemm && M <= HEPH_SKINNY_MAX_M && !split_gemm && !batch_split;
+    if (gamma && !(gemv && M == 1 && group_k == kChunk)) return HEPH_ERR_UNSUPPORTED;
     const bool fuse_ok = !skip_quant && !(flags & HEPH_FLAG_NO_FUSE) && group_k == kChunk;
-    const bool fused = fuse_ok && (batch_split || (gemv && gemv_fuses(M, N, K)) ||
-                                   (skinny && M <= kFusedMaxM));
-    if (gamma && !fused) return HEPH_ERR_SHAPE;
+    const bool fused = fuse_ok && (batch_split || (gemv && gemv_fuses(M, N, K)));
+    if (gamma && !fused) return HEPH_ERR_UNSUPPORTED;
     LaunchTiming t = take_timing();
     if (!skip_quant && !fused) {
         // A timed call spans both kernels: the quantizer carries the start
@@ -209,7 +227,6 @@ int fp8_linear_impl(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
     hipError_t e;
     if (batch_split) e = launch_fp8_gemv_split(op, fused, s, t, &g_last_kernel);
     else if (gemv) e = launch_fp8_gemv(op, fused, s, t, &g_last_kernel, gamma, eps);
-    else if (skinny) e = launch_fp8_skinny(op, fused, s, t, &g_last_kernel);
     else e = launch_fp8_gemm(op, s, t, &g_last_kernel);
     return launch_status(e);
 }
@@ -223,7 +240,18 @@ int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
 {
     return fp8_linear_impl(c, c_dtype, x_bf16, w, w_scale, w_block_n, w_block_k, q_ws,
                            q_ws_bytes, s_ws, s_ws_floats, M, N, K, group_k, flags, stream,
-                           nullptr, 0.0f);
+                           nullptr, 0.0f, nullptr);
+}
+
+int heph_fp8_linear_with(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t* w,
+                         const float* w_scale, int w_block_n, int w_block_k, uint8_t* q_ws,
+                         size_t q_ws_bytes, float* s_ws, size_t s_ws_floats, int M, int N,
+                         int K, int group_k, int flags, void* stream,
+                         const heph_launch_overrides* overrides)
+{
+    return fp8_linear_impl(c, c_dtype, x_bf16, w, w_scale, w_block_n, w_block_k, q_ws,
+                           q_ws_bytes, s_ws, s_ws_floats, M, N, K, group_k, flags, stream,
+                           nullptr, 0.0f, overrides);
 }
 
 int heph_fp8_linear_rmsnorm(void* c, int c_dtype, const uint16_t* x_bf16,
@@ -234,10 +262,10 @@ int heph_fp8_linear_rmsnorm(void* c, int c_dtype, const uint16_t* x_bf16,
 {
     if (!gamma_bf16 || !x_bf16) return HEPH_ERR_NULL;
     if (flags & ~HEPH_FLAG_ADD_RESIDUAL) return HEPH_ERR_FLAGS;
-    if (K > kNormMaxK) return HEPH_ERR_SHAPE;
+    if (K > kNormMaxK) return HEPH_ERR_UNSUPPORTED;
     return fp8_linear_impl(c, c_dtype, x_bf16, w, w_scale, w_block_n, w_block_k, q_ws,
                            q_ws_bytes, s_ws, s_ws_floats, 1, N, K, kChunk, flags, stream,
-                           gamma_bf16, eps);
+                           gamma_bf16, eps, nullptr);
 }
 
 int heph_bf16_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint16_t* w_bf16,
@@ -272,6 +300,9 @@ const char* heph_strerror(int status)
     case HEPH_ERR_FLAGS: return "unknown or contradictory flags";
     case HEPH_ERR_DEVICE: return "current HIP device is not gfx950 (MI355X)";
     case HEPH_ERR_LAUNCH: return "HIP kernel launch failed";
+    case HEPH_ERR_UNSUPPORTED:
+        return "shape outside this entry point's limits (fused RMSNorm linear: M = 1, "
+               "group 128, K <= 8192)";
     default: return "unknown status";
     }
 }
@@ -286,50 +317,5 @@ int heph_profile_next_launch(void* start_event, void* stop_event)
 }
 
 const char* heph_last_kernel(void) { return g_last_kernel; }
-
-int heph_set_tuning(int knob, int value)
-{
-    static std::mutex mu;
-    static int waves = 0, u = 0, gks = 0, gwaves = 0, gu = 0;
-    std::lock_guard<std::mutex> lock(mu);
-    switch (knob) {
-    case HEPH_TUNE_SKINNY_WAVES:
-        if (value != 0 && value != 2 && value != 4 && value != 8 && value != 16)
-            return HEPH_ERR_FLAGS;
-        waves = value;
-        break;
-    case HEPH_TUNE_SKINNY_U:
-        if (value != 0 && value != 2 && value != 4) return HEPH_ERR_FLAGS;
-        u = value;
-        break;
-    case HEPH_TUNE_GEMV_KS:
-        if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
-            return HEPH_ERR_FLAGS;
-        gks = value;
-        break;
-    case HEPH_TUNE_GEMV_WAVES:
-        if (value != 0 && value != 4 && value != 8 && value != 16) return HEPH_ERR_FLAGS;
-        gwaves = value;
-        break;
-    case HEPH_TUNE_GEMV_U:
-        if (value != 0 && value != 1 && value != 2) return HEPH_ERR_FLAGS;
-        gu = value;
-        break;
-    case HEPH_TUNE_GEMM_BM:
-        if (value != 0 && value != 1 && value != 64 && value != 128 && value != 192 &&
-            value != 256)
-            return HEPH_ERR_FLAGS;
-        gemm_tune(value);
-        return HEPH_OK;
-    case HEPH_TUNE_BATCH_SPLIT:
-        if (value < -1 || value > 64) return HEPH_ERR_FLAGS;
-        gemv_split_tune(value);
-        return HEPH_OK;
-    default: return HEPH_ERR_FLAGS;
-    }
-    skinny_tune(waves, u);
-    gemv_tune(gks, gwaves, gu);
-    return HEPH_OK;
-}
 
 }  // extern "C"

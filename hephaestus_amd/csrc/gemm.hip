@@ -24,7 +24,6 @@
 //     a grouped (8 tile-rows) order, so A and B tiles are reused from that
 //     XCD's L2.
 #include <algorithm>
-#include <atomic>
 #include <type_traits>
 
 #include "heph_kernels.h"
@@ -750,7 +749,6 @@ hipError_t launch_splitk_reduce(const Fp8Operands& op, hipStream_t stream, const
 
 namespace {
 
-std::atomic<int> g_tune_bm{0};
 int g_cu_count[64];
 
 int cu_count()
@@ -828,9 +826,8 @@ static double gemm_estimate(int M, int N, int K, int bm, long cycles, int s, lon
 // N = 6144 and 19456 and 192 rows for N = 2560, all unsplit; M = 512 runs
 // qkv in 64 rows, o_proj in 64 rows and 3 splits, gate_up in 192 rows and
 // down in 128 rows and 6 splits.
-GemmPlan gemm_plan(int M, int N, int K, bool can_split)
+GemmPlan gemm_plan(int M, int N, int K, bool can_split, int forced)
 {
-    const int forced = g_tune_bm.load(std::memory_order_relaxed);
     const long cus = cu_count();
     const int KC = K / kChunk;
     GemmPlan best{0, 1};
@@ -849,12 +846,10 @@ GemmPlan gemm_plan(int M, int N, int K, bool can_split)
     return best;
 }
 
-void gemm_tune(int bm) { g_tune_bm.store(bm, std::memory_order_relaxed); }
-
 bool gemm_splits_ready(const Fp8Operands& op)
 {
     if (!op.part || op.s_step == 0) return false;
-    const int s = gemm_plan(op.M, op.N, op.K, true).splits;
+    const int s = gemm_plan(op.M, op.N, op.K, true, op.tune.gemm_bm).splits;
     return s > 1 && op.part_bytes >= (size_t)s * op.M * op.N * 4;
 }
 
@@ -873,12 +868,12 @@ hipError_t launch_fp8_gemm(const Fp8Operands& op, hipStream_t stream,
     // 128x128 kernel. (Without splits the two run alike below M = 128; the
     // 256-column kernel is 1.3-2x faster from there on, MI355X.)
     const bool small_offsets = (long)op.M * op.K < (1L << 31) && (long)op.N * op.K < (1L << 31);
-    const bool force_128 = g_tune_bm.load(std::memory_order_relaxed) == 1;
+    const bool force_128 = op.tune.gemm_bm == 1;
     if (small_offsets && !force_128) {
         // K splits when the caller's scratch holds their partials (block or
         // per-channel weights with per-chunk activation scales).
         Fp8Operands o = op;
-        const GemmPlan plan = gemm_plan(o.M, o.N, o.K, gemm_splits_ready(o));
+        const GemmPlan plan = gemm_plan(o.M, o.N, o.K, gemm_splits_ready(o), o.tune.gemm_bm);
         o.splits = plan.splits;
         const bool sk = o.splits > 1;
         switch (plan.bm) {

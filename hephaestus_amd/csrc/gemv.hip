@@ -39,7 +39,6 @@
 //   * the last wave of a workgroup to finish sums the waves' slot partials
 //     in a fixed order (deterministic) and stores bf16 or f32, optionally
 //     adding the residual first (wmma_gfx12.mojo:712-715).
-#include <atomic>
 #include <type_traits>
 
 #include "heph_kernels.h"
@@ -505,10 +504,6 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
 
 namespace {
 
-std::atomic<int> g_tune_ks{0};
-std::atomic<int> g_tune_waves{0};
-std::atomic<int> g_tune_u{0};
-
 template <int WAVES, int KS, int MR, int MT, int U>
 hipError_t launch_ks(const GemvArgs& a, bool fused, hipStream_t stream, const LaunchTiming& t)
 {
@@ -595,21 +590,21 @@ int gemv_rows(int M)
 // 8 steps, else 8 (16 only when forced, for 8 < M <= 16); at M = 1, 2-step
 // batches when each wave has at most 2 steps, else (and for M > 1, whose
 // wider activation tiles need the registers) 1-step batches.
-void gemv_shape(int M, int N, int K, int* ks, int* waves, int* u)
+void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, int* u)
 {
     const int mr = gemv_rows(M);
     const int kmax = mr >= 2 ? 16 / mr : 8;
     const int tiles = N / 16, KC = K / kChunk;
     int k = 1;
     while (k < kmax && tiles * k < 600) k *= 2;
-    const int fk = g_tune_ks.load(std::memory_order_relaxed);
+    const int fk = tune.gemv_ks;
     if (fk) k = fk < kmax ? fk : kmax;
     const int S = (KC + k - 1) / k;
     int w = S <= 8 ? 4 : 8;
-    const int fw = g_tune_waves.load(std::memory_order_relaxed);
+    const int fw = tune.gemv_waves;
     if (fw) w = fw == 16 && (mr != 16 || M > 16) ? 8 : fw;
     int uu = mr == 1 && (S + w - 1) / w <= 2 ? 2 : 1;
-    const int fu = g_tune_u.load(std::memory_order_relaxed);
+    const int fu = tune.gemv_u;
     if (fu) uu = fu;
     if (w == 16) uu = 1;    // two-step batches would not fit 128 VGPRs
     *ks = k;
@@ -623,7 +618,7 @@ hipError_t launch_fp8_gemv(const Fp8Operands& op, bool fused, hipStream_t stream
 {
     GemvArgs a{op, fused, gamma, eps};
     int ks, waves, u;
-    gemv_shape(op.M, op.N, op.K, &ks, &waves, &u);
+    gemv_shape(op.M, op.N, op.K, op.tune, &ks, &waves, &u);
     const int mr = gemv_rows(op.M);
     if (op.M == 1) *name = gamma ? "fp8_gemv_rmsnorm_m1" : fused ? "fp8_gemv_fused_m1" : "fp8_gemv_m1";
     else if (op.M <= 16) *name = fused ? "fp8_gemv_fused_m16" : "fp8_gemv_m16";
@@ -637,13 +632,6 @@ hipError_t launch_fp8_gemv(const Fp8Operands& op, bool fused, hipStream_t stream
         return u == 2 ? launch_wu<4, 2>(a, fused, ks, mr, stream, t)
                       : launch_wu<4, 1>(a, fused, ks, mr, stream, t);
     }
-}
-
-void gemv_tune(int ks, int waves, int u)
-{
-    g_tune_ks.store(ks, std::memory_order_relaxed);
-    g_tune_waves.store(waves, std::memory_order_relaxed);
-    g_tune_u.store(u, std::memory_order_relaxed);
 }
 
 }  // namespace heph

@@ -30,7 +30,6 @@
 //     columns per lane; S splits: fp32 partials [split][M][N] in the
 //     caller's scratch, summed in split order by the large-M GEMM's
 //     reduction kernel.
-#include <atomic>
 
 #include "heph_kernels.h"
 
@@ -40,8 +39,6 @@ namespace {
 
 constexpr int kSplitCols = 64;     // output columns per workgroup (4 waves x 16)
 constexpr int kSplitMaxKB = 8;     // chunks per split at most
-
-std::atomic<int> g_tune_split{0};
 }  // namespace
 
 // Max over each aligned run of 8 lanes (unsigned), left in all 8.
@@ -228,11 +225,10 @@ __global__ __launch_bounds__(256) void fp8_gemv_split_kernel(Fp8Operands op)
 // staging: on MI355X every config shape at M = 8..32 ran fastest at the
 // minimum. An override n > 0 is raised to that minimum and capped at one
 // chunk a split.
-int gemv_split_count(int M, int N, int K)
+int gemv_split_count(int M, int N, int K, int forced)
 {
     (void)M;
     (void)N;
-    const int forced = g_tune_split.load(std::memory_order_relaxed);
     const int KC = K / kChunk;
     const int s_min = (KC + kSplitMaxKB - 1) / kSplitMaxKB;
     const int s = forced > s_min ? forced : s_min;
@@ -244,10 +240,6 @@ size_t gemv_split_bytes(int M, int N, int K)
     const int s = gemv_split_count(M, N, K);
     return s > 1 ? (size_t)s * M * N * 4 : 0;
 }
-
-void gemv_split_tune(int splits) { g_tune_split.store(splits, std::memory_order_relaxed); }
-
-int gemv_split_mode() { return g_tune_split.load(std::memory_order_relaxed); }
 
 // Where the fused split path beats the chunk-slot GEMV (quantization
 // included, HIP-graph replay on MI355X over the config shapes): from
@@ -265,7 +257,7 @@ bool gemv_split_routes(int M, int N, int K)
 bool gemv_split_ready(const Fp8Operands& op)
 {
     if (op.M > 32 || op.s_step == 0) return false;
-    const int s = gemv_split_count(op.M, op.N, op.K);
+    const int s = gemv_split_count(op.M, op.N, op.K, op.tune.batch_split);
     return s == 1 || (op.part && op.part_bytes >= (size_t)s * op.M * op.N * 4);
 }
 
@@ -273,7 +265,7 @@ hipError_t launch_fp8_gemv_split(const Fp8Operands& op, bool fused, hipStream_t 
                                  const LaunchTiming& t, const char** name)
 {
     Fp8Operands o = op;
-    o.splits = gemv_split_count(op.M, op.N, op.K);
+    o.splits = gemv_split_count(op.M, op.N, op.K, op.tune.batch_split);
     const int tiles = (op.N + kSplitCols - 1) / kSplitCols;
     const dim3 grid(tiles * o.splits), block(256);
     *name = o.splits > 1 ? (fused ? "fp8_gemv_split64_fused_splitk" : "fp8_gemv_split64_splitk")

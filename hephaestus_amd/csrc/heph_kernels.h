@@ -32,6 +32,18 @@ hipError_t launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t shme
     return hipGetLastError();
 }
 
+// Per-call launch-shape overrides (heph_fp8_linear_with; 0 = the built-in
+// choice): chunk slots, waves and steps per batch of the chunk-slot GEMV,
+// tile height of the large-M GEMM (1 = the 128x128 kernel), and the
+// batched-decode K-split kernel (-1 never, n > 0 always with n splits).
+struct Tuning {
+    int gemv_ks = 0;
+    int gemv_waves = 0;
+    int gemv_u = 0;
+    int gemm_bm = 0;
+    int batch_split = 0;
+};
+
 // Activation scale addressing shared by the kernels: chunk j of row m uses
 // s[m * s_ld + j * s_step]; group 128: s_ld = K/128, s_step = 1;
 // per-token (group K): s_ld = 1, s_step = 0.
@@ -56,6 +68,7 @@ struct Fp8Operands {
     float* part = nullptr;
     size_t part_bytes = 0;
     int splits = 1;
+    Tuning tune;
 };
 
 hipError_t launch_quant(const uint16_t* x, uint8_t* q, float* scales, int M,
@@ -65,15 +78,6 @@ hipError_t launch_quant(const uint16_t* x, uint8_t* q, float* scales, int M,
 // bf16 [N,K] -> e4m3 codes + f32 scale_inv [ceil(N/128), K/128].
 hipError_t launch_wquant(const uint16_t* w, uint8_t* q, float* scale_inv, int N, int K,
                          hipStream_t stream);
-
-// M <= 32 weight-streaming kernel. fused: quantize x inside the kernel
-// (group 128, M <= kFusedMaxM); workgroup 0 also writes q/s.
-constexpr int kFusedMaxM = 4;
-hipError_t launch_fp8_skinny(const Fp8Operands& op, bool fused, hipStream_t stream,
-                             const LaunchTiming& t, const char** name);
-
-// Overrides for the skinny kernel's launch shape (0 = automatic).
-void skinny_tune(int waves, int u);
 
 // M <= 32 kernel with K-chunk slots in the MFMA rows. fused: quantize x
 // inside the kernel (group 128); workgroup 0 also writes q/s. gamma (fused,
@@ -91,21 +95,19 @@ hipError_t launch_fp8_gemv(const Fp8Operands& op, bool fused, hipStream_t stream
 int gemv_rows(int M);
 // Whether the chunk-slot kernel quantizes x itself for M x N x K (group 128).
 bool gemv_fuses(int M, int N, int K);
-void gemv_shape(int M, int N, int K, int* ks, int* waves, int* u);
-void gemv_tune(int ks, int waves, int u);
+void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, int* u);
 
 // Tiled MFMA GEMM for any M (prefill); reads q/s from the workspace.
 hipError_t launch_fp8_gemm(const Fp8Operands& op, hipStream_t stream,
                            const LaunchTiming& t, const char** name);
 
 // Tile height (64, 128, 192 or 256) and K splits (1 = none) of the
-// large-M GEMM for M x N x K, splits only if can_split; the tile height's
-// override (0 = automatic).
+// large-M GEMM for M x N x K, splits only if can_split; forced_bm fixes
+// the tile height (0 = automatic).
 struct GemmPlan {
     int bm, splits;
 };
-GemmPlan gemm_plan(int M, int N, int K, bool can_split);
-void gemm_tune(int bm);
+GemmPlan gemm_plan(int M, int N, int K, bool can_split, int forced_bm = 0);
 // Scratch bytes for the partials of the split plan (0 when it does not
 // split), and whether op's scratch (part) holds them for a plan of more
 // than one split.
@@ -118,19 +120,18 @@ hipError_t launch_splitk_reduce(const Fp8Operands& op, hipStream_t stream, const
 
 // Batched decode (M <= 32, per-chunk activation scales): 64-column
 // workgroups over K splits, reading q/s from the workspace; partials in
-// op.part when it splits. Split count for M x N x K (override: n > 0
-// forces n), its scratch bytes, and whether op's scratch holds them.
+// op.part when it splits. Split count for M x N x K (forced > 0 raises it
+// to at least that), its scratch bytes (automatic count), and whether op's
+// scratch holds the partials of op's count.
 // fused: quantize x inside (group 128); column tile 0 writes q/s.
 hipError_t launch_fp8_gemv_split(const Fp8Operands& op, bool fused, hipStream_t stream,
                                  const LaunchTiming& t, const char** name);
-int gemv_split_count(int M, int N, int K);
+int gemv_split_count(int M, int N, int K, int forced = 0);
 size_t gemv_split_bytes(int M, int N, int K);
 bool gemv_split_ready(const Fp8Operands& op);
-// Whether M x N x K takes it by default; routing override: 0 automatic,
-// -1 never, n > 0 always (M <= 32, 1x128 groups) with n splits.
+// Whether M x N x K takes it by default (op.tune.batch_split: -1 never,
+// n > 0 always).
 bool gemv_split_routes(int M, int N, int K);
-void gemv_split_tune(int splits);
-int gemv_split_mode();
 
 // bf16 x [M,K] @ w [N,K]^T, f32 accumulation, M <= 32.
 hipError_t launch_bf16_skinny(void* c, bool c_f32, bool residual, const uint16_t* x,

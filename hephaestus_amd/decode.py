@@ -164,6 +164,9 @@ class KVCache:
 
 # ---------------------------------------------------------------- decoder ----
 
+# Longest row heph_fp8_linear_rmsnorm takes (its row and gamma sit in LDS).
+NORM_LINEAR_MAX_K = 8192
+
 class Qwen3Decoder:
     """Holds the activations and workspaces of a single-token decode step."""
 
@@ -195,11 +198,16 @@ class Qwen3Decoder:
 
     def _norm_linear(self, c, gamma, fw: Fp8Weight, K: int, eps: float, rec, li, op):
         """c = rmsnorm(self.x, gamma) @ fw: the norm inside the fused GEMV
-        (heph_fp8_linear_rmsnorm, bit for bit heph_rmsnorm + the linear). A
-        traced step also writes the normalized row to self.xn, for the record
-        only."""
-        HK.linear_fp8_rmsnorm(c, self.x, gamma, eps, fw.w, fw.scale, self.q_ws, self.s_ws,
-                              fw.N, K)
+        (heph_fp8_linear_rmsnorm, bit for bit heph_rmsnorm + the linear) for
+        rows up to NORM_LINEAR_MAX_K; longer rows take heph_rmsnorm, then
+        the linear. A traced step also writes the normalized row to self.xn,
+        for the record only."""
+        if K > NORM_LINEAR_MAX_K:
+            rmsnorm(self.xn, self.x, gamma, eps)
+            self._linear(c, self.xn, fw, K)
+        else:
+            HK.linear_fp8_rmsnorm(c, self.x, gamma, eps, fw.w, fw.scale, self.q_ws, self.s_ws,
+                                  fw.N, K)
         if rec.tracing:
             rmsnorm(self.xn, self.x, gamma, eps)
             rec(li, op, self.xn)

@@ -27,6 +27,8 @@ Scale granularity follows the `scale` tensor's shape:
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib as L
@@ -95,8 +97,16 @@ def quantize_act_fp8_pad(a_fp8, act_scale, x, k, ctx=None, *, group_k=128):
     quantize_act_rows_fp8(a_fp8, act_scale, x, 1, k, ctx, group_k=group_k)
 
 
+def _overrides(tune):
+    """A heph_launch_overrides for the dict `tune` (keys: its field names)."""
+    bad = set(tune) - {f for f, _ in L.LaunchOverrides._fields_}
+    if bad:
+        raise ValueError(f"unknown launch override(s): {sorted(bad)}")
+    return L.LaunchOverrides(**{k: int(v) for k, v in tune.items()})
+
+
 def _linear_fp8(c, a, w, scale, a_fp8_ws, act_scale_ws, m, n, k, ctx, *,
-                do_quantize, add_residual, group_k, flags, where):
+                do_quantize, add_residual, group_k, flags, where, tune=None):
     bn, bk = _weight_block(scale, n, k)
     if group_k is None:
         group_k = 128 if bn == 128 else k
@@ -112,12 +122,15 @@ def _linear_fp8(c, a, w, scale, a_fp8_ws, act_scale_ws, m, n, k, ctx, *,
     if not do_quantize:
         f |= L.FLAG_SKIP_QUANT
     x_ptr = _dev(a, "a", (torch.bfloat16,)) if do_quantize else (a.data_ptr() if a is not None else None)
-    s = L.lib().heph_fp8_linear(
-        _dev(c, "c", tuple(_OUT)), _OUT[c.dtype], x_ptr,
-        _dev(w, "w", _FP8), _dev(scale, "scale", (torch.float32,)), bn, bk,
-        _dev(a_fp8_ws, "a_fp8_ws", _FP8), a_fp8_ws.numel(),
-        _dev(act_scale_ws, "act_scale_ws", (torch.float32,)), act_scale_ws.numel(),
-        m, n, k, group_k, f, _stream(ctx))
+    args = (_dev(c, "c", tuple(_OUT)), _OUT[c.dtype], x_ptr,
+            _dev(w, "w", _FP8), _dev(scale, "scale", (torch.float32,)), bn, bk,
+            _dev(a_fp8_ws, "a_fp8_ws", _FP8), a_fp8_ws.numel(),
+            _dev(act_scale_ws, "act_scale_ws", (torch.float32,)), act_scale_ws.numel(),
+            m, n, k, group_k, f, _stream(ctx))
+    if tune:
+        s = L.lib().heph_fp8_linear_with(*args, ctypes.byref(_overrides(tune)))
+    else:
+        s = L.lib().heph_fp8_linear(*args)
     _check(s, where)
 
 
@@ -142,21 +155,22 @@ def linear_fp8_rmsnorm(c, x, gamma, eps, w, scale, a_fp8_ws, act_scale_ws, n, k,
 
 
 def linear_fp8(c, a, w, scale, a_fp8_ws, act_scale_ws, m, n, k, ctx=None, *,
-               do_quantize=True, group_k=None, flags=0):
+               do_quantize=True, group_k=None, flags=0, tune=None):
     """C = A @ W^T through the W8A8 FP8 path (quantize A, FP8 contraction,
-    scale epilogue). M <= 32 runs the weight-streaming kernel, larger M the
-    MFMA GEMM."""
+    scale epilogue). M <= 32 runs the weight-streaming kernels, larger M the
+    MFMA GEMM. `tune` (measurement and tests): launch-shape overrides of this
+    call, a dict over the fields of heph_launch_overrides."""
     _linear_fp8(c, a, w, scale, a_fp8_ws, act_scale_ws, m, n, k, ctx,
                 do_quantize=do_quantize, add_residual=False, group_k=group_k,
-                flags=flags, where="linear_fp8")
+                flags=flags, where="linear_fp8", tune=tune)
 
 
 def linear_add_residual_fp8(residual, a, w, scale, a_fp8_ws, act_scale_ws, m, n, k,
-                            ctx=None, *, do_quantize=True, group_k=None, flags=0):
+                            ctx=None, *, do_quantize=True, group_k=None, flags=0, tune=None):
     """residual += A @ W^T (f32 add of the bf16 residual, then the cast)."""
     _linear_fp8(residual, a, w, scale, a_fp8_ws, act_scale_ws, m, n, k, ctx,
                 do_quantize=do_quantize, add_residual=True, group_k=group_k,
-                flags=flags, where="linear_add_residual_fp8")
+                flags=flags, where="linear_add_residual_fp8", tune=tune)
 
 
 def gemv_fp8(c, a, w, scale, a_fp8_ws, act_scale_ws, n, k, ctx=None, *,
@@ -196,9 +210,3 @@ def workspace(m: int, k: int, device="cuda", group_k: int = 128, n: int | None =
 def last_kernel() -> str:
     """Name of the main kernel the last call on this thread launched."""
     return L.lib().heph_last_kernel().decode()
-
-
-def set_tuning(knob: int, value: int) -> None:
-    """Override one launch-shape choice process-wide (0 restores the
-    built-in choice); knobs are the TUNE_* constants of _lib."""
-    _check(L.lib().heph_set_tuning(knob, value), "set_tuning")

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define HEPH_ABI_VERSION 1
+#define HEPH_ABI_VERSION 2
 
 /* status codes */
 #define HEPH_OK                 0
@@ -50,6 +50,7 @@ extern "C" {
 #define HEPH_ERR_FLAGS        (-7)  /* unknown or contradictory flags */
 #define HEPH_ERR_DEVICE       (-8)  /* current device is not gfx950 */
 #define HEPH_ERR_LAUNCH       (-9)  /* HIP reported an error at launch */
+#define HEPH_ERR_UNSUPPORTED (-10)  /* valid shape outside this entry point's limits */
 
 /* output dtypes */
 #define HEPH_DTYPE_BF16 0
@@ -58,11 +59,10 @@ extern "C" {
 /* flags for heph_fp8_linear / heph_bf16_linear */
 #define HEPH_FLAG_ADD_RESIDUAL 0x1  /* c += result (c is read, then written) */
 #define HEPH_FLAG_SKIP_QUANT   0x2  /* q_ws / s_ws already hold this x's codes */
-#define HEPH_FLAG_FORCE_SKINNY 0x4  /* use the 16-column M <= 32 kernel (tests) */
 #define HEPH_FLAG_FORCE_GEMM   0x8  /* use the tiled MFMA GEMM (tests) */
 #define HEPH_FLAG_NO_FUSE      0x10 /* quantize in its own kernel (tests) */
 
-/* Largest M served by the weight-streaming kernels (chunk-slot GEMV, skinny). */
+/* Largest M served by the weight-streaming kernels (chunk-slot GEMV, K-split). */
 #define HEPH_SKINNY_MAX_M 32
 
 /*
@@ -120,7 +120,8 @@ int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16,
  * normalized row's codes and scales. Replaces the pair rms_norm + linear_fp8
  * of the reference's decode step (src/hephaestus/forward.mojo:359-615,
  * kernels.mojo:653-762). flags: HEPH_FLAG_ADD_RESIDUAL only; K <= 8192
- * (the row and gamma sit in the workgroup's LDS), else HEPH_ERR_SHAPE.
+ * (the row and gamma sit in the workgroup's LDS), else HEPH_ERR_UNSUPPORTED
+ * (callers with longer rows run heph_rmsnorm, then heph_fp8_linear).
  */
 int heph_fp8_linear_rmsnorm(void* c, int c_dtype, const uint16_t* x_bf16,
                             const uint16_t* gamma_bf16, float eps, const uint8_t* w,
@@ -174,32 +175,36 @@ int heph_profile_next_launch(void* start_event, void* stop_event);
 const char* heph_last_kernel(void);
 
 /*
- * Launch-shape overrides for measurement sweeps (process-wide; 0 restores
- * the built-in choice). No counterpart in the reference.
- *   HEPH_TUNE_SKINNY_WAVES  waves per workgroup of the forced skinny kernel:
- *                           0, 2, 4, 8 or 16
- *   HEPH_TUNE_SKINNY_U      chunks per load batch: 0, 2 or 4
- *   HEPH_TUNE_GEMV_KS       K-chunk slots per MFMA of the M <= 32 chunk-slot
- *                           kernel: 0, 1, 2, 4 or 8 (capped at 16 / rows per
- *                           slot, i.e. 1 for M > 8)
- *   HEPH_TUNE_GEMV_WAVES    its waves per workgroup: 0, 4, 8 or 16 (16 only
- *                           for 8 < M <= 16; 8 is used otherwise)
- *   HEPH_TUNE_GEMV_U        its steps per load batch: 0, 1, 2 (1 with 16 waves)
- *   HEPH_TUNE_GEMM_BM       tile height of the 256-column GEMM: 0, 64, 128,
- *                           192, 256; 1 selects the 128x128 GEMM (otherwise only
- *                           used when M*K or N*K reaches 2^31)
- *   HEPH_TUNE_BATCH_SPLIT   the 64-column K-split kernel for M <= 32 with
- *                           1x128 groups: 0 automatic, -1 never, n in 1..64
- *                           always with n K splits
+ * Launch-shape overrides for one call, for measurement sweeps and the
+ * cross-kernel tests; a zero field keeps the built-in choice. The library
+ * keeps no tuning state: heph_fp8_linear_with is heph_fp8_linear with the
+ * overrides applied to that call only. No counterpart in the reference.
+ *   gemv_ks      K-chunk slots per MFMA of the M <= 32 chunk-slot GEMV:
+ *                1, 2, 4 or 8 (capped at 16 / rows per slot, i.e. 1 for M > 8)
+ *   gemv_waves   its waves per workgroup: 4, 8 or 16 (16 only for
+ *                8 < M <= 16; 8 is used otherwise)
+ *   gemv_u       its steps per load batch: 1 or 2 (1 with 16 waves)
+ *   gemm_bm      tile height of the large-M GEMM: 64, 128, 192, 256; 1 selects
+ *                the 128x128 GEMM (otherwise used only when M*K or N*K
+ *                reaches 2^31)
+ *   batch_split  the 64-column K-split kernel for M <= 32 with 1x128 groups:
+ *                -1 never, n in 1..64 always, with at least n K splits
+ * Values outside these sets give HEPH_ERR_FLAGS.
  */
-#define HEPH_TUNE_SKINNY_WAVES 1
-#define HEPH_TUNE_SKINNY_U     2
-#define HEPH_TUNE_GEMV_KS      3
-#define HEPH_TUNE_GEMV_WAVES   4
-#define HEPH_TUNE_GEMV_U       5
-#define HEPH_TUNE_GEMM_BM      6
-#define HEPH_TUNE_BATCH_SPLIT  7
-int heph_set_tuning(int knob, int value);
+typedef struct heph_launch_overrides {
+    int gemv_ks;
+    int gemv_waves;
+    int gemv_u;
+    int gemm_bm;
+    int batch_split;
+} heph_launch_overrides;
+
+int heph_fp8_linear_with(void* c, int c_dtype, const uint16_t* x_bf16,
+                         const uint8_t* w, const float* w_scale, int w_block_n,
+                         int w_block_k, uint8_t* q_ws, size_t q_ws_bytes,
+                         float* s_ws, size_t s_ws_floats, int M, int N, int K,
+                         int group_k, int flags, void* stream,
+                         const heph_launch_overrides* overrides);
 
 #ifdef __cplusplus
 }

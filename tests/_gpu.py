@@ -32,10 +32,25 @@ def smoke_ints(n: int, seed: int) -> np.ndarray:
     return ((i * 17 + seed * 31) % 17) - 8
 
 
+# Launch-shape overrides that run_linear passes to every call it makes
+# (heph_launch_overrides fields; the library itself keeps no such state).
+TUNE: dict = {}
+
+
+def split_ws(codes: torch.Tensor, M: int, N: int, K: int, splits: int) -> torch.Tensor:
+    """A q_ws holding `codes` (M*K bytes) and room for `splits` fp32 K-split
+    partials of an M x N output past the next 256-byte boundary."""
+    q = torch.zeros(((M * K + 255) // 256) * 256 + splits * M * N * 4, dtype=torch.uint8,
+                    device="cuda")
+    q[: M * K] = codes.reshape(-1)[: M * K]
+    return q
+
+
 def run_linear(qw, sw, x=None, *, M, N, K, group_k=128, out=torch.bfloat16, flags=0,
-               q_ws=None, s_ws=None, residual=None, skip_quant=False):
+               q_ws=None, s_ws=None, residual=None, skip_quant=False, tune=None):
     """Call linear_fp8 (or the residual form) on device copies; returns
-    (output tensor, q_ws, s_ws)."""
+    (output tensor, q_ws, s_ws). tune (or TUNE): launch-shape overrides."""
+    tune = {**TUNE, **(tune or {})} or None
     w_t = dev(qw)
     sw_t = dev(np.ascontiguousarray(sw, np.float32))
     if q_ws is None:
@@ -45,11 +60,12 @@ def run_linear(qw, sw, x=None, *, M, N, K, group_k=128, out=torch.bfloat16, flag
     if residual is not None:
         c = residual.clone()
         HK.linear_add_residual_fp8(c, x_t, w_t, sw_t, q_ws, s_ws, M, N, K,
-                                   do_quantize=not skip_quant, group_k=group_k, flags=flags)
+                                   do_quantize=not skip_quant, group_k=group_k, flags=flags,
+                                   tune=tune)
     else:
         c = torch.zeros(M, N, dtype=out, device="cuda")
         HK.linear_fp8(c, x_t, w_t, sw_t, q_ws, s_ws, M, N, K,
-                      do_quantize=not skip_quant, group_k=group_k, flags=flags)
+                      do_quantize=not skip_quant, group_k=group_k, flags=flags, tune=tune)
     torch.cuda.synchronize()
     return c, q_ws, s_ws
 

@@ -26,8 +26,8 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_version_and_strerror(lib):
-    assert lib.heph_abi_version() == 1
-    for code in range(0, -10, -1):
+    assert lib.heph_abi_version() == 2
+    for code in range(0, -11, -1):
         msg = L.strerror(code)
         assert msg and msg != "unknown status", code
     assert L.strerror(-99) == "unknown status"
@@ -71,8 +71,7 @@ def lin(lib, **kw):
     (dict(sn=19), L.HEPH_ERR_WORKSPACE),
     (dict(M=3, qn=3 * 2560, sn=3), L.HEPH_ERR_WORKSPACE),
     (dict(flags=0x100), L.HEPH_ERR_FLAGS),
-    (dict(flags=L.FLAG_FORCE_GEMM | L.FLAG_FORCE_SKINNY), L.HEPH_ERR_FLAGS),
-    (dict(M=33, flags=L.FLAG_FORCE_SKINNY), L.HEPH_ERR_FLAGS),
+    (dict(flags=0x4), L.HEPH_ERR_FLAGS),
     (dict(c=ODD), L.HEPH_ERR_ALIGN),
     (dict(w=ODD), L.HEPH_ERR_ALIGN),
     (dict(x=ODD), L.HEPH_ERR_ALIGN),
@@ -116,22 +115,44 @@ def test_bf16_rejects(lib):
     assert b(FAKE, 1, FAKE, ODD, 1, 151936, 2560, 0, None) == L.HEPH_ERR_ALIGN
 
 
-def test_set_tuning_validates(lib):
-    ok = [(L.TUNE_SKINNY_WAVES, 16), (L.TUNE_SKINNY_U, 4), (L.TUNE_GEMV_KS, 8),
-          (L.TUNE_GEMV_WAVES, 4), (L.TUNE_GEMV_U, 2), (L.TUNE_GEMM_BM, 192),
-          (L.TUNE_GEMM_BM, 64),
-          (L.TUNE_BATCH_SPLIT, -1), (L.TUNE_BATCH_SPLIT, 64)]
-    bad = [(L.TUNE_SKINNY_WAVES, 3), (L.TUNE_SKINNY_U, 1), (L.TUNE_GEMV_KS, 16),
-           (L.TUNE_GEMV_WAVES, 2), (L.TUNE_GEMV_U, 4), (L.TUNE_GEMM_BM, 96),
-           (L.TUNE_BATCH_SPLIT, -2), (L.TUNE_BATCH_SPLIT, 65), (99, 0)]
-    try:
-        for knob, v in ok:
-            assert lib.heph_set_tuning(knob, v) == L.HEPH_OK, (knob, v)
-        for knob, v in bad:
-            assert lib.heph_set_tuning(knob, v) == L.HEPH_ERR_FLAGS, (knob, v)
-    finally:
-        for knob, _ in ok:
-            assert lib.heph_set_tuning(knob, 0) == L.HEPH_OK
+def with_overrides(lib, **ov):
+    o = L.LaunchOverrides(**ov)
+    return lib.heph_fp8_linear_with(FAKE, 0, FAKE, FAKE, FAKE, 128, 128, FAKE, 1 << 30, FAKE,
+                                    1 << 30, 1, 256, 2560, 128, 0, None, ctypes.byref(o))
+
+
+def test_launch_overrides_validate(lib):
+    # heph_fp8_linear_with checks every override before anything else; a
+    # valid set leaves the call to the device check (no GPU here).
+    ok = [dict(gemv_ks=8), dict(gemv_waves=4), dict(gemv_waves=16), dict(gemv_u=2),
+          dict(gemm_bm=192), dict(gemm_bm=64), dict(gemm_bm=1), dict(batch_split=-1),
+          dict(batch_split=64), dict()]
+    bad = [dict(gemv_ks=16), dict(gemv_ks=3), dict(gemv_waves=2), dict(gemv_u=4),
+           dict(gemm_bm=96), dict(batch_split=-2), dict(batch_split=65)]
+    for ov in ok:
+        assert with_overrides(lib, **ov) != L.HEPH_ERR_FLAGS, ov
+    for ov in bad:
+        assert with_overrides(lib, **ov) == L.HEPH_ERR_FLAGS, ov
+    # a NULL overrides pointer is the plain call
+    assert lib.heph_fp8_linear_with(FAKE, 0, FAKE, FAKE, FAKE, 128, 128, FAKE, 1 << 30, FAKE,
+                                    1 << 30, 1, 256, 2560, 128, 0, None, None) == lin(lib)
+
+
+def test_library_keeps_no_tuning_state(lib):
+    # the process-wide setter of earlier versions is gone
+    assert not hasattr(lib, "heph_set_tuning")
+
+
+def test_rmsnorm_linear_rejects(lib):
+    f = lib.heph_fp8_linear_rmsnorm
+    args = lambda K, flags=0, gamma=FAKE: (FAKE, 0, FAKE, gamma, 1e-6, FAKE, FAKE, 128, 128,
+                                           FAKE, 1 << 30, FAKE, 1 << 30, 256, K, flags, None)
+    # rows longer than the fused norm's LDS row (8192) are refused before any
+    # device work, with their own status
+    assert f(*args(8320)) == L.HEPH_ERR_UNSUPPORTED
+    assert f(*args(2560, flags=L.FLAG_SKIP_QUANT)) == L.HEPH_ERR_FLAGS
+    assert f(*args(2560, gamma=None)) == L.HEPH_ERR_NULL
+    assert f(*args(8192)) in (L.HEPH_ERR_DEVICE, L.HEPH_OK)
 
 
 def test_profile_hook_and_last_kernel(lib):

@@ -8,10 +8,15 @@ between the GPU and host math libraries: at least 99% of outputs
 identical, the rest within one bf16 step. The FP8 linears are within the
 linear path's tolerance (MFMA sums are not fp32-exact). End to end, every
 op of every layer is recomputed by the oracle from the GPU's own inputs
-and held to those bars, and the argmax is compared on identical logits;
-the free-running step is held to the oracle's own sensitivity.
+and held to those bars, and the argmax is compared on identical logits.
+The free-running step must give the oracle's token unless the oracle's own
+top-2 gap is below its measured sensitivity (a named near-tie exception,
+recorded with its numbers under gpurun_out/test_records/).
 """
+import json
+import os
 import time
+import warnings
 
 import numpy as np
 import pytest
@@ -65,7 +70,8 @@ def test_embed_bit_exact():
 
 
 @pytest.mark.parametrize("N,K,scale,out", [(6144, 2560, 1.0, "bf16"), (19456, 2560, 40.0, "bf16"),
-                                           (2560, 4224, 1e-3, "f32"), (4096, 1152, 1.0, "f32")])
+                                           (2560, 4224, 1e-3, "f32"), (4096, 1152, 1.0, "f32"),
+                                           (2560, 8192, 3.0, "bf16")])
 def test_fused_rmsnorm_linear_bit_exact(N, K, scale, out):
     # heph_fp8_linear_rmsnorm (the norm inside the fused M = 1 GEMV) gives
     # the bits of heph_rmsnorm followed by heph_fp8_linear, leaves the same
@@ -321,7 +327,27 @@ def op_by_op(cfg, ctx, token, seed):
     print(f"op-by-op replay done {time.time() - t0:.1f}s", flush=True)
 
 
-def free_running(cfg, ctx, token, seed):
+RECORD_DIR = os.environ.get("HEPH_TEST_RECORDS", "gpurun_out/test_records")
+
+
+def record(name: str, data: dict) -> None:
+    """Write a test's observations as JSON under RECORD_DIR and raise them as
+    a warning, so that a quiet (-q) pytest run still shows them."""
+    os.makedirs(RECORD_DIR, exist_ok=True)
+    with open(os.path.join(RECORD_DIR, name + ".json"), "w") as f:
+        json.dump(data, f, indent=1, sort_keys=True)
+    warnings.warn(f"{name}: " + json.dumps(data, sort_keys=True))
+
+
+def free_running(cfg, ctx, token, seed, name):
+    """The north star's end-to-end check: the GPU's free-running greedy token
+    must equal the oracle's. The one named exception is a near-tie the
+    oracle itself cannot resolve: its bf16 top-2 gap below its own measured
+    sensitivity (the largest logit change when one embedding block scale
+    moves by one bf16 step, 2^-8, i.e. 128 inputs by at most one bf16 step
+    each). Then the GPU's token must still be one the oracle ranks within
+    that sensitivity of its top logit. The observations are recorded
+    either way."""
     w, kv = setup_model(cfg, ctx, seed)
     kvh = DEC.host_kv(kv)
     dec_ = DEC.Qwen3Decoder(w, kv)
@@ -329,28 +355,28 @@ def free_running(cfg, ctx, token, seed):
     g = dec_.logits[0].cpu().numpy().astype(np.float64)
     model = DEC.host_model(w)
     c, c_idx = O.decode_step(model, {k: v.copy() for k, v in kvh.items()}, token, ctx)
-    # the oracle's own sensitivity: the same step with one embedding block
-    # scale raised by a bf16 step (2^-8): the token's first 128 embedding
-    # values move by at most one bf16 step each
     m2 = dict(model)
     m2["embed_scale"] = model["embed_scale"].copy()
     m2["embed_scale"][token // 128, 0] *= np.float32(1 + 2.0 ** -8)
-    p, _ = O.decode_step(m2, {k: v.copy() for k, v in kvh.items()}, token, ctx)
+    p, p_idx = O.decode_step(m2, {k: v.copy() for k, v in kvh.items()}, token, ctx)
     c = c.astype(np.float64)
     err, sens = np.abs(g - c).max(), np.abs(p.astype(np.float64) - c).max()
     cb = f32(bf16_np(c))
     order = np.argsort(-cb, kind="stable")
-    gap = cb[order[0]] - cb[order[1]]
-    print(f"free-running: argmax gpu {g_idx} oracle {c_idx}; |gpu - oracle| {err:.3e}, "
-          f"oracle sensitivity {sens:.3e}, max|logit| {np.abs(c).max():.3e}, "
-          f"oracle top-2 gap {gap:.3e}", flush=True)
-    assert err <= 4 * max(sens, 1e-3 * np.abs(c).max()), (err, sens)
-    if gap > 2 * err:
-        assert g_idx == c_idx
+    gap = float(cb[order[0]] - cb[order[1]])
+    near_tie = gap < sens
+    obs = {"argmax_gpu": g_idx, "argmax_oracle": c_idx, "argmax_oracle_perturbed": int(p_idx),
+           "oracle_top2_gap": gap, "oracle_sensitivity": float(sens),
+           "gpu_vs_oracle_max_abs": float(err), "max_abs_logit": float(np.abs(c).max()),
+           "match": g_idx == c_idx, "named_exception_near_tie": bool(near_tie and g_idx != c_idx),
+           "gpu_rank_in_oracle": int(np.flatnonzero(order == g_idx)[0]),
+           "oracle_logit_gap_to_gpu_pick": float(cb[c_idx] - cb[g_idx]),
+           "layers": cfg.n_layers, "context": ctx, "token": token, "seed": seed}
+    record(name, obs)
+    if not near_tie:
+        assert g_idx == c_idx, obs
     else:
-        # a near-tie within the chaotic envelope: the GPU's pick must be one
-        # of the oracle's candidates inside it
-        assert cb[c_idx] - cb[g_idx] <= 2 * err, (g_idx, c_idx, gap, err)
+        assert g_idx == c_idx or cb[c_idx] - cb[g_idx] <= sens, obs
 
 
 SMALL = Qwen3Config(vocab=4096, hidden=512, n_layers=3, n_heads=4, n_kv_heads=2, head_dim=128,
@@ -361,8 +387,18 @@ def test_decode_small_model_op_by_op():
     op_by_op(SMALL, ctx=300, token=1234, seed=11)
 
 
+def test_decode_wide_hidden_takes_separate_norm():
+    # hidden 8320 is past the fused norm linear's 8192-element LDS row: the
+    # decoder runs heph_rmsnorm, then the linear, for qkv, gate_up and the
+    # lm_head, and every op still matches the oracle
+    wide = Qwen3Config(vocab=512, hidden=8320, n_layers=1, n_heads=2, n_kv_heads=1,
+                       head_dim=128, inter=256)
+    assert wide.hidden > DEC.NORM_LINEAR_MAX_K
+    op_by_op(wide, ctx=40, token=77, seed=21)
+
+
 def test_decode_small_model_free_running():
-    free_running(SMALL, ctx=300, token=1234, seed=11)
+    free_running(SMALL, ctx=300, token=1234, seed=11, name="small_free_running_argmax")
 
 
 def test_decode_qwen3_4b_config4_op_by_op():
@@ -374,4 +410,4 @@ def test_decode_qwen3_4b_config4_op_by_op():
 
 
 def test_decode_qwen3_4b_config4_free_running():
-    free_running(Qwen3Config(), ctx=4096, token=12345, seed=4)
+    free_running(Qwen3Config(), ctx=4096, token=12345, seed=4, name="config4_free_running_argmax")

@@ -4,7 +4,7 @@ Bars: activation codes and scales bit-exact; exact-integer inputs give
 bit-exact bf16 outputs; random inputs stay within the north star's
 max-abs-rel 1e-2 of the oracle's fp32-accumulated dequant-matmul (and,
 element-wise, within bf16 output rounding plus 1e-3 of the row scale);
-kernel variants that must agree (skinny vs GEMM, fused vs separate
+kernel variants that must agree (GEMV vs K-split vs GEMM, fused vs separate
 quantization, fused residual vs separate add) agree bit for bit.
 """
 import os
@@ -16,8 +16,9 @@ import torch
 from hephaestus_amd import _lib as L
 from hephaestus_amd import kernels as HK
 from oracle import oracle as O
+from tests import _gpu as T
 from tests._gpu import (bf16_of, dev, f32_of_bf16, host_bf16, max_abs_rel, run_linear,
-                        smoke_codes)
+                        smoke_codes, split_ws)
 
 pytestmark = pytest.mark.gpu
 
@@ -46,9 +47,9 @@ def check_close(got_bf16: np.ndarray, ref_f32: np.ndarray, what: str):
 def gemv_only():
     """Route M <= 32 to the chunk-slot GEMV (the 64-column K-split kernel
     off) for tests that target the GEMV itself."""
-    HK.set_tuning(L.TUNE_BATCH_SPLIT, -1)
+    T.TUNE["batch_split"] = -1
     yield
-    HK.set_tuning(L.TUNE_BATCH_SPLIT, 0)
+    T.TUNE.clear()
 
 
 # ---------------------------------------------------------------- KATs ----
@@ -66,12 +67,12 @@ def test_mfma_all_ones_kat():
     s = torch.ones(M, dtype=torch.float32, device="cuda")
     w = dev(np.full((N, K), 0x38, np.uint8))
     for sw in (torch.ones(1, 1, device="cuda"), torch.ones(N, 1, device="cuda")):
-        for flags in (0, L.FLAG_FORCE_SKINNY, L.FLAG_FORCE_GEMM):
+        for flags, tune in ((0, None), (0, {"batch_split": 1}), (L.FLAG_FORCE_GEMM, None)):
             c = torch.zeros(M, N, dtype=torch.float32, device="cuda")
             HK.linear_fp8(c, None, w, sw, q, s, M, N, K, do_quantize=False, group_k=K,
-                          flags=flags)
+                          flags=flags, tune=tune)
             torch.cuda.synchronize()
-            assert torch.all(c == 128.0), (flags, c)
+            assert torch.all(c == 128.0), (flags, tune, c)
 
 
 def test_kat_1280():
@@ -191,13 +192,13 @@ def test_quant_nan_and_inf_groups(M):
     qw, sw = O.gen_weight(91, N, K)
     try:
         for ks in ((1, 2, 4, 8) if M == 1 else (0,)):
-            HK.set_tuning(L.TUNE_GEMV_KS, ks)
+            T.TUNE["gemv_ks"] = ks
             _, q_ws, s_ws = run_linear(qw, sw, x, M=M, N=N, K=K)
             assert HK.last_kernel().startswith("fp8_gemv_fused"), HK.last_kernel()
             assert np.array_equal(s_ws.cpu().numpy().reshape(so.shape), so), ks
             assert codes_match(q_ws.cpu().numpy().reshape(qo.shape), qo), ks
     finally:
-        HK.set_tuning(L.TUNE_GEMV_KS, 0)
+        T.TUNE.clear()
 
 
 # ------------------------------------------------ exact-integer parity ----
@@ -220,12 +221,19 @@ def test_exact_integer_bit_exact(M, N, K):
     # |sum| <= 64 K / 16 on a 1/16 grid: exact in f32 in any order
     ref = (ia.astype(np.float64) @ iw.astype(np.float64).T) * 0.0625 * 2.0 ** -5
     want = bf16_of(ref.astype(np.float32))
-    forced = ((L.FLAG_FORCE_SKINNY,) if M <= 32 else ()) + (L.FLAG_FORCE_GEMM,)
-    for flags in ((0,) if M <= 32 else ()) + forced:
+    codes = dev(qa.reshape(-1))
+    # the chunk-slot GEMV, the 64-column K-split kernel (with room for its
+    # partials) and the GEMM for M <= 32; the GEMM beyond
+    variants = [(0, {"batch_split": -1}, codes),
+                (0, {"batch_split": 1}, split_ws(codes, M, N, K, -(-(K // 128) // 8)))] \
+        if M <= 32 else []
+    for flags, tune, q in variants + [(L.FLAG_FORCE_GEMM, None, codes)]:
         c, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, flags=flags, skip_quant=True,
-                             q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
+                             q_ws=q, s_ws=dev(sa), tune=tune)
+        if tune and tune["batch_split"] > 0:
+            assert HK.last_kernel().startswith("fp8_gemv_split64"), HK.last_kernel()
         got = host_bf16(c)
-        assert np.array_equal(got, want), (flags, np.argwhere(got != want)[:5].tolist())
+        assert np.array_equal(got, want), (flags, tune, np.argwhere(got != want)[:5].tolist())
 
 
 @pytest.mark.parametrize("M,N,K", [
@@ -252,7 +260,7 @@ def test_reference_smoke_cross_kernel(M, N, K):
         ref = (acc * np.float32(0.02)) * np.float32(0.01)
     want = bf16_of(np.float32([ref]))[0]
     outs = []
-    for flags in (0, L.FLAG_FORCE_SKINNY, L.FLAG_FORCE_GEMM):
+    for flags in (0, L.FLAG_FORCE_GEMM):
         c, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, group_k=K, flags=flags,
                              skip_quant=True, q_ws=dev(qa), s_ws=dev(sa))
         outs.append(host_bf16(c))
@@ -270,13 +278,12 @@ def test_reference_granularity_random_cross_kernel():
     w = O.gen_normal(32, N * K, 0.0, 0.02).reshape(N, K)
     qw, sw = O.quant_weight(w, 1, K)
     outs = []
-    for flags in (0, L.FLAG_FORCE_SKINNY, L.FLAG_FORCE_GEMM):
+    for flags in (0, L.FLAG_FORCE_GEMM):
         c, _, _ = run_linear(qw, sw, x, M=M, N=N, K=K, group_k=K, flags=flags)
         outs.append(host_bf16(c))
     ref = O.quant_linear(x, qw, sw, group_k=K, bn=1, bk=K)
     check_close(outs[0], ref, "per-channel chunk-slot")
-    check_close(outs[1], ref, "per-channel skinny")
-    check_close(outs[2], ref, "per-channel gemm")
+    check_close(outs[1], ref, "per-channel gemm")
 
 
 @pytest.mark.parametrize("N,K", [(16, 128), (48, 384), (2560, 1152), (2560, 9728)])
@@ -304,9 +311,9 @@ def test_gemv_every_launch_shape(N, K):
         for ks in (1, 2, 4, 8):
             for waves in (4, 8):
                 for u in (1, 2):
-                    HK.set_tuning(L.TUNE_GEMV_KS, ks)
-                    HK.set_tuning(L.TUNE_GEMV_WAVES, waves)
-                    HK.set_tuning(L.TUNE_GEMV_U, u)
+                    T.TUNE["gemv_ks"] = ks
+                    T.TUNE["gemv_waves"] = waves
+                    T.TUNE["gemv_u"] = u
                     cfg = (ks, waves, u)
                     c, _, _ = run_linear(qw, sw, None, M=1, N=N, K=K, skip_quant=True,
                                          q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
@@ -323,8 +330,7 @@ def test_gemv_every_launch_shape(N, K):
                     pf, _, _ = run_linear(cq, cs, x, M=1, N=N, K=K)
                     check_close(host_bf16(pf), ref_bc, f"per-channel fused {cfg}")
     finally:
-        for knob in (L.TUNE_GEMV_KS, L.TUNE_GEMV_WAVES, L.TUNE_GEMV_U):
-            HK.set_tuning(knob, 0)
+        T.TUNE.clear()
 
 
 def gemv_shapes(M):
@@ -372,9 +378,9 @@ def test_gemv_rows_every_launch_shape(M, N, K):
     try:
         for cfg in gemv_shapes(M):
             ks, waves, u = cfg
-            HK.set_tuning(L.TUNE_GEMV_KS, ks)
-            HK.set_tuning(L.TUNE_GEMV_WAVES, waves)
-            HK.set_tuning(L.TUNE_GEMV_U, u)
+            T.TUNE["gemv_ks"] = ks
+            T.TUNE["gemv_waves"] = waves
+            T.TUNE["gemv_u"] = u
             c, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, skip_quant=True,
                                  q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
             assert HK.last_kernel() == plain
@@ -393,8 +399,7 @@ def test_gemv_rows_every_launch_shape(M, N, K):
             pf, _, _ = run_linear(cq, cs, x, M=M, N=N, K=K)
             check_close(host_bf16(pf), ref_bc, f"per-channel {cfg}")
     finally:
-        for knob in (L.TUNE_GEMV_KS, L.TUNE_GEMV_WAVES, L.TUNE_GEMV_U):
-            HK.set_tuning(knob, 0)
+        T.TUNE.clear()
 
 
 # ----------------------------------------------------- random parity ----
@@ -451,6 +456,34 @@ def test_prefill_m4096_sampled_rows():
     assert np.array_equal(q_ws.cpu().numpy().reshape(M, K), qo)
     ref = O.linear(qo[rows], so[rows], qw, sw)
     check_close(host_bf16(c)[rows], ref, "gate_up M=4096 rows")
+
+
+CONFIG_SHAPES = ["qkv", "o_proj", "gate_up", "down"]
+
+
+@pytest.mark.parametrize("M", [2, 4, 8, 16, 32, 512, 4096])
+@pytest.mark.parametrize("name", CONFIG_SHAPES)
+def test_config_matrix_vs_oracle(M, name):
+    # Every configs[2] and configs[3] case (M x the config-1 shapes) on the
+    # route a caller with a split-capable workspace gets (the bench's
+    # route): within the tolerance of the oracle, every activation code and
+    # scale bit-exact. configs[3] carries the 0.1% x50 outliers. M = 4096 is
+    # compared on 32 sampled rows (rows of C are independent).
+    N, K = SHAPES[name]
+    x = O.gen_act_bf16(400 + M, M, K, outlier_p=1e-3 if M >= 512 else 0.0)
+    qw, sw = O.gen_weight(1000 + N + K, N, K)
+    q_ws, s_ws = HK.workspace(M, K, n=N)
+    c, q_ws, s_ws = run_linear(qw, sw, x, M=M, N=N, K=K, q_ws=q_ws, s_ws=s_ws)
+    kernel = HK.last_kernel()
+    qo, so = O.quant_act(x, 128)
+    assert np.array_equal(q_ws[: M * K].cpu().numpy().reshape(M, K), qo), kernel
+    assert np.array_equal(s_ws[: M * (K // 128)].cpu().numpy().reshape(M, K // 128), so), kernel
+    if M == 4096:
+        rows = np.sort(np.random.default_rng(M + N).choice(M, 32, replace=False))
+        check_close(host_bf16(c)[rows], O.linear(qo[rows], so[rows], qw, sw),
+                    f"{name} M={M} rows ({kernel})")
+    else:
+        check_close(host_bf16(c), O.linear(qo, so, qw, sw), f"{name} M={M} ({kernel})")
 
 
 # ------------------------------------------------ variant equivalence ----
@@ -585,7 +618,7 @@ def test_fused_gemv_every_bf16_amax():
     sw = np.ones((1, K // 128), np.float32)
     try:
         for ks in (1, 2, 4, 8):
-            HK.set_tuning(L.TUNE_GEMV_KS, ks)
+            T.TUNE["gemv_ks"] = ks
             _, q_ws, s_ws = run_linear(qw, sw, x, M=1, N=N, K=K)
             assert HK.last_kernel() == "fp8_gemv_fused_m1", HK.last_kernel()
             sg = s_ws.cpu().numpy().reshape(so.shape)
@@ -593,7 +626,7 @@ def test_fused_gemv_every_bf16_amax():
             assert bad.size == 0, (ks, bad[:4], sg.reshape(-1)[bad[:4]], so.reshape(-1)[bad[:4]])
             assert np.array_equal(q_ws.cpu().numpy().reshape(qo.shape), qo), ks
     finally:
-        HK.set_tuning(L.TUNE_GEMV_KS, 0)
+        T.TUNE.clear()
 
 
 @pytest.mark.parametrize("N,K", [(256, 384), (300, 2560), (19456, 2560)])
@@ -653,9 +686,9 @@ def test_graph_capture_replays_match_eager():
 @pytest.fixture(params=[64, 128, 192, 256])
 def tile_m(request):
     """Force the large-M kernel's tile height for one test."""
-    HK.set_tuning(L.TUNE_GEMM_BM, request.param)
+    T.TUNE["gemm_bm"] = request.param
     yield request.param
-    HK.set_tuning(L.TUNE_GEMM_BM, 0)
+    T.TUNE.clear()
 
 
 @pytest.mark.parametrize("mode", ["block", "channel_token", "channel_g128"])
@@ -781,7 +814,7 @@ def test_gemm_128x128_fallback(mode, M):
     # The 128x128 GEMM serves operands past 32-bit offsets; forced here on
     # small shapes: random data within the tolerance in every scale mode,
     # exact-integer lattices bit for bit, residual and f32 output.
-    HK.set_tuning(L.TUNE_GEMM_BM, 1)
+    T.TUNE["gemm_bm"] = 1
     try:
         N, K = 400, 1152
         x = O.gen_act_bf16(110 + M, M, K, outlier_p=1e-3)
@@ -807,7 +840,7 @@ def test_gemm_128x128_fallback(mode, M):
         assert HK.last_kernel() == "fp8_gemm_128x128"
         assert np.array_equal(host_bf16(c), bf16_of(exact.astype(np.float32)))
     finally:
-        HK.set_tuning(L.TUNE_GEMM_BM, 0)
+        T.TUNE.clear()
 
 
 @pytest.mark.parametrize("M,N,K", [(512, 2560, 4096), (256, 2560, 9728), (384, 1040, 4224)])
@@ -851,14 +884,14 @@ def test_batched_decode_split_gemm_route(M, name):
     qo, _ = O.quant_act(x, 128)
     q_ws, s_ws = HK.workspace(M, K, n=N)
     try:
-        HK.set_tuning(L.TUNE_BATCH_SPLIT, -1)
+        T.TUNE["batch_split"] = -1
         c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K, q_ws=q_ws, s_ws=s_ws)
         big = N * K >= 32 << 20
         assert HK.last_kernel().startswith("fp8_gemm") == big, HK.last_kernel()
         check_close(host_bf16(c), ref, f"{name} M={M}")
         assert np.array_equal(q_ws[: M * K].cpu().numpy().reshape(M, K), qo)
     finally:
-        HK.set_tuning(L.TUNE_BATCH_SPLIT, 0)
+        T.TUNE.clear()
     c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K, q_ws=q_ws, s_ws=s_ws)
     routed = (M >= 24 and N * K < 32 << 20) or K >= 8192
     assert HK.last_kernel().startswith("fp8_gemv_split64") == routed, HK.last_kernel()
@@ -880,7 +913,7 @@ def test_batch_split_kernel_config_shapes(M, name):
     routed = M >= 24 or (M >= 12 and K >= 8192)
     outs = []
     try:
-        HK.set_tuning(L.TUNE_BATCH_SPLIT, 0 if routed else 1)
+        T.TUNE["batch_split"] = 0 if routed else 1
         if not routed:
             q_ws = torch.zeros(((M * K + 255) // 256) * 256 + 64 * M * N * 4, dtype=torch.uint8,
                                device="cuda")
@@ -889,7 +922,7 @@ def test_batch_split_kernel_config_shapes(M, name):
             assert HK.last_kernel().startswith("fp8_gemv_split64_fused"), HK.last_kernel()
             outs.append(host_bf16(c))
     finally:
-        HK.set_tuning(L.TUNE_BATCH_SPLIT, 0)
+        T.TUNE.clear()
     assert np.array_equal(outs[0], outs[1])
     check_close(outs[0], O.quant_linear(x, qw, sw), f"{name} M={M}")
     qo, _ = O.quant_act(x, 128)
@@ -911,7 +944,7 @@ def test_batch_split_kernel_forced_splits_ragged(M, kc, splits):
     qw, sw = O.gen_weight(2000 + splits, N, K)
     ref = O.quant_linear(x, qw, sw)
     try:
-        HK.set_tuning(L.TUNE_BATCH_SPLIT, splits)
+        T.TUNE["batch_split"] = splits
         q_ws, s_ws = HK.workspace(M, K, n=N)
         need = eff * M * N * 4 + (-(-M * K // 256)) * 256
         if q_ws.numel() < need:
@@ -941,7 +974,7 @@ def test_batch_split_kernel_forced_splits_ragged(M, kc, splits):
         check_close(host_bf16(c), O.quant_linear(x, qw, swc, bn=1, bk=K),
                     f"per-channel M={M} splits={splits}")
     finally:
-        HK.set_tuning(L.TUNE_BATCH_SPLIT, 0)
+        T.TUNE.clear()
 
 
 @pytest.mark.parametrize("out,resid", [("bf16", False), ("f32", True)])
