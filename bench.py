@@ -52,19 +52,66 @@ LM_HEAD = ("lm_head", 151936, 2560)
 
 TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                "fp8_gemv_m1_pmc_traffic.md")
+PREFILL_TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                                       "fp8_gemm_m4096_pmc_traffic.md")
 
 
-def profiled_traffic():
+def profiled_traffic(path=TRAFFIC_PROFILE):
     """HBM bytes per step measured by the committed rocprofv3 PMC summary
     (FETCH_SIZE + WRITE_SIZE, calibrated by a copy of known size), or None."""
     try:
-        with open(TRAFFIC_PROFILE) as f:
+        with open(path) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_step:"):
                     return int(line.split(":", 1)[1])
     except OSError:
         pass
     return None
+
+
+BENCH_LIB = os.path.join(os.path.dirname(os.path.abspath(__file__)), "hephaestus_amd",
+                         "libhephbench.so")
+
+
+def achievable_read(sizes, timer_graph_calls=20):
+    """The plain-read denominator: graph-replayed time of a streaming read
+    (hephaestus_amd/bench_csrc/hbm_read.hip) of each size in bytes, every
+    call on the next window of a 1 GiB buffer so that the windows rotate
+    past the 256 MB Infinity Cache as the GEMV's weight copies do; the best
+    of three grid sizes. Returns {bytes: {"us", "GBs", "blocks"}}."""
+    import ctypes
+    import torch
+    lib = ctypes.CDLL(BENCH_LIB)
+    lib.heph_bench_read.restype = ctypes.c_int
+    lib.heph_bench_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                    ctypes.c_void_p, ctypes.c_void_p]
+    pool = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    pool.fill_(1)
+    sink = torch.empty(1 << 16, dtype=torch.int32, device="cuda")
+    out = {}
+    for size in sizes:
+        size = (size + 4095) // 4096 * 4096
+        best = None
+        for blocks in (1024, 2048, 4096):
+            slots = max(1, (1 << 30) // size)
+            it = [0]
+
+            def run(size=size, blocks=blocks, slots=slots, it=it):
+                off = (it[0] % slots) * size
+                it[0] += 1
+                st = lib.heph_bench_read(pool.data_ptr() + off, size, blocks, sink.data_ptr(),
+                                         torch.cuda.current_stream().cuda_stream)
+                if st:
+                    raise RuntimeError(f"heph_bench_read failed: {st}")
+            run()
+            ms = graph_call_ms(run, timer_graph_calls if size < (256 << 20) else 4)
+            if best is None or ms < best[0]:
+                best = (ms, blocks)
+        ms, blocks = best
+        out[size] = {"us": round(ms * 1e3, 3), "GBs": round(size / (ms * 1e-3) / 1e9, 1),
+                     "blocks": blocks}
+    del pool
+    return out
 
 
 def fp8_bytes(M, N, K):
@@ -115,6 +162,12 @@ def prefill_pass(steps):
         print(f"prefill-pass {name} M={M} N={N} K={K} kernel={HK.last_kernel()} "
               f"launches={100 + steps} (the last {steps} are the measured ones)", flush=True)
         del lin
+    a = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print("prefill-pass copy 268435456 bytes x3", flush=True)
 
 
 def decode_pass(steps):
@@ -315,8 +368,30 @@ def main():
     kern_ms = sum(durs)
     achieved = step_bytes * args.steps / (kern_ms * 1e-3) / 1e9
 
+    # each shape alone, graph-replayed per call (as the configs[2] sweep and
+    # the plain read below), against the plain read of its weight bytes
+    reads = achievable_read([N * K for _, N, K in SHAPES] + [1 << 30])
+    for j, (name, N, K) in enumerate(SHAPES):
+        lin, c = lins[j], outs[j]
+
+        def run_1(lin=lin, c=c):
+            w, s = lin.next()
+            HK.linear_fp8(c, xs[lin.K], w, s, lin.q_ws, lin.s_ws, 1, lin.N, lin.K)
+        ms = graph_call_ms(run_1, 20)
+        rd = reads[(N * K + 4095) // 4096 * 4096]
+        gbs = fp8_bytes(1, N, K) / (ms * 1e-3) / 1e9
+        per_shape[name].update({"graph_us": round(ms * 1e3, 3), "graph_GBs": round(gbs, 1),
+                                "frac_of_8TBs": round(gbs / HBM_PEAK_GBS, 4),
+                                "plain_read_us": rd["us"], "plain_read_GBs": rd["GBs"],
+                                "frac_of_plain_read": round(rd["us"] / (ms * 1e3), 4)})
     detail = {"m1_shapes": per_shape,
-              "kernel_time_per_step_us": round(1e3 * kern_ms / args.steps, 3)}
+              "kernel_time_per_step_us": round(1e3 * kern_ms / args.steps, 3),
+              "achievable_read": {"method": "graph-replayed plain streaming read of the same "
+                                            "byte count over a rotating window of a 1 GiB "
+                                            "buffer (libhephbench.so), best of 1024/2048/4096 "
+                                            "workgroups",
+                                  "sizes": {str(k): v for k, v in reads.items()},
+                                  "read_1GiB_GBs": reads[1 << 30]["GBs"]}}
     if not args.quick:
         detail.update(detail_sweeps(lins))
 
@@ -350,6 +425,20 @@ def main():
         "cpu_baseline": cpu,
         "detail": detail,
     }
+    pk = detail.get("prefill_m4096_kernel")
+    if pk:
+        line["prefill_roofline"] = {
+            "bound": "mfma", "achieved": pk["TFLOPs"], "peak": FP8_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(pk["TFLOPs"] / FP8_PEAK_TFLOPS, 4),
+            "traffic": profiled_traffic(PREFILL_TRAFFIC_PROFILE),
+            "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE per 4-shape step, "
+                              "profiles/fp8_gemm_m4096_pmc_traffic.md",
+            "kernel": ", ".join(sorted(set(pk["kernels"]))),
+            "flops_per_step": pk["flops_per_step"],
+            "workload": "configs[3] M=4096 over the 4 config-1 shapes, GEMM kernel only "
+                        "(activations quantized beforehand), weights rotated past the "
+                        "Infinity Cache",
+            "path_TFLOPs_quant_plus_gemm": detail.get("prefill_m4096_TFLOPs")}
     print(json.dumps(line))
 
 
@@ -441,6 +530,7 @@ def detail_sweeps(lins):
                              "frac": round(tf / FP8_PEAK_TFLOPS, 4)}
         pre[f"M={M}"] = row
     out["prefill"] = pre
+    out["prefill_m4096_kernel"] = prefill_kernel_times(lins, timer)
     out["decode_step_config4"] = decode_step_timing()
     t4096 = sum(2.0 * 4096 * l.N * l.K for l in lins)
     us4096 = sum(v["us"] for v in pre["M=4096"].values())
@@ -448,6 +538,40 @@ def detail_sweeps(lins):
     out["prefill_m4096_frac"] = round(out["prefill_m4096_TFLOPs"] / FP8_PEAK_TFLOPS, 4)
     timer.close()
     return out
+
+
+def prefill_kernel_times(lins, timer, M=4096, calls=10):
+    """configs[3] at M = 4096, the GEMM kernel alone: the activations are
+    quantized once, then each call runs with SKIP_QUANT over the rotated
+    weight copies, stamped by HIP events at the kernel's begin and end
+    (after ~20 ms of the same launches, so the clock has settled)."""
+    import torch
+    from hephaestus_amd import kernels as HK
+    per, names = {}, []
+    for lin in lins:
+        xm = act(M, lin.K, seed=M + 1, outliers=True)
+        cm = torch.empty(M, lin.N, dtype=torch.bfloat16, device="cuda")
+        q_ws, s_ws = HK.workspace(M, lin.K, n=lin.N)
+        HK.quantize_act_rows_fp8(q_ws, s_ws, xm, M, lin.K)
+
+        def run(lin=lin, cm=cm, q_ws=q_ws, s_ws=s_ws):
+            w, s = lin.next()
+            HK.linear_fp8(cm, None, w, s, q_ws, s_ws, M, lin.N, lin.K, do_quantize=False)
+        t_end = time.perf_counter() + 0.02
+        while time.perf_counter() < t_end:
+            for _ in range(8):
+                run()
+            torch.cuda.synchronize()
+        ms = time_calls(run, calls, timer) / calls
+        names.append(HK.last_kernel())
+        tf = 2.0 * M * lin.N * lin.K / (ms * 1e-3) / 1e12
+        per[lin.name] = {"kernel_us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
+                         "frac": round(tf / FP8_PEAK_TFLOPS, 4), "kernel": names[-1]}
+    flops = sum(2.0 * M * l.N * l.K for l in lins)
+    us = sum(v["kernel_us"] for v in per.values())
+    return {"shapes": per, "kernels": names, "flops_per_step": flops,
+            "kernel_us_per_step": round(us, 2),
+            "TFLOPs": round(flops / (us * 1e-6) / 1e12, 1)}
 
 
 def decode_step_timing(steps=20):
@@ -486,15 +610,26 @@ def decode_step_timing(steps=20):
             "argmax": int(dec.next_token.item())}
 
 
+def cpu_threads():
+    """Host threads for the CPU baseline: OMP_NUM_THREADS when set (the GPU
+    boxes set it to the cores one GPU's share of the host holds), else every
+    core this process may run on."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    return len(os.sched_getaffinity(0))
+
+
 def cpu_baseline(lins, xs, seconds):
-    """The oracle's quantize + dequant-matmul on host cores, M = 1, over the
-    same four shapes (same weights and activations, copied to the host)."""
+    """The oracle's quantize + dequant-matmul (f32 accumulation) on the host
+    cores over the same four shapes and the same weights: M = 1 (configs[1],
+    GB/s, the bench's unit) for ~seconds, then the M = 512 prefill leg
+    (configs[3], TFLOP/s) for about as long again."""
     import numpy as np
     import torch
     from oracle import oracle as O
     O.build()
-    threads = max(1, min(16, os.cpu_count() or 1))
-    os.environ.setdefault("OMP_NUM_THREADS", str(threads))
+    threads = cpu_threads()
     host = []
     for lin in lins:
         host.append((lin.w[0].cpu().numpy(), lin.s[0].cpu().numpy(),
@@ -514,6 +649,19 @@ def cpu_baseline(lins, xs, seconds):
         tot_bytes += n * fp8_bytes(1, N, K)
         tot_s += el
         reps[N * 100000 + K] = n
+    # configs[3] M = 512 leg: one call per shape, repeated while the budget lasts
+    M = 512
+    flops, pre_s, pre_calls, t_end = 0.0, 0.0, 0, time.perf_counter() + seconds
+    xm = {K: O.gen_act_bf16(M + 1, M, K, outlier_p=1e-3) for K in {h[4] for h in host}}
+    while True:
+        for qw, sw, _, N, K in host:
+            t0 = time.perf_counter()
+            O.quant_linear(xm[K], qw, sw, nthreads=threads)
+            pre_s += time.perf_counter() - t0
+            flops += 2.0 * M * N * K
+            pre_calls += 1
+        if time.perf_counter() >= t_end:
+            break
     cpu_name = ""
     try:
         for ln in open("/proc/cpuinfo"):
@@ -524,8 +672,14 @@ def cpu_baseline(lins, xs, seconds):
         pass
     return {"value": round(tot_bytes / tot_s / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
-            "sample": f"oracle quant + f32 dequant-matmul, M=1, the 4 config-1 shapes, "
-                      f"~{seconds:.0f} s total ({sum(reps.values())} calls); CPU: {cpu_name}"}
+            "nproc": os.cpu_count(), "affinity_cores": len(os.sched_getaffinity(0)),
+            "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS"),
+            "prefill_m512": {"TFLOPs": round(flops / pre_s / 1e12, 4), "calls": pre_calls,
+                             "seconds": round(pre_s, 2)},
+            "sample": f"oracle quant + f32 dequant-matmul on {threads} threads: M=1 over the 4 "
+                      f"config-1 shapes for ~{seconds:.0f} s ({sum(reps.values())} calls), then "
+                      f"the configs[3] M=512 leg ({pre_calls} calls, {pre_s:.1f} s); "
+                      f"CPU: {cpu_name}"}
 
 
 if __name__ == "__main__":
