@@ -27,6 +27,7 @@ HEPH_ERR_FLAGS = -7
 HEPH_ERR_DEVICE = -8
 HEPH_ERR_LAUNCH = -9
 HEPH_ERR_UNSUPPORTED = -10
+HEPH_ERR_SCRATCH = -11
 
 HEPH_DTYPE_BF16 = 0
 HEPH_DTYPE_F32 = 1
@@ -58,6 +59,8 @@ SIGNATURES = {
                              _i, _i, _i, _i, _i, _vp]),
     "heph_fp8_linear_with": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _vp, _sz, _vp, _sz,
                                   _i, _i, _i, _i, _i, _vp, ctypes.POINTER(LaunchOverrides)]),
+    "heph_fp8_linear_noalloc": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp]),
+    "heph_noalloc_scratch_bytes": (_sz, []),
     "heph_fp8_linear_rmsnorm": (_i, [_vp, _i, _vp, _vp, ctypes.c_float, _vp, _vp, _i, _i, _vp,
                                      _sz, _vp, _sz, _i, _i, _i, _vp]),
     "heph_bf16_linear": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _i, _vp]),

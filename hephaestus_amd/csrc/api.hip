@@ -114,6 +114,8 @@ int heph_fp8_quant_weight(const uint16_t* w_bf16, uint8_t* q, float* scale_inv, 
                                        static_cast<hipStream_t>(stream)));
 }
 
+}  // extern "C"
+
 namespace {
 
 // Launch-shape overrides of one heph_fp8_linear_with call, checked and
@@ -137,8 +139,13 @@ int take_overrides(const heph_launch_overrides* ov, Tuning* t)
     return HEPH_OK;
 }
 
+}  // namespace
+
+namespace heph {
+
 // heph_fp8_linear, and with gamma (M = 1, group 128, fused GEMV only) the
-// RMSNorm of x folded into the GEMV's quantization prologue.
+// RMSNorm of x folded into the GEMV's quantization prologue; also the body
+// of the allocation-free entry point (noalloc.hip).
 int fp8_linear_impl(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t* w,
                     const float* w_scale, int w_block_n, int w_block_k, uint8_t* q_ws,
                     size_t q_ws_bytes, float* s_ws, size_t s_ws_floats, int M, int N, int K,
@@ -231,7 +238,9 @@ int fp8_linear_impl(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
     return launch_status(e);
 }
 
-}  // namespace
+}  // namespace heph
+
+extern "C" {
 
 int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t* w,
                     const float* w_scale, int w_block_n, int w_block_k, uint8_t* q_ws,
@@ -300,6 +309,9 @@ const char* heph_strerror(int status)
     case HEPH_ERR_FLAGS: return "unknown or contradictory flags";
     case HEPH_ERR_DEVICE: return "current HIP device is not gfx950 (MI355X)";
     case HEPH_ERR_LAUNCH: return "HIP kernel launch failed";
+    case HEPH_ERR_SCRATCH:
+        return "codes and scales larger than the allocation-free entry point's fixed scratch "
+               "(heph_noalloc_scratch_bytes)";
     case HEPH_ERR_UNSUPPORTED:
         return "shape outside this entry point's limits (fused RMSNorm linear: M = 1, "
                "group 128, K <= 8192)";

@@ -51,6 +51,7 @@ extern "C" {
 #define HEPH_ERR_DEVICE       (-8)  /* current device is not gfx950 */
 #define HEPH_ERR_LAUNCH       (-9)  /* HIP reported an error at launch */
 #define HEPH_ERR_UNSUPPORTED (-10)  /* valid shape outside this entry point's limits */
+#define HEPH_ERR_SCRATCH     (-11)  /* codes + scales exceed the fixed no-alloc scratch */
 
 /* output dtypes */
 #define HEPH_DTYPE_BF16 0
@@ -138,6 +139,34 @@ int heph_fp8_linear_rmsnorm(void* c, int c_dtype, const uint16_t* x_bf16,
 int heph_bf16_linear(void* c, int c_dtype, const uint16_t* x_bf16,
                      const uint16_t* w_bf16, int M, int N, int K, int flags,
                      void* stream);
+
+/*
+ * heph_fp8_linear without workspace arguments, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference, whose
+ * callers preallocate a_fp8_ws / act_scale_ws (forward.mojo:121-125).
+ * The activation codes, scales and K-split partials live in one fixed
+ * device array of HEPH_NOALLOC_SCRATCH_BYTES (64 MiB) that the library's
+ * code object holds on every GPU it runs on until the process ends; the
+ * call allocates and frees nothing. Limit: round256(M*K) +
+ * round256(4*M*K/group_k) <= HEPH_NOALLOC_SCRATCH_BYTES (e.g. M = 4096 at
+ * K = 9728), else HEPH_ERR_SCRATCH before any device work. All calls on
+ * one GPU share the array: HEPH_FLAG_SKIP_QUANT reuses the codes the
+ * previous call on that GPU left there (same M, K, group_k), and calls that
+ * overlap on one GPU (several streams or threads) race on it and must be
+ * serialized by the caller. Arguments and flags otherwise as
+ * heph_fp8_linear; outputs are bit for bit those of heph_fp8_linear with a
+ * q_ws of heph_fp8_linear_ws_bytes(M, N, K) bytes whenever the K-split
+ * partials fit the array's remainder.
+ */
+#define HEPH_NOALLOC_SCRATCH_BYTES (64u << 20)
+int heph_fp8_linear_noalloc(void* c, int c_dtype, const uint16_t* x_bf16,
+                            const uint8_t* w, const float* w_scale, int w_block_n,
+                            int w_block_k, int M, int N, int K, int group_k,
+                            int flags, void* stream);
+
+/* HEPH_NOALLOC_SCRATCH_BYTES of the built library. */
+size_t heph_noalloc_scratch_bytes(void);
 
 /* Workspace sizes heph_fp8_linear needs for (M, K, group_k). */
 size_t heph_fp8_q_ws_bytes(int M, int K);

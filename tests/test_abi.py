@@ -27,7 +27,7 @@ def test_exports_every_declared_symbol(lib):
 
 def test_version_and_strerror(lib):
     assert lib.heph_abi_version() == 2
-    for code in range(0, -11, -1):
+    for code in range(0, -12, -1):
         msg = L.strerror(code)
         assert msg and msg != "unknown status", code
     assert L.strerror(-99) == "unknown status"
@@ -205,3 +205,16 @@ def test_decode_ops_reject(lib):
     assert lib.heph_argmax_bf16(FAKE, FAKE, 10, None, aw, None) == L.HEPH_ERR_NULL
     assert lib.heph_argmax_bf16(FAKE, FAKE, 0, FAKE, aw, None) == L.HEPH_ERR_SHAPE
     assert lib.heph_argmax_bf16(FAKE, FAKE, 151936, FAKE, aw - 8, None) == L.HEPH_ERR_WORKSPACE
+
+
+def test_noalloc_limits(lib):
+    # the allocation-free entry point has a fixed 64 MiB scratch: codes plus
+    # scales past it are refused before any device work, with their own status
+    assert lib.heph_noalloc_scratch_bytes() == 64 << 20
+    na = lib.heph_fp8_linear_noalloc
+    assert na(FAKE, 0, FAKE, FAKE, FAKE, 128, 128, 8192, 256, 9728, 128, 0, None) == \
+        L.HEPH_ERR_SCRATCH
+    assert na(FAKE, 0, FAKE, FAKE, FAKE, 128, 128, 1, 256, 2500, 128, 0, None) == L.HEPH_ERR_SHAPE
+    # M = 4096 at K = 9728 fits (40 MB of codes, 1.2 MB of scales)
+    assert na(FAKE, 0, FAKE, FAKE, FAKE, 128, 128, 4096, 256, 9728, 128, 0, None) in \
+        (L.HEPH_ERR_DEVICE, L.HEPH_OK)
