@@ -337,6 +337,147 @@ __device__ __forceinline__ uint32_t pack_bf16_hw(float a, float b)
 {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
+// Epilogue of the large-M kernels: lane l holds C[row r16][cols 4*slice ..
+// +3] of each 16x16 block of its (BM/2) x 64 wave tile, already scaled.
+// K splits store the fp32 partial tile; bf16 output goes through LDS once
+// as bf16 for coalesced 16-byte stores; f32 output or a residual in two
+// f32 passes (the residual added before the one rounding). Every thread of
+// the workgroup calls it; LDS_BYTES of smem are free to reuse.
+template <int SM, int BM, int LDS_BYTES>
+__device__ __forceinline__ void big_epilogue(const Fp8Operands& op, f32x4 (&acc)[BM / 32][L_NT],
+                                             uint8_t* smem, int m0, int n0, int split, int S)
+{
+    constexpr int L_BM = BM, L_WM = BM / 2, L_MT = BM / 32;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, slice = lane >> 4;
+    const int wm = wave >> 2, wn = wave & 3;
+    const int M = op.M, N = op.N;
+    // Lane l holds C[row r16][cols 4*slice .. +3] of each 16x16 block.
+    const int r_lane = wm * L_WM + r16;                  // tile row of (mi = 0)
+    const int c_lane = wn * L_WN + slice * 4;            // tile col of (ni = 0)
+    if constexpr (SM != 2) {
+        if (S > 1) {
+            // split over K: the fp32 partial tile goes to the scratch
+            // [split][M][N]; splitk_reduce_kernel finishes the output.
+            float* pp = op.part + (size_t)split * M * N;
+#pragma unroll
+            for (int mi = 0; mi < L_MT; ++mi) {
+                const int row = m0 + r_lane + mi * 16;
+                if (row >= M) continue;
+#pragma unroll
+                for (int ni = 0; ni < L_NT; ++ni) {
+                    const int col = n0 + c_lane + ni * 16;
+                    if (col < N) *reinterpret_cast<f32x4*>(pp + (size_t)row * N + col) = acc[mi][ni];
+                }
+            }
+            return;
+        }
+    }
+    if (!op.residual && !op.c_f32) {
+        // bf16 output: the whole tile goes through LDS once as bf16, rows
+        // padded to 520 bytes (130 dwords: consecutive rows 2 banks apart),
+        // each lane writing 8 bytes per block; then 16-byte coalesced stores.
+        constexpr int RB = 520;
+        static_assert(L_BM * RB <= LDS_BYTES, "bf16 tile must fit the stage buffers");
+        __syncthreads();
+#pragma unroll
+        for (int mi = 0; mi < L_MT; ++mi) {
+            float sa = 1.0f;
+            if constexpr (SM == 2) sa = op.s[min(m0 + r_lane + mi * 16, M - 1)];
+#pragma unroll
+            for (int ni = 0; ni < L_NT; ++ni) {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[e] = acc[mi][ni][e];
+                    if constexpr (SM == 2)
+                    {
+                        // reference association: acc*(sa*sw) at M = 1
+                        // (wmma_gfx12.mojo:711-712), (acc*sa)*sw otherwise (:848)
+                        const float sw = op.sw[min(n0 + c_lane + ni * 16 + e, N - 1)];
+                        v[e] = M == 1 ? v[e] * (sa * sw) : (v[e] * sa) * sw;
+                    }
+                }
+                const uint2 pk = make_uint2(pack_bf16_hw(v[0], v[1]), pack_bf16_hw(v[2], v[3]));
+                *reinterpret_cast<uint2*>(smem + (r_lane + mi * 16) * RB +
+                                          (c_lane + ni * 16) * 2) = pk;
+            }
+        }
+        __syncthreads();
+        for (int e = tid; e < L_BM * (L_BN / 8); e += 512) {
+            const int r = e / (L_BN / 8);
+            const int c8 = (e % (L_BN / 8)) * 8;
+            const int grow = m0 + r, gcol = n0 + c8;
+            if (grow >= M || gcol >= N) continue;
+            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(op.c) + (size_t)grow * N + gcol) =
+                *reinterpret_cast<const uint4*>(smem + r * RB + c8 * 2);
+        }
+        return;
+    }
+    // f32 output or residual: two passes of L_WM rows through LDS in f32
+    // (the residual is added before the one rounding).
+    constexpr int CST = L_BN + 4;
+    static_assert(L_WM * CST * 4 <= LDS_BYTES, "epilogue tile must fit the stage buffers");
+    float* Cs = reinterpret_cast<float*>(smem);
+    float* cw = Cs + r16 * CST + c_lane;
+    for (int pass = 0; pass < 2; ++pass) {
+        __syncthreads();
+        if (wm == pass) {
+#pragma unroll
+            for (int mi = 0; mi < L_MT; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < L_NT; ++ni)
+                    *reinterpret_cast<f32x4*>(cw + mi * 16 * CST + ni * 16) = acc[mi][ni];
+        }
+        __syncthreads();
+        // L_WM rows x 256 cols: each thread writes 8 consecutive outputs
+        for (int e = tid; e < L_WM * (L_BN / 8); e += 512) {
+            const int r = e / (L_BN / 8);
+            const int c8 = (e % (L_BN / 8)) * 8;
+            const int grow = m0 + pass * L_WM + r;
+            const int gcol = n0 + c8;
+            if (grow >= M || gcol >= N) continue;
+            const f32x4 lo = *reinterpret_cast<const f32x4*>(&Cs[r * CST + c8]);
+            const f32x4 hi = *reinterpret_cast<const f32x4*>(&Cs[r * CST + c8 + 4]);
+            float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            if constexpr (SM == 2) {
+                // reference association: acc*(sa*sw) at M = 1, else (acc*sa)*sw
+                const float sa = op.s[grow];
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+                    v[t] = M == 1 ? v[t] * (sa * op.sw[gcol + t]) : (v[t] * sa) * op.sw[gcol + t];
+            }
+            const size_t o = (size_t)grow * N + gcol;
+            if (op.c_f32) {
+                float* c = static_cast<float*>(op.c) + o;
+                if (op.residual) {
+                    const float4 r0 = *reinterpret_cast<const float4*>(c);
+                    const float4 r1 = *reinterpret_cast<const float4*>(c + 4);
+                    v[0] += r0.x; v[1] += r0.y; v[2] += r0.z; v[3] += r0.w;
+                    v[4] += r1.x; v[5] += r1.y; v[6] += r1.z; v[7] += r1.w;
+                }
+                *reinterpret_cast<float4*>(c) = make_float4(v[0], v[1], v[2], v[3]);
+                *reinterpret_cast<float4*>(c + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            } else {
+                uint16_t* c = static_cast<uint16_t*>(op.c) + o;
+                const uint4 rr = *reinterpret_cast<const uint4*>(c);
+                v[0] += bf16lo(rr.x); v[1] += bf16hi(rr.x);
+                v[2] += bf16lo(rr.y); v[3] += bf16hi(rr.y);
+                v[4] += bf16lo(rr.z); v[5] += bf16hi(rr.z);
+                v[6] += bf16lo(rr.w); v[7] += bf16hi(rr.w);
+                uint4 out;
+                out.x = f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+                out.y = f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+                out.z = f32_to_bf16(v[4]) | ((uint32_t)f32_to_bf16(v[5]) << 16);
+                out.w = f32_to_bf16(v[6]) | ((uint32_t)f32_to_bf16(v[7]) << 16);
+                *reinterpret_cast<uint4*>(c) = out;
+            }
+        }
+    }
+}
+
 template <int SM, int BM>
 __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
 {
@@ -587,129 +728,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     }
     if constexpr (SM != 2) rescale(L_MT - 1, (L_MT - 1) & 1);
 
-    // ---- epilogue ----
-    // Lane l holds C[row r16][cols 4*slice .. +3] of each 16x16 block.
-    const int r_lane = wm * L_WM + r16;                  // tile row of (mi = 0)
-    const int c_lane = wn * L_WN + slice * 4;            // tile col of (ni = 0)
-    if constexpr (SM != 2) {
-        if (S > 1) {
-            // split over K: the fp32 partial tile goes to the scratch
-            // [split][M][N]; splitk_reduce_kernel finishes the output.
-            float* pp = op.part + (size_t)split * M * N;
-#pragma unroll
-            for (int mi = 0; mi < L_MT; ++mi) {
-                const int row = m0 + r_lane + mi * 16;
-                if (row >= M) continue;
-#pragma unroll
-                for (int ni = 0; ni < L_NT; ++ni) {
-                    const int col = n0 + c_lane + ni * 16;
-                    if (col < N) *reinterpret_cast<f32x4*>(pp + (size_t)row * N + col) = acc[mi][ni];
-                }
-            }
-            return;
-        }
-    }
-    if (!op.residual && !op.c_f32) {
-        // bf16 output: the whole tile goes through LDS once as bf16, rows
-        // padded to 520 bytes (130 dwords: consecutive rows 2 banks apart),
-        // each lane writing 8 bytes per block; then 16-byte coalesced stores.
-        constexpr int RB = 520;
-        static_assert(L_BM * RB <= T::BYTES, "bf16 tile must fit the stage buffers");
-        __syncthreads();
-#pragma unroll
-        for (int mi = 0; mi < L_MT; ++mi) {
-            float sa = 1.0f;
-            if constexpr (SM == 2) sa = op.s[min(m0 + r_lane + mi * 16, M - 1)];
-#pragma unroll
-            for (int ni = 0; ni < L_NT; ++ni) {
-                float v[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    v[e] = acc[mi][ni][e];
-                    if constexpr (SM == 2)
-                    {
-                        // reference association: acc*(sa*sw) at M = 1
-                        // (wmma_gfx12.mojo:711-712), (acc*sa)*sw otherwise (:848)
-                        const float sw = op.sw[min(n0 + c_lane + ni * 16 + e, N - 1)];
-                        v[e] = M == 1 ? v[e] * (sa * sw) : (v[e] * sa) * sw;
-                    }
-                }
-                const uint2 pk = make_uint2(pack_bf16_hw(v[0], v[1]), pack_bf16_hw(v[2], v[3]));
-                *reinterpret_cast<uint2*>(smem + (r_lane + mi * 16) * RB +
-                                          (c_lane + ni * 16) * 2) = pk;
-            }
-        }
-        __syncthreads();
-        for (int e = tid; e < L_BM * (L_BN / 8); e += 512) {
-            const int r = e / (L_BN / 8);
-            const int c8 = (e % (L_BN / 8)) * 8;
-            const int grow = m0 + r, gcol = n0 + c8;
-            if (grow >= M || gcol >= N) continue;
-            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(op.c) + (size_t)grow * N + gcol) =
-                *reinterpret_cast<const uint4*>(smem + r * RB + c8 * 2);
-        }
-        return;
-    }
-    // f32 output or residual: two passes of L_WM rows through LDS in f32
-    // (the residual is added before the one rounding).
-    constexpr int CST = L_BN + 4;
-    static_assert(L_WM * CST * 4 <= T::BYTES, "epilogue tile must fit the stage buffers");
-    float* Cs = reinterpret_cast<float*>(smem);
-    float* cw = Cs + r16 * CST + c_lane;
-    for (int pass = 0; pass < 2; ++pass) {
-        __syncthreads();
-        if (wm == pass) {
-#pragma unroll
-            for (int mi = 0; mi < L_MT; ++mi)
-#pragma unroll
-                for (int ni = 0; ni < L_NT; ++ni)
-                    *reinterpret_cast<f32x4*>(cw + mi * 16 * CST + ni * 16) = acc[mi][ni];
-        }
-        __syncthreads();
-        // L_WM rows x 256 cols: each thread writes 8 consecutive outputs
-        for (int e = tid; e < L_WM * (L_BN / 8); e += 512) {
-            const int r = e / (L_BN / 8);
-            const int c8 = (e % (L_BN / 8)) * 8;
-            const int grow = m0 + pass * L_WM + r;
-            const int gcol = n0 + c8;
-            if (grow >= M || gcol >= N) continue;
-            const f32x4 lo = *reinterpret_cast<const f32x4*>(&Cs[r * CST + c8]);
-            const f32x4 hi = *reinterpret_cast<const f32x4*>(&Cs[r * CST + c8 + 4]);
-            float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            if constexpr (SM == 2) {
-                // reference association: acc*(sa*sw) at M = 1, else (acc*sa)*sw
-                const float sa = op.s[grow];
-#pragma unroll
-                for (int t = 0; t < 8; ++t)
-                    v[t] = M == 1 ? v[t] * (sa * op.sw[gcol + t]) : (v[t] * sa) * op.sw[gcol + t];
-            }
-            const size_t o = (size_t)grow * N + gcol;
-            if (op.c_f32) {
-                float* c = static_cast<float*>(op.c) + o;
-                if (op.residual) {
-                    const float4 r0 = *reinterpret_cast<const float4*>(c);
-                    const float4 r1 = *reinterpret_cast<const float4*>(c + 4);
-                    v[0] += r0.x; v[1] += r0.y; v[2] += r0.z; v[3] += r0.w;
-                    v[4] += r1.x; v[5] += r1.y; v[6] += r1.z; v[7] += r1.w;
-                }
-                *reinterpret_cast<float4*>(c) = make_float4(v[0], v[1], v[2], v[3]);
-                *reinterpret_cast<float4*>(c + 4) = make_float4(v[4], v[5], v[6], v[7]);
-            } else {
-                uint16_t* c = static_cast<uint16_t*>(op.c) + o;
-                const uint4 rr = *reinterpret_cast<const uint4*>(c);
-                v[0] += bf16lo(rr.x); v[1] += bf16hi(rr.x);
-                v[2] += bf16lo(rr.y); v[3] += bf16hi(rr.y);
-                v[4] += bf16lo(rr.z); v[5] += bf16hi(rr.z);
-                v[6] += bf16lo(rr.w); v[7] += bf16hi(rr.w);
-                uint4 out;
-                out.x = f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
-                out.y = f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
-                out.z = f32_to_bf16(v[4]) | ((uint32_t)f32_to_bf16(v[5]) << 16);
-                out.w = f32_to_bf16(v[6]) | ((uint32_t)f32_to_bf16(v[7]) << 16);
-                *reinterpret_cast<uint4*>(c) = out;
-            }
-        }
-    }
+    big_epilogue<SM, BM, T::BYTES>(op, acc, smem, m0, n0, split, S);
 }
 
 // Sums the K-split partials of the large-M GEMM in split order, adds the

@@ -691,6 +691,11 @@ def tile_m(request):
     T.TUNE.clear()
 
 
+def gemm_name(bm, block=True, split=False):
+    """Kernel name the large-M dispatch reports at a forced tile height."""
+    return f"fp8_gemm_{bm}x256" + ("_splitk" if split else "")
+
+
 @pytest.mark.parametrize("mode", ["block", "channel_token", "channel_g128"])
 @pytest.mark.parametrize("out,resid", [("bf16", False), ("bf16", True), ("f32", False), ("f32", True)])
 def test_large_m_gemm_modes(mode, out, resid, tile_m):
@@ -709,7 +714,7 @@ def test_large_m_gemm_modes(mode, out, resid, tile_m):
     r = O.gen_normal(62, M * N).reshape(M, N).astype(np.float32)
     res_t = (dev(bf16_of(r)) if out == "bf16" else dev(r)) if resid else None
     c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K, group_k=g, out=dt, residual=res_t)
-    assert HK.last_kernel() == f"fp8_gemm_{tile_m}x256"
+    assert HK.last_kernel() == gemm_name(tile_m, mode == "block")
     ref = O.quant_linear(x, qw, sw, group_k=g, bn=bn, bk=bk)
     if resid:
         ref = ref + (f32_of_bf16(bf16_of(r)) if out == "bf16" else r)
@@ -729,7 +734,7 @@ def test_large_m_short_k(K, tile_m):
     x = O.gen_act_bf16(66 + K, M, K, outlier_p=1e-3)
     qw, sw = O.gen_weight(67 + K, N, K)
     c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K)
-    assert HK.last_kernel() == f"fp8_gemm_{tile_m}x256"
+    assert HK.last_kernel() == gemm_name(tile_m)
     check_close(host_bf16(c), O.quant_linear(x, qw, sw), f"K={K} BM={tile_m}")
     qo, _ = O.quant_act(x, 128)
     assert np.array_equal(q_ws.cpu().numpy().reshape(M, K), qo)
@@ -751,7 +756,7 @@ def test_large_m_bf16_is_rounded_f32(mode, tile_m):
         g = K if mode == "channel_token" else 128
     f, _, _ = run_linear(qw, sw, x, M=M, N=N, K=K, group_k=g, out=torch.float32)
     b, _, _ = run_linear(qw, sw, x, M=M, N=N, K=K, group_k=g)
-    assert HK.last_kernel() == f"fp8_gemm_{tile_m}x256"
+    assert HK.last_kernel() == gemm_name(tile_m, mode == "block")
     assert np.array_equal(host_bf16(b), bf16_of(f.cpu().numpy()))
 
 
@@ -780,7 +785,7 @@ def test_large_m_exact_integer(M, tile_m):
     ref = (ia.astype(np.float64) @ iw.astype(np.float64).T) * 0.0625 * 2.0 ** -5
     c, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, skip_quant=True,
                          q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
-    assert HK.last_kernel() == f"fp8_gemm_{tile_m}x256"
+    assert HK.last_kernel() == gemm_name(tile_m)
     assert np.array_equal(host_bf16(c), bf16_of(ref.astype(np.float32)))
 
 
@@ -794,7 +799,7 @@ def test_large_m_odd_chunk_counts(K, tile_m):
     x = O.gen_act_bf16(80 + K, M, K, outlier_p=1e-3)
     qw, sw = O.gen_weight(81 + K, N, K)
     c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K)
-    assert HK.last_kernel() == f"fp8_gemm_{tile_m}x256"
+    assert HK.last_kernel() == gemm_name(tile_m)
     ref = O.quant_linear(x, qw, sw)
     assert max_abs_rel(f32_of_bf16(host_bf16(c)), ref) <= TOL
     ia, qa = lattice(M, K, 5000 + K)
@@ -804,7 +809,7 @@ def test_large_m_odd_chunk_counts(K, tile_m):
     exact = (ia.astype(np.float64) @ iw.astype(np.float64).T) * 0.0625 * 2.0 ** -5
     c, _, _ = run_linear(qwl, swl, None, M=M, N=N, K=K, skip_quant=True,
                          q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
-    assert HK.last_kernel() == f"fp8_gemm_{tile_m}x256"
+    assert HK.last_kernel() == gemm_name(tile_m)
     assert np.array_equal(host_bf16(c), bf16_of(exact.astype(np.float32)))
 
 
@@ -992,7 +997,7 @@ def test_large_m_split_k_every_tile(out, resid, tile_m):
     res_t = (dev(bf16_of(r)) if out == "bf16" else dev(r)) if resid else None
     q_ws, s_ws = HK.workspace(M, K, n=N)
     c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K, out=dt, residual=res_t, q_ws=q_ws, s_ws=s_ws)
-    assert HK.last_kernel() == f"fp8_gemm_{tile_m}x256_splitk", HK.last_kernel()
+    assert HK.last_kernel() == gemm_name(tile_m, split=True), HK.last_kernel()
     ref = O.quant_linear(x, qw, sw)
     if resid:
         ref = ref + (f32_of_bf16(bf16_of(r)) if out == "bf16" else r)
