@@ -59,6 +59,8 @@ SIGNATURES = {
                              _i, _i, _i, _i, _i, _vp]),
     "heph_fp8_linear_with": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _vp, _sz, _vp, _sz,
                                   _i, _i, _i, _i, _i, _vp, ctypes.POINTER(LaunchOverrides)]),
+    "heph_rmsnorm_quant_fp8": (_i, [_vp, _vp, _vp, _vp, _i, _i, ctypes.c_float, _i, _vp]),
+    "heph_silu_mul_quant_fp8": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "heph_fp8_linear_noalloc": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp]),
     "heph_noalloc_scratch_bytes": (_sz, []),
     "heph_fp8_linear_rmsnorm": (_i, [_vp, _i, _vp, _vp, ctypes.c_float, _vp, _vp, _i, _i, _vp,

@@ -171,7 +171,7 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
     float ss = a * a;
     ss = __builtin_fmaf(b, b, ss);
     ss = wave_sum64(ss);
-    const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)D) + eps));
+    const float r = __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(ss, (float)D) + eps));
     a = round_bf16(f32_of_bf16(gamma[l]) * round_bf16(a * r));
     b = round_bf16(f32_of_bf16(gamma[l + 64]) * round_bf16(b * r));
     float c, s;

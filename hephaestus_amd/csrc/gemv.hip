@@ -229,13 +229,21 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
                     for (int d = 0; d < E / 2; ++d) b.xv[u][mt].d[d] = live ? v.d[d] : 0u;
                 }
             } else {
+                // Only the R lanes per column group that hold a real A row
+                // (r16 < R) load it; the others keep zeros and issue no
+                // load, so codes from the workspace cost R/16 of a full
+                // 16-row A tile per step.
                 const int ja = st * KS + ta;
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
                     const int row = mt * 16 + ma;
                     const uint8_t* p = op.q + (size_t)min(row, M - 1) * K +
                                        (size_t)min(ja, KC - 1) * kChunk + g * 16;
-                    const i32x4 lo = ldg16(p), hi = ldg16(p + 64);
+                    i32x4 lo = i32x4{0, 0, 0, 0}, hi = i32x4{0, 0, 0, 0};
+                    if (r16 < R) {
+                        lo = ldg16(p);
+                        hi = ldg16(p + 64);
+                    }
                     const bool live = r16 < R && row < M && ja < KC;
                     b.alo[u][mt] = live ? lo : i32x4{0, 0, 0, 0};
                     b.ahi[u][mt] = live ? hi : i32x4{0, 0, 0, 0};

@@ -196,9 +196,30 @@ __device__ __forceinline__ float fold256_every_wave(float v, float* red)
     return __shfl(a, 0, 64);
 }
 
+// sqrt(a) rounded to nearest, for the RMS factors. __fsqrt_rn compiles to
+// v_sqrt_f32, which is within one ulp but not always the nearest float (a
+// 512-row RMSNorm test met one row off by an ulp against the host's sqrtf).
+// With y that estimate and d, u its neighbours below and above: sqrt(a) is
+// nearer d than y iff a <= d*y, nearer u iff a > u*y. (The midpoint m of y
+// and d has m^2 = d*y + (y-d)^2/4, and that excess is ~2^-48 of a, far
+// below a's own spacing of ~2^-23, so no float a lies between d*y and m^2;
+// equality a == d*y puts sqrt(a) below m. Likewise for u.) Each product is
+// compared exactly through the sign of one FMA. a <= 0, inf and NaN keep
+// the estimate.
+__device__ __forceinline__ float sqrt_rn(float a)
+{
+    const float y = __fsqrt_rn(a);
+    if (!(a > 0.0f) || !__builtin_isfinite(a)) return y;
+    const uint32_t b = __float_as_uint(y);
+    const float d = __uint_as_float(b - 1u), u = __uint_as_float(b + 1u);
+    if (__builtin_fmaf(-d, y, a) <= 0.0f) return d;
+    if (__builtin_fmaf(-u, y, a) > 0.0f) return u;
+    return y;
+}
+
 __device__ __forceinline__ float rms_inv(float ss, int cols, float eps)
 {
-    return __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)cols) + eps));
+    return __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(ss, (float)cols) + eps));
 }
 
 __device__ __forceinline__ uint4 ldg16u(const void* p)

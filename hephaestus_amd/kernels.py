@@ -97,6 +97,36 @@ def quantize_act_fp8_pad(a_fp8, act_scale, x, k, ctx=None, *, group_k=128):
     quantize_act_rows_fp8(a_fp8, act_scale, x, 1, k, ctx, group_k=group_k)
 
 
+def rmsnorm_quant_fp8(a_fp8, act_scale, x, gamma, m, k, eps=1e-6, ctx=None, *, group_k=128):
+    """Producer-side quantization for a linear fed by an RMSNorm: codes and
+    scales of bf16(gamma * bf16(x * r)) per row of x [m, k] (bit for bit
+    rmsnorm then quantize_act_rows_fp8); the linear then runs with
+    do_quantize=False on these workspaces."""
+    if x.numel() < m * k or gamma.numel() < k:
+        raise HephError(L.HEPH_ERR_SHAPE, "rmsnorm_quant_fp8")
+    if a_fp8.numel() < m * k or act_scale.numel() < m * (k // max(group_k, 1)):
+        raise HephError(L.HEPH_ERR_WORKSPACE, "rmsnorm_quant_fp8")
+    s = L.lib().heph_rmsnorm_quant_fp8(
+        _dev(a_fp8, "a_fp8", _FP8), _dev(act_scale, "act_scale", (torch.float32,)),
+        _dev(x, "x", (torch.bfloat16,)), _dev(gamma, "gamma", (torch.bfloat16,)), m, k,
+        float(eps), group_k, _stream(ctx))
+    _check(s, "rmsnorm_quant_fp8")
+
+
+def silu_mul_quant_fp8(a_fp8, act_scale, gate, up, m, n, ld=None, ctx=None, *, group_k=128):
+    """Producer-side quantization for a linear fed by SwiGLU: codes and
+    scales of bf16(bf16(silu(gate)) * up) per row (row r at gate + r*ld,
+    up + r*ld; ld defaults to n), bit for bit silu_mul then
+    quantize_act_rows_fp8."""
+    ld = n if ld is None else ld
+    if a_fp8.numel() < m * n or act_scale.numel() < m * (n // max(group_k, 1)):
+        raise HephError(L.HEPH_ERR_WORKSPACE, "silu_mul_quant_fp8")
+    s = L.lib().heph_silu_mul_quant_fp8(
+        _dev(a_fp8, "a_fp8", _FP8), _dev(act_scale, "act_scale", (torch.float32,)),
+        gate.data_ptr(), up.data_ptr(), m, n, ld, group_k, _stream(ctx))
+    _check(s, "silu_mul_quant_fp8")
+
+
 def _overrides(tune):
     """A heph_launch_overrides for the dict `tune` (keys: its field names)."""
     bad = set(tune) - {f for f, _ in L.LaunchOverrides._fields_}

@@ -168,6 +168,37 @@ int heph_fp8_linear_noalloc(void* c, int c_dtype, const uint16_t* x_bf16,
 /* HEPH_NOALLOC_SCRATCH_BYTES of the built library. */
 size_t heph_noalloc_scratch_bytes(void);
 
+/*
+ * Producer-side activation quantization: the op that feeds an FP8 linear
+ * writes that linear's activation codes and scales itself (bit for bit what
+ * the producer followed by heph_fp8_quant_act writes), so the linear runs
+ * with HEPH_FLAG_SKIP_QUANT and the separate quantizer launch, with its pass
+ * over the bf16 activations, is gone. Replaces the pairs rms_norm +
+ * quantize_act_rows_fp8 and silu_mul + quantize_act_rows_fp8 of the
+ * reference's prefill (src/hephaestus/forward.mojo:45-81,
+ * kernels.mojo:1243-1278, :270-287; the quantization is the one linear_fp8
+ * runs at kernels.mojo:449-450).
+ *
+ * heph_rmsnorm_quant_fp8: per row of cols, y = bf16(gamma * bf16(x * r)),
+ * r = 1/sqrt(mean(x^2) + eps) summed as heph_rmsnorm sums it; q [rows, cols]
+ * codes and scales [rows, cols / group_k] of y. cols % 128 == 0 and
+ * cols <= 16384 (the row is staged in LDS; HEPH_ERR_UNSUPPORTED beyond).
+ *
+ * heph_silu_mul_quant_fp8: per row, y = bf16(bf16(g / (1 + exp(-g))) * up)
+ * as heph_silu_mul computes it, over n elements of gate and up, row r at
+ * gate + r * ld and up + r * ld (elements; ld % 8 == 0, e.g. the fused
+ * gate|up output [rows, 2n] with up = gate + n and ld = 2n); q [rows, n] and
+ * scales [rows, n / group_k]. n % 128 == 0; group_k = n needs n <= 16384.
+ *
+ * group_k is 128 or the row length; q, gate and up 16-byte aligned.
+ */
+int heph_rmsnorm_quant_fp8(uint8_t* q, float* scales, const uint16_t* x_bf16,
+                           const uint16_t* gamma_bf16, int rows, int cols, float eps,
+                           int group_k, void* stream);
+int heph_silu_mul_quant_fp8(uint8_t* q, float* scales, const uint16_t* gate_bf16,
+                            const uint16_t* up_bf16, int rows, int n, int ld, int group_k,
+                            void* stream);
+
 /* Workspace sizes heph_fp8_linear needs for (M, K, group_k). */
 size_t heph_fp8_q_ws_bytes(int M, int K);
 size_t heph_fp8_s_ws_floats(int M, int K, int group_k);

@@ -218,3 +218,18 @@ def test_noalloc_limits(lib):
     # M = 4096 at K = 9728 fits (40 MB of codes, 1.2 MB of scales)
     assert na(FAKE, 0, FAKE, FAKE, FAKE, 128, 128, 4096, 256, 9728, 128, 0, None) in \
         (L.HEPH_ERR_DEVICE, L.HEPH_OK)
+
+
+def test_producer_quant_rejects(lib):
+    rq, sq = lib.heph_rmsnorm_quant_fp8, lib.heph_silu_mul_quant_fp8
+    assert rq(None, FAKE, FAKE, FAKE, 1, 2560, 1e-6, 128, None) == L.HEPH_ERR_NULL
+    assert rq(FAKE, FAKE, FAKE, FAKE, 1, 2500, 1e-6, 128, None) == L.HEPH_ERR_SHAPE
+    assert rq(FAKE, FAKE, FAKE, FAKE, 1, 2560, 1e-6, 256, None) == L.HEPH_ERR_GROUP
+    assert rq(FAKE, FAKE, FAKE, FAKE, 1, 16512, 1e-6, 128, None) == L.HEPH_ERR_UNSUPPORTED
+    assert rq(ODD, FAKE, FAKE, FAKE, 1, 2560, 1e-6, 128, None) == L.HEPH_ERR_ALIGN
+    assert sq(FAKE, FAKE, FAKE, None, 1, 9728, 19456, 128, None) == L.HEPH_ERR_NULL
+    assert sq(FAKE, FAKE, FAKE, FAKE, 1, 9728, 9000, 128, None) == L.HEPH_ERR_SHAPE
+    assert sq(FAKE, FAKE, FAKE, FAKE, 1, 9728, 19460, 128, None) == L.HEPH_ERR_SHAPE
+    assert sq(FAKE, FAKE, FAKE, FAKE, 1, 9728, 19456, 64, None) == L.HEPH_ERR_GROUP
+    assert sq(FAKE, FAKE, FAKE, FAKE, 1, 32768, 32768, 32768, None) == L.HEPH_ERR_UNSUPPORTED
+    assert sq(FAKE, FAKE, ODD, FAKE, 1, 9728, 19456, 128, None) == L.HEPH_ERR_ALIGN

@@ -105,7 +105,8 @@ def test_fused_rmsnorm_linear_bit_exact(N, K, scale, out):
 
 
 @pytest.mark.parametrize("rows,cols,scale", [(3, 2560, 1.0), (1, 9728, 40.0), (2, 2560, 1e-4),
-                                             (32, 128, 1.0), (2, 12288, 1.0)])
+                                             (32, 128, 1.0), (2, 12288, 1.0), (4096, 2560, 1.0),
+                                             (1024, 128, 3.0)])
 def test_rmsnorm_bit_exact(rows, cols, scale):
     x = rng_bf16(cols + rows, rows * cols, scale).reshape(rows, cols)
     g = rng_bf16(7, cols)
