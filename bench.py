@@ -531,6 +531,7 @@ def detail_sweeps(lins):
         pre[f"M={M}"] = row
     out["prefill"] = pre
     out["prefill_m4096_kernel"] = prefill_kernel_times(lins, timer)
+    out["prefill_producer_path"] = prefill_producer_path(lins)
     out["decode_step_config4"] = decode_step_timing()
     t4096 = sum(2.0 * 4096 * l.N * l.K for l in lins)
     us4096 = sum(v["us"] for v in pre["M=4096"].values())
@@ -572,6 +573,81 @@ def prefill_kernel_times(lins, timer, M=4096, calls=10):
     return {"shapes": per, "kernels": names, "flops_per_step": flops,
             "kernel_us_per_step": round(us, 2),
             "TFLOPs": round(flops / (us * 1e-6) / 1e12, 1)}
+
+
+def prefill_producer_path(lins, Ms=(512, 4096)):
+    """configs[3] as a prefill layer feeds its linears: the op that produces
+    each linear's input quantizes it (qkv and gate_up: RMSNorm of the hidden
+    rows, heph_rmsnorm_quant_fp8; down: SwiGLU of the gate and up rows,
+    heph_silu_mul_quant_fp8) and the GEMM runs with SKIP_QUANT, against the
+    unfused producer + quantizer + GEMM; o_proj's input comes from prefill
+    attention, outside this library, so it keeps quantizer + GEMM in both.
+    Per call graph-replayed over rotated weights; us and TFLOP/s of the
+    GEMM's work."""
+    import torch
+    from hephaestus_amd import decode as DEC
+    from hephaestus_amd import kernels as HK
+    out = {}
+    for M in Ms:
+        row = {}
+        for lin in lins:
+            N, K = lin.N, lin.K
+            cm = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+            q_ws, s_ws = HK.workspace(M, K, n=N)
+            if lin.name == "down":
+                gate = act(M, K, seed=M + 2)
+                upv = act(M, K, seed=M + 5)
+                y = torch.empty(M, K, dtype=torch.bfloat16, device="cuda")
+
+                def unfused(lin=lin, gate=gate, upv=upv, y=y, cm=cm, q_ws=q_ws, s_ws=s_ws, M=M, K=K, N=N):
+                    w, s = lin.next()
+                    DEC.silu_mul(y, gate, upv, M * K)            # elementwise over all rows
+                    HK.linear_fp8(cm, y, w, s, q_ws, s_ws, M, N, K)
+
+                def fused(lin=lin, gate=gate, upv=upv, cm=cm, q_ws=q_ws, s_ws=s_ws, M=M, K=K, N=N):
+                    w, s = lin.next()
+                    HK.silu_mul_quant_fp8(q_ws, s_ws, gate, upv, M, K)
+                    HK.linear_fp8(cm, None, w, s, q_ws, s_ws, M, N, K, do_quantize=False)
+            elif lin.name in ("qkv", "gate_up"):
+                src = act(M, K, seed=M + 3)
+                gam = (1.0 + 0.1 * torch.randn(K, device="cuda")).to(torch.bfloat16)
+                y = torch.empty(M, K, dtype=torch.bfloat16, device="cuda")
+
+                def unfused(lin=lin, src=src, gam=gam, y=y, cm=cm, q_ws=q_ws, s_ws=s_ws, M=M, K=K, N=N):
+                    w, s = lin.next()
+                    DEC.rmsnorm(y, src, gam)
+                    HK.linear_fp8(cm, y, w, s, q_ws, s_ws, M, N, K)
+
+                def fused(lin=lin, src=src, gam=gam, cm=cm, q_ws=q_ws, s_ws=s_ws, M=M, K=K, N=N):
+                    w, s = lin.next()
+                    HK.rmsnorm_quant_fp8(q_ws, s_ws, src, gam, M, K)
+                    HK.linear_fp8(cm, None, w, s, q_ws, s_ws, M, N, K, do_quantize=False)
+            else:
+                src = act(M, K, seed=M + 4)
+
+                def unfused(lin=lin, src=src, cm=cm, q_ws=q_ws, s_ws=s_ws, M=M, K=K, N=N):
+                    w, s = lin.next()
+                    HK.linear_fp8(cm, src, w, s, q_ws, s_ws, M, N, K)
+                fused = unfused
+            t_end = time.perf_counter() + 0.02
+            while time.perf_counter() < t_end:
+                for _ in range(8):
+                    fused()
+                torch.cuda.synchronize()
+            ms_u = graph_call_ms(unfused, 20)
+            ms_f = graph_call_ms(fused, 20)
+            fl = 2.0 * M * N * K
+            row[lin.name] = {"unfused_us": round(ms_u * 1e3, 2), "fused_us": round(ms_f * 1e3, 2),
+                             "unfused_TFLOPs": round(fl / (ms_u * 1e-3) / 1e12, 1),
+                             "fused_TFLOPs": round(fl / (ms_f * 1e-3) / 1e12, 1)}
+        tot_u = sum(v["unfused_us"] for v in row.values())
+        tot_f = sum(v["fused_us"] for v in row.values())
+        fl = sum(2.0 * M * l.N * l.K for l in lins)
+        row["all"] = {"unfused_us": round(tot_u, 2), "fused_us": round(tot_f, 2),
+                      "fused_TFLOPs": round(fl / (tot_f * 1e-6) / 1e12, 1),
+                      "unfused_TFLOPs": round(fl / (tot_u * 1e-6) / 1e12, 1)}
+        out[f"M={M}"] = row
+    return out
 
 
 def decode_step_timing(steps=20):

@@ -68,6 +68,9 @@ struct Fp8Operands {
     float* part = nullptr;
     size_t part_bytes = 0;
     int splits = 1;
+    // Batched-decode K splits: the value the launch's completion flags
+    // carry (unique per launch).
+    uint64_t epoch = 0;
     Tuning tune;
 };
 
@@ -119,8 +122,8 @@ bool gemm_splits_ready(const Fp8Operands& op);
 hipError_t launch_splitk_reduce(const Fp8Operands& op, hipStream_t stream, const LaunchTiming& t);
 
 // Batched decode (M <= 32, per-chunk activation scales): 64-column
-// workgroups over K splits, reading q/s from the workspace; partials in
-// op.part when it splits. Split count for M x N x K (forced > 0 raises it
+// workgroups over K splits in one launch, reading q/s from the workspace;
+// partials and completion flags in op.part when it splits. Split count for M x N x K (forced > 0 raises it
 // to at least that), its scratch bytes (automatic count), and whether op's
 // scratch holds the partials of op's count.
 // fused: quantize x inside (group 128); column tile 0 writes q/s.

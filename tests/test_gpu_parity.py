@@ -982,6 +982,75 @@ def test_batch_split_kernel_forced_splits_ragged(M, kc, splits):
         T.TUNE.clear()
 
 
+def test_batch_split_flags_graph_replays_and_garbage_workspace():
+    # With 2 or 3 splits the K-split kernel sums its splits in one launch:
+    # the last split of a column tile waits for the others' completion flags
+    # (the call's epoch) and clears them. Checked here: a workspace whose
+    # scratch starts as random bytes or all-ones; back-to-back calls of
+    # different shapes on one workspace (flags at other offsets, other
+    # epochs, and a 10-split call through the reduction kernel between); a
+    # HIP graph replayed five times with eager calls between, every replay
+    # bitwise equal to the eager result (a replay repeats its epoch, so the
+    # clearing matters).
+    M = 32
+    cases = [("qkv", 6144, 2560), ("down", 2560, 9728), ("k12", 2560, 1536)]
+    Kmax, Nmax = 9728, 6144
+    xh = {K: O.gen_act_bf16(300 + K, M, K) for _, _, K in cases}
+    wh = {n: O.gen_weight(310 + i, N, K) for i, (n, N, K) in enumerate(cases)}
+    x = {K: dev(a) for K, a in xh.items()}
+    wts = {n: (dev(qw), dev(sw)) for n, (qw, sw) in wh.items()}
+    outs = {n: torch.zeros(M, N, dtype=torch.bfloat16, device="cuda") for n, N, _ in cases}
+    need = max(L.lib().heph_fp8_linear_ws_bytes(M, N, K) for _, N, K in cases)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    q_ws = torch.randint(0, 256, (need,), dtype=torch.uint8, device="cuda", generator=g)
+    s_ws = torch.empty(M * (Kmax // 128), dtype=torch.float32, device="cuda")
+
+    def run(tune={"batch_split": 1}):
+        for n, N, K in cases:
+            w, sw = wts[n]
+            HK.linear_fp8(outs[n], x[K], w, sw, q_ws, s_ws, M, N, K, tune=tune)
+
+    # reference outputs: the chunk-slot GEMV (no flags) vs the oracle
+    ref = {}
+    for n, N, K in cases:
+        w, sw = wts[n]
+        want = O.quant_linear(xh[K], *wh[n])
+        run_one = torch.zeros(M, N, dtype=torch.bfloat16, device="cuda")
+        ws2 = HK.workspace(M, K)
+        HK.linear_fp8(run_one, x[K], w, sw, ws2[0], ws2[1], M, N, K, tune={"batch_split": -1})
+        check_close(host_bf16(run_one), want, f"{n} gemv")
+        ref[n] = want
+    run()
+    torch.cuda.synchronize()
+    assert HK.last_kernel() == "fp8_gemv_split64_fused_splitk", HK.last_kernel()
+    eager = {n: outs[n].clone() for n in outs}
+    for n, _, _ in cases:
+        check_close(host_bf16(eager[n]), ref[n], f"{n} split, random workspace")
+    q_ws.fill_(255)                          # all-ones flags and partials
+    run()
+    torch.cuda.synchronize()
+    for n in outs:
+        assert torch.equal(outs[n], eager[n]), n
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        run()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            run()
+    for rep in range(5):
+        for c in outs.values():
+            c.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        for n in outs:
+            assert torch.equal(outs[n], eager[n]), (n, rep)
+        run()                                # eager calls (new epochs) between replays
+        torch.cuda.synchronize()
+        for n in outs:
+            assert torch.equal(outs[n], eager[n]), (n, rep, "eager")
+
+
 @pytest.mark.parametrize("out,resid", [("bf16", False), ("f32", True)])
 def test_large_m_split_k_every_tile(out, resid, tile_m):
     # Few tiles (M = 200, N = 272) and 17 chunks: every forced tile height
