@@ -593,25 +593,37 @@ int gemv_rows(int M)
     return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16;
 }
 
-// Launch shape: the fewest chunk slots (at most 16 / rows-per-slot) that
-// give >= 600 workgroups (about 2.3 per CU); 4 waves when there are at most
-// 8 steps, else 8 (16 only when forced, for 8 < M <= 16); at M = 1, 2-step
-// batches when each wave has at most 2 steps, else (and for M > 1, whose
-// wider activation tiles need the registers) 1-step batches.
+// Launch shape. Chunk slots: at M <= 2 the fewest (at most 16 / rows per
+// slot) that give >= 600 workgroups (about 2.3 per CU); at 4 and 8 rows
+// per slot one (two at 4 rows when K >= 8192), as every workgroup quantizes
+// all M x K activations again and wider workgroups do that less often
+// (MI355X, graph-replayed, fused: M = 8 qkv 7.6 against 9.1 us with two
+// slots, o_proj 6.3 against 7.6, down 13.3 against 16.5); 16 rows: one.
+// Waves: 4 when there are fewer than 8 steps (at M = 1, up to 8), else 8,
+// and at 9..16 rows 4 up to 24 steps (M = 16 qkv 9.9 against 10.9 us); 16 only when forced,
+// for 8 < M <= 16. Steps per batch: at M = 1 two when each wave has at
+// most 2 steps; at 5..8 rows with K >= 8192 two; else one (wider
+// activation tiles need the registers).
 void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, int* u)
 {
     const int mr = gemv_rows(M);
     const int kmax = mr >= 2 ? 16 / mr : 8;
     const int tiles = N / 16, KC = K / kChunk;
     int k = 1;
-    while (k < kmax && tiles * k < 600) k *= 2;
+    if (mr <= 2)
+        while (k < kmax && tiles * k < 600) k *= 2;
+    else if (mr == 4 && K >= 8192)
+        k = 2;
     const int fk = tune.gemv_ks;
     if (fk) k = fk < kmax ? fk : kmax;
     const int S = (KC + k - 1) / k;
-    int w = S <= 8 ? 4 : 8;
+    int w = S < 8 || (mr == 1 && S == 8) ? 4 : 8;
+    if (mr == 16 && M <= 16 && S <= 24) w = 4;
     const int fw = tune.gemv_waves;
     if (fw) w = fw == 16 && (mr != 16 || M > 16) ? 8 : fw;
-    int uu = mr == 1 && (S + w - 1) / w <= 2 ? 2 : 1;
+    int uu = 1;
+    if (mr == 1 && (S + w - 1) / w <= 2) uu = 2;
+    if (mr == 8 && K >= 8192) uu = 2;
     const int fu = tune.gemv_u;
     if (fu) uu = fu;
     if (w == 16) uu = 1;    // two-step batches would not fit 128 VGPRs

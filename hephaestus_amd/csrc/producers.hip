@@ -75,7 +75,9 @@ __device__ __forceinline__ void quant_row_from_lds(const uint16_t* yrow, int col
 // One 256-thread workgroup per row. The norm is heph_rmsnorm's: thread t
 // owns elements t, t + 256, ... and sums their squares in that order (fma),
 // the 256 sums fold as fold256_wave0 does, and y = bf16(gamma * bf16(x * r)).
-// y goes to LDS instead of global memory; then the row is quantized.
+// y goes to LDS instead of global memory (dynamic, 2 * cols bytes, so that
+// short rows leave room for more workgroups per CU); then the row is
+// quantized.
 template <int PER>
 __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(uint8_t* q, float* scales,
                                                             const uint16_t* in,
@@ -84,7 +86,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(uint8_t* q, float* s
 {
     __shared__ float red[256];
     __shared__ float res;
-    __shared__ __attribute__((aligned(16))) uint16_t yrow[kProdMaxCols];
+    extern __shared__ __attribute__((aligned(16))) uint16_t yrow[];
     const uint16_t* x = in + (size_t)blockIdx.x * cols;
     const int t = threadIdx.x;
     if constexpr (PER > 0) {
@@ -179,7 +181,7 @@ __global__ __launch_bounds__(256) void silu_mul_quant_row_kernel(uint8_t* q, flo
                                                                  const uint16_t* up, int n,
                                                                  long ld)
 {
-    __shared__ __attribute__((aligned(16))) uint16_t yrow[kProdMaxCols];
+    extern __shared__ __attribute__((aligned(16))) uint16_t yrow[];    // n bf16
     const size_t off = (size_t)blockIdx.x * ld;
     for (int k = threadIdx.x * 8; k < n; k += 256 * 8)
         *reinterpret_cast<uint4*>(yrow + k) = swiglu8(ldg16u(gate + off + k), ldg16u(up + off + k));
@@ -209,17 +211,18 @@ int heph_rmsnorm_quant_fp8(uint8_t* q, float* scales, const uint16_t* x_bf16,
     if (int st = check_device()) return st;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int per = (cols + 255) / 256;
+    const size_t lds = (size_t)cols * 2;
     if (per <= 10)
-        rmsnorm_quant_kernel<10><<<rows, 256, 0, s>>>(q, scales, x_bf16, gamma_bf16, cols, eps,
+        rmsnorm_quant_kernel<10><<<rows, 256, lds, s>>>(q, scales, x_bf16, gamma_bf16, cols, eps,
                                                       group_k);
     else if (per <= 16)
-        rmsnorm_quant_kernel<16><<<rows, 256, 0, s>>>(q, scales, x_bf16, gamma_bf16, cols, eps,
+        rmsnorm_quant_kernel<16><<<rows, 256, lds, s>>>(q, scales, x_bf16, gamma_bf16, cols, eps,
                                                       group_k);
     else if (per <= 40)
-        rmsnorm_quant_kernel<40><<<rows, 256, 0, s>>>(q, scales, x_bf16, gamma_bf16, cols, eps,
+        rmsnorm_quant_kernel<40><<<rows, 256, lds, s>>>(q, scales, x_bf16, gamma_bf16, cols, eps,
                                                       group_k);
     else
-        rmsnorm_quant_kernel<0><<<rows, 256, 0, s>>>(q, scales, x_bf16, gamma_bf16, cols, eps,
+        rmsnorm_quant_kernel<0><<<rows, 256, lds, s>>>(q, scales, x_bf16, gamma_bf16, cols, eps,
                                                      group_k);
     return hipGetLastError() == hipSuccess ? HEPH_OK : HEPH_ERR_LAUNCH;
 }
@@ -241,8 +244,8 @@ int heph_silu_mul_quant_fp8(uint8_t* q, float* scales, const uint16_t* gate_bf16
         silu_mul_quant_g128_kernel<<<blocks, 256, 0, s>>>(q, scales, gate_bf16, up_bf16, n,
                                                           (long)ld, n_groups);
     } else {
-        silu_mul_quant_row_kernel<<<rows, 256, 0, s>>>(q, scales, gate_bf16, up_bf16, n,
-                                                       (long)ld);
+        silu_mul_quant_row_kernel<<<rows, 256, (size_t)n * 2, s>>>(q, scales, gate_bf16, up_bf16,
+                                                                    n, (long)ld);
     }
     return hipGetLastError() == hipSuccess ? HEPH_OK : HEPH_ERR_LAUNCH;
 }
