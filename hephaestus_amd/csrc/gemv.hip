@@ -599,11 +599,13 @@ int gemv_rows(int M)
 // all M x K activations again and wider workgroups do that less often
 // (MI355X, graph-replayed, fused: M = 8 qkv 7.6 against 9.1 us with two
 // slots, o_proj 6.3 against 7.6, down 13.3 against 16.5); 16 rows: one.
-// Waves: 4 when there are fewer than 8 steps (at M = 1, up to 8), else 8,
-// and at 9..16 rows 4 up to 24 steps (M = 16 qkv 9.9 against 10.9 us); 16 only when forced,
-// for 8 < M <= 16. Steps per batch: at M = 1 two when each wave has at
-// most 2 steps; at 5..8 rows with K >= 8192 two; else one (wider
-// activation tiles need the registers).
+// Waves: at M = 1, 8 from 4 steps on (o_proj 4.85 against 5.06 us with 4
+// waves of 2-step batches, q_proj 4.70 against 4.97); at M >= 2, 4 when
+// there are fewer than 8 steps, else 8, and at 9..16 rows 4 up to 24
+// steps (M = 16 qkv 9.9 against 10.9 us); 16 only when forced, for
+// 8 < M <= 16. Steps per batch: at M = 1 two when each wave has exactly
+// 2 steps; at 5..8 rows with K >= 8192 two; else one (wider activation
+// tiles need the registers).
 void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, int* u)
 {
     const int mr = gemv_rows(M);
@@ -617,12 +619,12 @@ void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, in
     const int fk = tune.gemv_ks;
     if (fk) k = fk < kmax ? fk : kmax;
     const int S = (KC + k - 1) / k;
-    int w = S < 8 || (mr == 1 && S == 8) ? 4 : 8;
+    int w = mr == 1 ? (S <= 3 ? 4 : 8) : (S < 8 ? 4 : 8);
     if (mr == 16 && M <= 16 && S <= 24) w = 4;
     const int fw = tune.gemv_waves;
     if (fw) w = fw == 16 && (mr != 16 || M > 16) ? 8 : fw;
     int uu = 1;
-    if (mr == 1 && (S + w - 1) / w <= 2) uu = 2;
+    if (mr == 1 && (S + w - 1) / w == 2) uu = 2;
     if (mr == 8 && K >= 8192) uu = 2;
     const int fu = tune.gemv_u;
     if (fu) uu = fu;
