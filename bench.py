@@ -131,22 +131,28 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--prefill-pass", action="store_true",
-                    help="only run the configs[3] M = 4096 prefill launches eagerly (quant + "
-                         "GEMM, 10 per shape, for rocprofv3 traces); prints no JSON")
+                    help="only run the configs[3] M = 4096 prefill launches eagerly (per "
+                         "shape 100 + --steps GEMM launches on quantized activations, then "
+                         "--steps quantizer launches; for rocprofv3 traces and counters); "
+                         "prints no JSON")
     ap.add_argument("--decode-pass", action="store_true",
                     help="only run configs[4] decode steps eagerly (random-init Qwen3-4B, "
                          "4096 cached tokens; for rocprofv3 traces); prints no JSON")
     ap.add_argument("--pmc-pass", action="store_true",
-                    help="only run the M = 1 launches eagerly plus a 256 MiB device "
-                         "copy (for rocprofv3 --pmc traffic counts); prints no JSON")
+                    help="only run the M = 1, 16 and 32 launches (2 eager calls, then a "
+                         "HIP graph of --steps calls replayed 4 times, per shape) plus a 256 "
+                         "MiB device copy (for rocprofv3 --pmc traffic counts and kernel "
+                         "traces); prints no JSON")
     return ap.parse_args()
 
 
 def prefill_pass(steps):
-    """configs[3] at M = 4096: quantize + GEMM for each shape, eagerly, over
-    the rotated weight copies (as the detail sweep: weights come from HBM,
-    not the Infinity Cache); 100 launches per shape before the counted ones,
-    so that every shape runs at the clock sustained under FP8 MFMA load."""
+    """configs[3] at M = 4096, per shape: the activations quantized once,
+    then the GEMM alone (SKIP_QUANT, as the bench's kernel-only prefill
+    figure) eagerly over the rotated weight copies (weights come from HBM,
+    not the Infinity Cache), 100 launches before the `steps` counted ones so
+    that every shape runs at the clock sustained under FP8 MFMA load; then
+    `steps` launches of the activation quantizer alone."""
     import torch
     from hephaestus_amd import kernels as HK
     torch.cuda.set_device(0)
@@ -155,12 +161,18 @@ def prefill_pass(steps):
         lin = Linear(name, N, K, M, seed=100 + i)
         x = act(M, K, seed=M + 1, outliers=True)
         c = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        HK.quantize_act_rows_fp8(lin.q_ws, lin.s_ws, x, M, K)
         for _ in range(100 + steps):
             w, s = lin.next()
-            HK.linear_fp8(c, x, w, s, lin.q_ws, lin.s_ws, M, N, K)
+            HK.linear_fp8(c, None, w, s, lin.q_ws, lin.s_ws, M, N, K, do_quantize=False)
         torch.cuda.synchronize()
-        print(f"prefill-pass {name} M={M} N={N} K={K} kernel={HK.last_kernel()} "
-              f"launches={100 + steps} (the last {steps} are the measured ones)", flush=True)
+        kern = HK.last_kernel()
+        for _ in range(steps):
+            HK.quantize_act_rows_fp8(lin.q_ws, lin.s_ws, x, M, K)
+        torch.cuda.synchronize()
+        print(f"prefill-pass {name} M={M} N={N} K={K} kernel={kern}: 1 quantizer launch, "
+              f"{100 + steps} GEMM launches (the last {steps} are the measured ones), "
+              f"{steps} quantizer launches", flush=True)
         del lin
     a = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
     b = torch.empty_like(a)
@@ -190,23 +202,44 @@ def decode_pass(steps):
 
 
 def pmc_pass(steps):
-    """Eager M = 1 launches of every shape and one plain copy of known size.
+    """Launches of every shape at M = 1, then the configs[2] batched decode
+    sizes M = 16 and 32 (bf16 rows, default route), and one plain copy of
+    known size.
 
     Under rocprofv3 --pmc FETCH_SIZE (or WRITE_SIZE) the copy kernel's count
     calibrates the counter: bytes = count * (copy bytes / copy count)."""
     import torch
     from hephaestus_amd import kernels as HK
     torch.cuda.set_device(0)
-    lins = [Linear(n, N, K, 1, seed=100 + i) for i, (n, N, K) in enumerate(SHAPES)]
-    for lin in lins:
-        x = act(1, lin.K, seed=lin.K)
-        c = torch.empty(1, lin.N, dtype=torch.bfloat16, device="cuda")
-        for _ in range(steps):
-            w, s = lin.next()
-            HK.linear_fp8(c, x, w, s, lin.q_ws, lin.s_ws, 1, lin.N, lin.K)
-        torch.cuda.synchronize()
-        print(f"pmc-pass {lin.name} N={lin.N} K={lin.K} kernel={HK.last_kernel()} "
-              f"launches={steps}", flush=True)
+    lins = [Linear(n, N, K, 32, seed=100 + i) for i, (n, N, K) in enumerate(SHAPES)]
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    for M in (1, 16, 32):
+        for lin in lins:
+            x = act(M, lin.K, seed=lin.K + M)
+            c = torch.empty(M, lin.N, dtype=torch.bfloat16, device="cuda")
+
+            def call(lin=lin, x=x, c=c, M=M):
+                w, s = lin.next()
+                HK.linear_fp8(c, x, w, s, lin.q_ws, lin.s_ws, M, lin.N, lin.K)
+            # two eager calls, then `steps` calls captured in a HIP graph:
+            # back to back on the GPU, as in bench.py's timed region
+            with torch.cuda.stream(stream):
+                call()
+                call()
+                torch.cuda.synchronize()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    for _ in range(steps):
+                        call()
+            # four replays back to back: the first ones bring the shader
+            # clock up from the idle gaps of the set-up; read the last
+            for _ in range(4):
+                graph.replay()
+            torch.cuda.synchronize()
+            print(f"pmc-pass M={M} {lin.name} N={lin.N} K={lin.K} kernel={HK.last_kernel()} "
+                  f"calls=2 eager + 4 x {steps} graph-replayed (the last {steps} are the "
+                  f"measured ones)", flush=True)
     a = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
     b = torch.empty_like(a)
     for _ in range(3):

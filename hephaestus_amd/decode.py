@@ -254,15 +254,12 @@ class Qwen3Decoder:
             rec(li, "o_residual", self.x)
             self._norm_linear(self.gu, lw.ffn_norm, lw.gate_up, H, eps, rec, li, "ffn_norm")
             rec(li, "gate_up", self.gu)
-            # SwiGLU writes the down projection's codes and scales itself
-            # (bit for bit silu_mul then the quantizer), so down skips its own
-            # quantization pass; a traced step also keeps the bf16 row
-            HK.silu_mul_quant_fp8(self.q_ws, self.s_ws, self.gu, self.gu[:, I:], 1, I)
-            if rec.tracing:
-                silu_mul(self.act, self.gu, self.gu[:, I:], I)
-                rec(li, "silu_mul", self.act)
-            HK.linear_add_residual_fp8(self.x, None, lw.down.w, lw.down.scale, self.q_ws,
-                                       self.s_ws, 1, lw.down.N, I, do_quantize=False)
+            # SwiGLU, then down with its quantization fused in the GEMV: for one
+            # row ~1.2 us per layer faster on MI355X than the producer-side
+            # form (heph_silu_mul_quant_fp8), which pays at prefill sizes
+            silu_mul(self.act, self.gu, self.gu[:, I:], I)
+            rec(li, "silu_mul", self.act)
+            self._linear(self.x, self.act, lw.down, I, residual=True)
             rec(li, "down_residual", self.x)
         self._norm_linear(self.logits, w.final_norm, w.embed, H, eps, rec, -1, "final_norm")
         rec(-1, "logits", self.logits)
