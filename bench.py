@@ -114,6 +114,92 @@ def achievable_read(sizes, timer_graph_calls=20):
     return out
 
 
+def achievable_mfma(blocks=1024, iters=16384):
+    """The MFMA denominator: FP8 TFLOP/s of a loop of independent
+    v_mfma_f32_16x16x128_f8f6f4 on pseudo-random E4M3 register operands
+    (four sets, cycled, so the multipliers switch as on real data) with no
+    memory traffic (hephaestus_amd/bench_csrc/hbm_read.hip), 4 waves per
+    workgroup, after one untimed launch; HIP events over three launches."""
+    import ctypes
+    import torch
+    lib = ctypes.CDLL(BENCH_LIB)
+    lib.heph_bench_mfma.restype = ctypes.c_int
+    lib.heph_bench_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    sink = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+
+    def run():
+        st = lib.heph_bench_mfma(blocks, iters, sink.data_ptr(),
+                                 torch.cuda.current_stream().cuda_stream)
+        if st:
+            raise RuntimeError(f"heph_bench_mfma failed: {st}")
+    run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(3):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / 3
+    flops = blocks * 4.0 * iters * 8 * 65536
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"TFLOPs": round(tf, 1), "frac_of_peak": round(tf / FP8_PEAK_TFLOPS, 4),
+            "ms_per_launch": round(ms, 3),
+            "method": f"{blocks} workgroups x 4 waves x {iters} rounds of 8 independent "
+                      "16x16x128 FP8 MFMAs, pseudo-random register operands cycled over 4 "
+                      "sets, HIP events over 3 launches"}
+
+
+def vendor_fp8_gemm(M=4096, calls=10):
+    """hipBLASLt's FP8 GEMM through torch._scaled_mm on the configs[3] shapes
+    at M = 4096: E4M3 operands with one fp32 scale per tensor (the vendor
+    library has no 128x128 block-scale mode), bf16 out, weights rotated past
+    the Infinity Cache as for this library's GEMM; per call (HIP events
+    around `calls` calls after ~20 ms of the same calls). A comparison, not
+    a parity check."""
+    import torch
+    out = {}
+    if not hasattr(torch, "_scaled_mm"):
+        return {"error": "torch._scaled_mm unavailable"}
+    one = torch.ones((), dtype=torch.float32, device="cuda")
+    tot_fl, tot_us = 0.0, 0.0
+    for i, (name, N, K) in enumerate(SHAPES):
+        a = act(M, K, seed=M + 7).to(torch.float8_e4m3fn)
+        copies = max(1, math.ceil(ROTATE_BYTES / (N * K)))
+        g = torch.Generator(device="cuda").manual_seed(300 + i)
+        w0 = (torch.randn(N, K, generator=g, device="cuda") * 0.5).to(torch.float8_e4m3fn)
+        ws = [w0] + [w0.clone() for _ in range(copies - 1)]
+        it = [0]
+
+        def run(ws=ws, it=it, a=a):
+            w = ws[it[0] % len(ws)]
+            it[0] += 1
+            return torch._scaled_mm(a, w.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+        try:
+            run()
+        except Exception as e:          # no FP8 GEMM for this build / device
+            return {"error": f"torch._scaled_mm failed: {type(e).__name__}: {e}"[:200]}
+        t_end = time.perf_counter() + 0.02
+        while time.perf_counter() < t_end:
+            for _ in range(4):
+                run()
+            torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(calls):
+            run()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / calls
+        fl = 2.0 * M * N * K
+        out[name] = {"us": round(us, 2), "TFLOPs": round(fl / (us * 1e-6) / 1e12, 1)}
+        tot_fl += fl
+        tot_us += us
+        del ws
+    out["all"] = {"us": round(tot_us, 2), "TFLOPs": round(tot_fl / (tot_us * 1e-6) / 1e12, 1)}
+    return out
+
+
 def fp8_bytes(M, N, K):
     return N * K + (-(-N // 128)) * (K // 128) * 4 + M * K * 2 + M * N * 2
 
@@ -472,6 +558,12 @@ def main():
                         "(activations quantized beforehand), weights rotated past the "
                         "Infinity Cache",
             "path_TFLOPs_quant_plus_gemm": detail.get("prefill_m4096_TFLOPs")}
+        am = detail.get("achievable_mfma")
+        if am and am.get("TFLOPs"):
+            line["prefill_roofline"]["frac_of_achievable_mfma"] = round(pk["TFLOPs"] / am["TFLOPs"], 4)
+        vg = (detail.get("vendor_fp8_gemm_m4096") or {}).get("all")
+        if vg:
+            line["prefill_roofline"]["vs_hipblaslt_per_tensor_fp8"] = round(pk["TFLOPs"] / vg["TFLOPs"], 3)
     print(json.dumps(line))
 
 
@@ -564,6 +656,8 @@ def detail_sweeps(lins):
         pre[f"M={M}"] = row
     out["prefill"] = pre
     out["prefill_m4096_kernel"] = prefill_kernel_times(lins, timer)
+    out["achievable_mfma"] = achievable_mfma()
+    out["vendor_fp8_gemm_m4096"] = vendor_fp8_gemm()
     out["prefill_producer_path"] = prefill_producer_path(lins)
     out["decode_step_config4"] = decode_step_timing()
     t4096 = sum(2.0 * 4096 * l.N * l.K for l in lins)
