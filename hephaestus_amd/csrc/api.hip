@@ -271,6 +271,7 @@ int heph_fp8_linear_rmsnorm(void* c, int c_dtype, const uint16_t* x_bf16,
 {
     if (!gamma_bf16 || !x_bf16) return HEPH_ERR_NULL;
     if (flags & ~HEPH_FLAG_ADD_RESIDUAL) return HEPH_ERR_FLAGS;
+    if (!aligned16(gamma_bf16)) return HEPH_ERR_ALIGN;     // read in 16-byte pieces
     if (K > kNormMaxK) return HEPH_ERR_UNSUPPORTED;
     return fp8_linear_impl(c, c_dtype, x_bf16, w, w_scale, w_block_n, w_block_k, q_ws,
                            q_ws_bytes, s_ws, s_ws_floats, 1, N, K, kChunk, flags, stream,

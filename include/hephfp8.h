@@ -120,9 +120,10 @@ int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16,
  * bit heph_rmsnorm followed by heph_fp8_linear; the workspaces hold the
  * normalized row's codes and scales. Replaces the pair rms_norm + linear_fp8
  * of the reference's decode step (src/hephaestus/forward.mojo:359-615,
- * kernels.mojo:653-762). flags: HEPH_FLAG_ADD_RESIDUAL only; K <= 8192
- * (the row and gamma sit in the workgroup's LDS), else HEPH_ERR_UNSUPPORTED
- * (callers with longer rows run heph_rmsnorm, then heph_fp8_linear).
+ * kernels.mojo:653-762). flags: HEPH_FLAG_ADD_RESIDUAL only; gamma 16-byte
+ * aligned (HEPH_ERR_ALIGN); K <= 8192 (the row and gamma sit in the
+ * workgroup's LDS), else HEPH_ERR_UNSUPPORTED (callers with longer rows run
+ * heph_rmsnorm, then heph_fp8_linear).
  */
 int heph_fp8_linear_rmsnorm(void* c, int c_dtype, const uint16_t* x_bf16,
                             const uint16_t* gamma_bf16, float eps, const uint8_t* w,

@@ -152,6 +152,8 @@ def test_rmsnorm_linear_rejects(lib):
     assert f(*args(8320)) == L.HEPH_ERR_UNSUPPORTED
     assert f(*args(2560, flags=L.FLAG_SKIP_QUANT)) == L.HEPH_ERR_FLAGS
     assert f(*args(2560, gamma=None)) == L.HEPH_ERR_NULL
+    # gamma is read in 16-byte pieces
+    assert f(*args(2560, gamma=FAKE + 2)) == L.HEPH_ERR_ALIGN
     assert f(*args(8192)) in (L.HEPH_ERR_DEVICE, L.HEPH_OK)
 
 
