@@ -58,9 +58,10 @@ namespace {
 
 constexpr int kSplitCols = 64;     // output columns per workgroup (4 waves x 16)
 constexpr int kSplitMaxKB = 8;     // chunks per split at most
-// Polls of a completion flag before the last split gives up (each poll
-// sleeps ~128 cycles: about a quarter of a second in all).
-constexpr int kSpinLimit = 1 << 21;
+// Polls of a completion flag before the last split gives up: each poll is
+// a load from the coherent level (~1 us) and a ~128-cycle sleep, so about
+// a quarter to half a second in all.
+constexpr int kSpinLimit = 1 << 18;
 // Split counts up to this sum their partials inside the launch (the last
 // split of a tile waits for the others); larger counts store every split's
 // partials and leave the sum to the reduction kernel. On MI355X at M = 32
