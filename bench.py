@@ -6,8 +6,11 @@ Qwen3-4B FP8 linear shape -- fused QKV 6144x2560, o_proj 2560x4096, fused
 gate_up 19456x2560, down_proj 2560x9728 -- each with dynamic 1x128-group
 activation quantization, 128x128 block-scaled E4M3 weights, fp32
 accumulation and bf16 output. One step is one pass over the four shapes
-(one decoder layer's FP8 linears). Inputs are synthetic and seeded on the
-GPU (W ~ N(0, 0.02) quantized per 128x128 block, x ~ N(0, 1) in bf16).
+(one decoder layer's FP8 linears). Inputs are synthetic: the seeded
+splitmix64 + Box-Muller generator of the parity tests, run on the host
+(W ~ N(0, 0.02) in bf16, quantized per 128x128 block by the library;
+x ~ N(0, 1) in bf16), every input checked against its committed FNV-1a
+digest ("input_digests").
 Every shape's weights are rotated over enough distinct copies (>= 640 MB)
 that the 256 MB Infinity Cache cannot hold them between launches.
 
@@ -17,10 +20,9 @@ graph and bracketed by device synchronizations. Algorithmic bytes of one
 FP8 linear = N*K + ceil(N/128)*(K/128)*4 + M*K*2 + M*N*2.
 
 "roofline" covers the dominant kernel (the fused M = 1 weight-streaming
-kernel): achieved = algorithmic bytes / kernel duration, both summed over
---steps eager steps of the same launches, with durations stamped at each
-kernel's own begin and end by HIP events (hipExtLaunchKernel) on the launch
-stream.
+kernel, the only kernel of the step): achieved = algorithmic bytes of the
+timed steps / the time between HIP events recorded on the replay stream
+around the timed graph replays.
 "detail" adds per-shape figures, the bf16 lm_head, the batched-decode M
 sweep (configs[2], per call graph-replayed over rotated weights, as the
 M = 1 line) and the prefill GEMM at M = 512 and 4096 (configs[3], quant +
@@ -71,6 +73,99 @@ def profiled_traffic(path=TRAFFIC_PROFILE):
 
 BENCH_LIB = os.path.join(os.path.dirname(os.path.abspath(__file__)), "hephaestus_amd",
                          "libhephbench.so")
+
+# Seeds of the synthetic inputs (hephaestus_amd/bench_csrc/synth.cpp, the
+# parity tests' splitmix64 + Box-Muller stream). Weights: W ~ N(0, 0.02)
+# rounded to bf16 (the checkpoint dtype FP8 staging starts from) and
+# quantized per 128 x 128 block by the library; activations: x ~ N(0, 1) in
+# bf16, with ~0.1 % of entries x 50 where a configuration asks for outliers.
+CONFIG0_SEED = 0                 # configs[0]'s activation row
+WEIGHT_SEEDS = {"qkv": 100, "o_proj": 101, "gate_up": 102, "down": 103, "q_proj": 7,
+                "lm_head": 9}
+
+# FNV-1a 64 digests of the inputs as generated here and on the GPU box:
+# <shape>_w_bf16 the generated weights, <shape>_w_e4m3 / <shape>_scale_inv the
+# library's quantization of them copied back from the GPU, x_* the
+# activation rows (x_m1_k<K>: the M = 1 rows of seed K). tests/test_bench_synth.py
+# derives every one from the generator and the CPU quantizer.
+BENCH_DIGESTS = {
+    "qkv_w_bf16": "612137bbc3d5d4b6", "qkv_w_e4m3": "bfc7373ef4d6d4a3",
+    "qkv_scale_inv": "b4b83f5d901d6e30",
+    "o_proj_w_bf16": "adea71fe3c873096", "o_proj_w_e4m3": "baa6e6e5d986a82e",
+    "o_proj_scale_inv": "f23d23453abccea5",
+    "gate_up_w_bf16": "f06f48183227526e", "gate_up_w_e4m3": "dcb1ea786f46ec8f",
+    "gate_up_scale_inv": "df2bb0da8c37348e",
+    "down_w_bf16": "9201ededf4bfeab4", "down_w_e4m3": "a2c565dce55f9db7",
+    "down_scale_inv": "5be0ebc17ef0c8cf",
+    "q_proj_w_bf16": "d0076a63d0e81feb", "q_proj_w_e4m3": "746abfc13619fe61",
+    "q_proj_scale_inv": "981e450e75ad742c",
+    "lm_head_w_bf16": "3fd6190e415a50eb",
+    "x_config0": "64959a856e22d0ff",
+    "x_m1_k2560": "2183ab0aabdb581f", "x_m1_k4096": "061f45ac35038d6c",
+    "x_m1_k9728": "0e151c44c17df616",
+}
+
+_SYNTH = None
+INPUT_CHECKS = {}                # digest name -> matched
+
+
+def synth():
+    """libhephbench.so's generator and digest entry points (ctypes)."""
+    global _SYNTH
+    if _SYNTH is None:
+        import ctypes
+        lib = ctypes.CDLL(BENCH_LIB)
+        u64, sz, f32, f64, vp = (ctypes.c_uint64, ctypes.c_size_t, ctypes.c_float,
+                                 ctypes.c_double, ctypes.c_void_p)
+        lib.heph_bench_gen_normal.argtypes = [u64, u64, sz, f32, f32, vp]
+        lib.heph_bench_gen_normal.restype = None
+        lib.heph_bench_gen_normal_bf16.argtypes = [u64, u64, sz, f32, f32, vp]
+        lib.heph_bench_gen_normal_bf16.restype = None
+        lib.heph_bench_gen_act_bf16.argtypes = [u64, sz, f64, f32, vp]
+        lib.heph_bench_gen_act_bf16.restype = None
+        lib.heph_bench_fnv1a64.argtypes = [vp, sz]
+        lib.heph_bench_fnv1a64.restype = u64
+        _SYNTH = lib
+    return _SYNTH
+
+
+def fnv1a64(a) -> str:
+    """Digest of a contiguous numpy array's bytes."""
+    import numpy as np
+    a = np.ascontiguousarray(a)
+    return "%016x" % synth().heph_bench_fnv1a64(a.ctypes.data, a.nbytes)
+
+
+def check_digest(name, a):
+    """Records whether array a matches the committed digest `name`."""
+    want = BENCH_DIGESTS.get(name)
+    if want is None:
+        return
+    ok = fnv1a64(a) == want
+    INPUT_CHECKS[name] = ok
+    if not ok:
+        print(f"bench: input {name} does not match its committed digest", file=sys.stderr,
+              flush=True)
+
+
+def host_normal_bf16(seed, n, mean, std):
+    import numpy as np
+    out = np.empty(n, np.uint16)
+    synth().heph_bench_gen_normal_bf16(seed, 0, n, mean, std, out.ctypes.data)
+    return out
+
+
+def host_normal_f32(seed, n, mean, std):
+    import numpy as np
+    out = np.empty(n, np.float32)
+    synth().heph_bench_gen_normal(seed, 0, n, mean, std, out.ctypes.data)
+    return out
+
+
+def bf16_to_device(bits, shape):
+    """uint16 bf16 bit patterns (host) -> bf16 tensor on cuda:0."""
+    import torch
+    return torch.from_numpy(bits.view("int16")).view(torch.bfloat16).reshape(shape).to("cuda")
 
 
 def achievable_read(sizes, timer_graph_calls=20):
@@ -166,8 +261,8 @@ def vendor_fp8_gemm(M=4096, calls=10):
     for i, (name, N, K) in enumerate(SHAPES):
         a = act(M, K, seed=M + 7).to(torch.float8_e4m3fn)
         copies = max(1, math.ceil(ROTATE_BYTES / (N * K)))
-        g = torch.Generator(device="cuda").manual_seed(300 + i)
-        w0 = (torch.randn(N, K, generator=g, device="cuda") * 0.5).to(torch.float8_e4m3fn)
+        w0 = torch.from_numpy(host_normal_f32(300 + i, N * K, 0.0, 0.5)).reshape(N, K)
+        w0 = w0.to("cuda").to(torch.float8_e4m3fn)
         ws = [w0] + [w0.clone() for _ in range(copies - 1)]
         it = [0]
 
@@ -244,7 +339,7 @@ def prefill_pass(steps):
     torch.cuda.set_device(0)
     M = 4096
     for i, (name, N, K) in enumerate(SHAPES):
-        lin = Linear(name, N, K, M, seed=100 + i)
+        lin = Linear(name, N, K, M, seed=WEIGHT_SEEDS[name])
         x = act(M, K, seed=M + 1, outliers=True)
         c = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
         HK.quantize_act_rows_fp8(lin.q_ws, lin.s_ws, x, M, K)
@@ -297,7 +392,7 @@ def pmc_pass(steps):
     import torch
     from hephaestus_amd import kernels as HK
     torch.cuda.set_device(0)
-    lins = [Linear(n, N, K, 32, seed=100 + i) for i, (n, N, K) in enumerate(SHAPES)]
+    lins = [Linear(n, N, K, 32, seed=WEIGHT_SEEDS[n]) for i, (n, N, K) in enumerate(SHAPES)]
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     for M in (1, 16, 32):
@@ -342,10 +437,15 @@ class Linear:
         from hephaestus_amd import kernels as HK
         from hephaestus_amd.weights import quantize_weight_fp8
         self.name, self.N, self.K = name, N, K
-        g = torch.Generator(device="cuda").manual_seed(seed)
-        w = (torch.randn(N, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+        wh = host_normal_bf16(seed, N * K, 0.0, 0.02)
+        w = bf16_to_device(wh, (N, K))
         q, s = quantize_weight_fp8(w)
         del w
+        if seed == WEIGHT_SEEDS.get(name):
+            check_digest(f"{name}_w_bf16", wh)
+            check_digest(f"{name}_w_e4m3", q.cpu().numpy())
+            check_digest(f"{name}_scale_inv", s.cpu().numpy())
+        del wh
         copies = max(1, math.ceil(ROTATE_BYTES / (N * K))) if rotate else 1
         self.w = [q] + [q.clone() for _ in range(copies - 1)]
         self.s = [s] + [s.clone() for _ in range(copies - 1)]
@@ -358,14 +458,16 @@ class Linear:
         return w, s
 
 
-def act(M, K, seed, outliers=False):
-    import torch
-    g = torch.Generator(device="cuda").manual_seed(seed)
-    x = torch.randn(M, K, generator=g, device="cuda")
-    if outliers:
-        u = torch.rand(M, K, generator=g, device="cuda")
-        x = torch.where(u < 1e-3, x * 50.0, x)
-    return x.to(torch.bfloat16)
+def act(M, K, seed, outliers=False, digest=None):
+    """M x K bf16 activations of `seed` on cuda:0 (outliers: ~0.1 % x 50);
+    checked against the committed digest `digest` when given."""
+    import numpy as np
+    xh = np.empty(M * K, np.uint16)
+    synth().heph_bench_gen_act_bf16(seed, M * K, 1e-3 if outliers else 0.0, 50.0,
+                                    xh.ctypes.data)
+    if digest:
+        check_digest(digest, xh)
+    return bf16_to_device(xh, (M, K))
 
 
 def time_calls(fn, n, timer):
@@ -425,8 +527,8 @@ def main():
 
     torch.cuda.set_device(0)
     props = torch.cuda.get_device_properties(0)
-    lins = [Linear(n, N, K, 32, seed=100 + i) for i, (n, N, K) in enumerate(SHAPES)]
-    xs = {K: act(1, K, seed=K) for K in {K for _, _, K in SHAPES}}
+    lins = [Linear(n, N, K, 32, seed=WEIGHT_SEEDS[n]) for i, (n, N, K) in enumerate(SHAPES)]
+    xs = {K: act(1, K, seed=K, digest=f"x_m1_k{K}") for K in {K for _, _, K in SHAPES}}
     outs = [torch.empty(1, N, dtype=torch.bfloat16, device="cuda") for _, N, _ in SHAPES]
 
     def step(timer=None):
@@ -538,7 +640,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp8_e4m3 x fp8_e4m3 -> f32 acc -> bf16",
-        "data": "synthetic (seeded GPU randn; weights quantized per 128x128 block)",
+        "data": "synthetic (seeded splitmix64 + Box-Muller host generator, "
+                "bench_csrc/synth.cpp; bf16 weights quantized per 128x128 block on "
+                "the GPU; digests checked)",
         "config": {"workload": "configs[1]: M=1 FP8 GEMV over Qwen3-4B linears "
                                "(qkv 6144x2560, o 2560x4096, gate_up 19456x2560, "
                                "down 2560x9728), fused 1x128 act quant, bf16 out",
@@ -552,6 +656,9 @@ def main():
                      "kernel": kernel_names[-1],
                      "bytes_per_step": step_bytes},
         "cpu_baseline": cpu,
+        "input_digests": {"checked": len(INPUT_CHECKS),
+                          "ok": bool(INPUT_CHECKS) and all(INPUT_CHECKS.values()),
+                          "mismatched": sorted(k for k, v in INPUT_CHECKS.items() if not v)},
         "detail": detail,
     }
     pk = detail.get("prefill_m4096_kernel")
@@ -585,8 +692,8 @@ def detail_sweeps(lins):
     timer = KernelTimer(64)
 
     # config 0: q_proj at M = 1
-    qp = Linear(*Q_PROJ, 1, seed=7)
-    x = act(1, qp.K, seed=8)
+    qp = Linear(*Q_PROJ, 1, seed=WEIGHT_SEEDS["q_proj"])
+    x = act(1, qp.K, seed=CONFIG0_SEED, digest="x_config0")
     c = torch.empty(1, qp.N, dtype=torch.bfloat16, device="cuda")
 
     def run_q():
@@ -600,9 +707,11 @@ def detail_sweeps(lins):
 
     # bf16 lm_head at M = 1 (f32 logits), two weight copies (> 1.5 GB)
     name, N, K = LM_HEAD
-    g = torch.Generator(device="cuda").manual_seed(9)
-    lw = [(torch.randn(N, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
-          for _ in range(2)]
+    wh = host_normal_bf16(WEIGHT_SEEDS["lm_head"], N * K, 0.0, 0.02)
+    check_digest("lm_head_w_bf16", wh)
+    lw = [bf16_to_device(wh, (N, K))]
+    lw.append(lw[0].clone())
+    del wh
     xl = act(1, K, seed=10)
     logits = torch.empty(1, N, dtype=torch.float32, device="cuda")
     it = [0]
@@ -756,7 +865,7 @@ def prefill_producer_path(lins, Ms=(512, 4096)):
                     HK.linear_fp8(cm, None, w, s, q_ws, s_ws, M, N, K, do_quantize=False)
             elif lin.name in ("qkv", "gate_up"):
                 src = act(M, K, seed=M + 3)
-                gam = (1.0 + 0.1 * torch.randn(K, device="cuda")).to(torch.bfloat16)
+                gam = bf16_to_device(host_normal_bf16(M + 6, K, 1.0, 0.1), (K,))
                 y = torch.empty(M, K, dtype=torch.bfloat16, device="cuda")
 
                 def unfused(lin=lin, src=src, gam=gam, y=y, cm=cm, q_ws=q_ws, s_ws=s_ws, M=M, K=K, N=N):
