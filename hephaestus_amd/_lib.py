@@ -45,7 +45,8 @@ class LaunchOverrides(ctypes.Structure):
     """heph_launch_overrides: per-call launch-shape overrides (0 = built-in)."""
     _fields_ = [("gemv_ks", ctypes.c_int), ("gemv_waves", ctypes.c_int),
                 ("gemv_u", ctypes.c_int), ("gemm_bm", ctypes.c_int),
-                ("batch_split", ctypes.c_int)]
+                ("batch_split", ctypes.c_int), ("wide_tiles", ctypes.c_int),
+                ("wide_waves", ctypes.c_int)]
 
 
 _vp = ctypes.c_void_p

@@ -131,6 +131,11 @@ int take_overrides(const heph_launch_overrides* ov, Tuning* t)
     if (bm != 0 && bm != 1 && bm != 64 && bm != 128 && bm != 192 && bm != 256)
         return HEPH_ERR_FLAGS;
     if (ov->batch_split < -1 || ov->batch_split > 64) return HEPH_ERR_FLAGS;
+    const int wt = ov->wide_tiles, ww = ov->wide_waves;
+    if (wt != -1 && wt != 0 && wt != 1 && wt != 2 && wt != 4) return HEPH_ERR_FLAGS;
+    if (ww != 0 && ww != 4 && ww != 8 && ww != 16) return HEPH_ERR_FLAGS;
+    t->wide_tiles = wt;
+    t->wide_waves = ww;
     t->gemv_ks = ks;
     t->gemv_waves = w;
     t->gemv_u = u;
@@ -204,20 +209,27 @@ int fp8_linear_impl(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
     }
 
     // M <= 32 takes the chunk-slot GEMV unless the GEMM is forced. Batched
-    // decode (gemv_split_routes: larger M, 1x128 groups) takes quantizer +
-    // the 64-column K-split kernel when the caller's scratch holds its
-    // partials; otherwise, at 16 <= M <= 32, quantizer + K-split GEMM on
-    // large weights when scratch allows (MI355X, gate_up graph-replayed over
-    // HBM-streamed weights: M = 16 17.9 us against 19.8 for the GEMV; M = 8
-    // 17.1 against 15.0). The RMSNorm entry point always takes the GEMV.
+    // decode from M = 8 (codes) or 9 (bf16 rows, quantized first) takes the
+    // wide-tile kernel (gemv_wide_routes), except past M = 24 on large
+    // weights: there the 64-column K-split kernel where gemv_split_routes
+    // holds and the caller's scratch holds its partials, else quantizer +
+    // K-split GEMM on weights of >= 32M elements when scratch allows. Forced
+    // K splits or chunk-slot shapes (overrides) keep the wide kernel out.
+    // The RMSNorm entry point always takes the GEMV.
     const bool forced_gemm = flags & HEPH_FLAG_FORCE_GEMM;
+    const int wmode = gamma ? -1 : tune.wide_tiles;
     const int bmode = gamma ? -1 : tune.batch_split;
-    const bool batch_split = !forced_gemm && M <= HEPH_SKINNY_MAX_M && group_k == kChunk &&
-                             bmode >= 0 && (bmode > 0 || gemv_split_routes(M, N, K)) &&
-                             gemv_split_ready(op);
-    const bool split_gemm = !gamma && !batch_split && M >= 16 && (long)N * K >= (32L << 20) &&
-                            gemm_splits_ready(op);
-    const bool gemv = !forced_gemm && M <= HEPH_SKINNY_MAX_M && !split_gemm && !batch_split;
+    const bool wide_auto = bmode <= 0 && !tune.gemv_ks && !tune.gemv_waves &&
+                           gemv_wide_routes(M, N, K, skip_quant);
+    const bool wide = !forced_gemm && M <= HEPH_SKINNY_MAX_M && wmode >= 0 &&
+                      (wmode > 0 || wide_auto);
+    const bool batch_split = !forced_gemm && !wide && M <= HEPH_SKINNY_MAX_M &&
+                             group_k == kChunk && bmode >= 0 &&
+                             (bmode > 0 || gemv_split_routes(M, N, K)) && gemv_split_ready(op);
+    const bool split_gemm = !gamma && !wide && !batch_split && M >= 16 &&
+                            (long)N * K >= (32L << 20) && gemm_splits_ready(op);
+    const bool gemv =
+        !forced_gemm && M <= HEPH_SKINNY_MAX_M && !split_gemm && !batch_split && !wide;
     if (gamma && !(gemv && M == 1 && group_k == kChunk)) return HEPH_ERR_UNSUPPORTED;
     const bool fuse_ok = !skip_quant && !(flags & HEPH_FLAG_NO_FUSE) && group_k == kChunk;
     const bool fused = fuse_ok && (batch_split || (gemv && gemv_fuses(M, N, K)));
@@ -232,7 +244,8 @@ int fp8_linear_impl(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
         t.start = nullptr;
     }
     hipError_t e;
-    if (batch_split) e = launch_fp8_gemv_split(op, fused, s, t, &g_last_kernel);
+    if (wide) e = launch_fp8_gemv_wide(op, s, t, &g_last_kernel);
+    else if (batch_split) e = launch_fp8_gemv_split(op, fused, s, t, &g_last_kernel);
     else if (gemv) e = launch_fp8_gemv(op, fused, s, t, &g_last_kernel, gamma, eps);
     else e = launch_fp8_gemm(op, s, t, &g_last_kernel);
     return launch_status(e);

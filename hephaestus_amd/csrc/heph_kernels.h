@@ -42,6 +42,8 @@ struct Tuning {
     int gemv_u = 0;
     int gemm_bm = 0;
     int batch_split = 0;
+    int wide_tiles = 0;
+    int wide_waves = 0;
 };
 
 // Activation scale addressing shared by the kernels: chunk j of row m uses
@@ -135,6 +137,16 @@ bool gemv_split_ready(const Fp8Operands& op);
 // Whether M x N x K takes it by default (op.tune.batch_split: -1 never,
 // n > 0 always).
 bool gemv_split_routes(int M, int N, int K);
+
+// Batched decode (M <= 32): workgroups of 16*T columns over all of K
+// (gemv_wide.hip), reading q/s from the workspace. Launch shape for
+// M x N x K with op.tune's overrides, and whether M x N x K takes it by
+// default with codes already in the workspace (codes) or bf16 rows to
+// quantize first (op.tune.wide_tiles: -1 never, > 0 always).
+hipError_t launch_fp8_gemv_wide(const Fp8Operands& op, hipStream_t stream,
+                                const LaunchTiming& t, const char** name);
+void gemv_wide_shape(int M, int N, int K, const Tuning& tune, int* tiles, int* waves, int* u);
+bool gemv_wide_routes(int M, int N, int K, bool codes);
 
 // bf16 x [M,K] @ w [N,K]^T, f32 accumulation, M <= 32.
 hipError_t launch_bf16_skinny(void* c, bool c_f32, bool residual, const uint16_t* x,

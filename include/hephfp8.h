@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define HEPH_ABI_VERSION 2
+#define HEPH_ABI_VERSION 3
 
 /* status codes */
 #define HEPH_OK                 0
@@ -250,6 +250,10 @@ const char* heph_last_kernel(void);
  *                reaches 2^31)
  *   batch_split  the 64-column K-split kernel for M <= 32 with 1x128 groups:
  *                -1 never, n in 1..64 always, with at least n K splits
+ *   wide_tiles   the wide-tile batched-decode kernel for M <= 32: -1 never,
+ *                1, 2 or 4 always, with 16 x that many output columns per
+ *                workgroup (halved until it divides N / 16)
+ *   wide_waves   its waves per workgroup: 4, 8 or 16 (16: one column tile)
  * Values outside these sets give HEPH_ERR_FLAGS.
  */
 typedef struct heph_launch_overrides {
@@ -258,6 +262,8 @@ typedef struct heph_launch_overrides {
     int gemv_u;
     int gemm_bm;
     int batch_split;
+    int wide_tiles;
+    int wide_waves;
 } heph_launch_overrides;
 
 int heph_fp8_linear_with(void* c, int c_dtype, const uint16_t* x_bf16,

@@ -45,9 +45,10 @@ def check_close(got_bf16: np.ndarray, ref_f32: np.ndarray, what: str):
 
 @pytest.fixture
 def gemv_only():
-    """Route M <= 32 to the chunk-slot GEMV (the 64-column K-split kernel
-    off) for tests that target the GEMV itself."""
+    """Route M <= 32 to the chunk-slot GEMV (the 64-column K-split and the
+    wide-tile kernels off) for tests that target the GEMV itself."""
     T.TUNE["batch_split"] = -1
+    T.TUNE["wide_tiles"] = -1
     yield
     T.TUNE.clear()
 
@@ -222,16 +223,20 @@ def test_exact_integer_bit_exact(M, N, K):
     ref = (ia.astype(np.float64) @ iw.astype(np.float64).T) * 0.0625 * 2.0 ** -5
     want = bf16_of(ref.astype(np.float32))
     codes = dev(qa.reshape(-1))
-    # the chunk-slot GEMV, the 64-column K-split kernel (with room for its
-    # partials) and the GEMM for M <= 32; the GEMM beyond
-    variants = [(0, {"batch_split": -1}, codes),
-                (0, {"batch_split": 1}, split_ws(codes, M, N, K, -(-(K // 128) // 8)))] \
+    # the chunk-slot GEMV, the wide-tile kernel at 1, 2 and 4 column tiles,
+    # the 64-column K-split kernel (with room for its partials) and the GEMM
+    # for M <= 32; the GEMM beyond
+    variants = [(0, {"batch_split": -1, "wide_tiles": -1}, codes)] + \
+        [(0, {"wide_tiles": t}, codes) for t in (1, 2, 4)] + \
+        [(0, {"batch_split": 1}, split_ws(codes, M, N, K, -(-(K // 128) // 8)))] \
         if M <= 32 else []
     for flags, tune, q in variants + [(L.FLAG_FORCE_GEMM, None, codes)]:
         c, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, flags=flags, skip_quant=True,
                              q_ws=q, s_ws=dev(sa), tune=tune)
-        if tune and tune["batch_split"] > 0:
+        if tune and tune.get("batch_split", 0) > 0:
             assert HK.last_kernel().startswith("fp8_gemv_split64"), HK.last_kernel()
+        if tune and tune.get("wide_tiles", 0) > 0:
+            assert HK.last_kernel() == "fp8_gemv_wide", HK.last_kernel()
         got = host_bf16(c)
         assert np.array_equal(got, want), (flags, tune, np.argwhere(got != want)[:5].tolist())
 
@@ -398,6 +403,66 @@ def test_gemv_rows_every_launch_shape(M, N, K):
             check_close(host_bf16(pc), ref_c, f"per-token {cfg}")
             pf, _, _ = run_linear(cq, cs, x, M=M, N=N, K=K)
             check_close(host_bf16(pf), ref_bc, f"per-channel {cfg}")
+    finally:
+        T.TUNE.clear()
+
+
+WIDE_SHAPES = [(t, w, u) for t in (1, 2, 4) for w in (4, 8, 16) for u in (1, 2)
+               if not (w == 16 and (t > 1 or u > 1))]
+
+
+@pytest.mark.parametrize("M", [1, 8, 9, 16, 17, 32])
+@pytest.mark.parametrize("N,K", [(16, 128), (64, 384), (2560, 1152), (192, 9728)])
+def test_wide_every_launch_shape(M, N, K):
+    # The wide-tile batched-decode kernel at every launch shape it takes
+    # (1, 2, 4 column tiles, halved to divide N/16; 4, 8, 16 waves; 1- and
+    # 2-chunk batches), with waves whose K run is empty (K/128 = 1 and 3
+    # chunks), ragged runs (9 and 76 chunks), one and two row tiles with
+    # rows past M masked: exact-integer inputs stay bit-exact; random block
+    # scales, per-token activations with per-channel weights and per-channel
+    # weights with 1x128 groups stay within tolerance of the oracle (the
+    # quantizer runs first, its codes equal the oracle's); the f32 output
+    # with a residual adds in f32.
+    ia, qa = lattice(M, K, 820 + M + K)
+    iw, qw = lattice(N, K, 920 + N)
+    sa = np.full(M * (K // 128), 2.0 ** -3, np.float32)
+    sw = np.full((-(-N // 128), K // 128), 2.0 ** -2, np.float32)
+    want = bf16_of(((ia.astype(np.float64) @ iw.astype(np.float64).T) * 2.0 ** -9)
+                   .astype(np.float32))
+    x = O.gen_act_bf16(730 + M + N + K, M, K)
+    rw = O.gen_normal(731 + N, N * K, 0.0, 0.02).reshape(N, K)
+    bq, bs = O.quant_weight(rw)
+    cq, cs = O.quant_weight(rw, 1, K)
+    ref_b = O.quant_linear(x, bq, bs)
+    ref_c = O.quant_linear(x, cq, cs, group_k=K, bn=1, bk=K)
+    ref_bc = O.quant_linear(x, cq, cs, group_k=128, bn=1, bk=K)
+    qo, so = O.quant_act(x, 128)
+    res = bf16_of(O.gen_normal(733 + M, M * N, 0.0, 1.0)).reshape(M, N)
+    try:
+        for cfg in WIDE_SHAPES:
+            t, waves, u = cfg
+            T.TUNE["wide_tiles"] = t
+            T.TUNE["wide_waves"] = waves
+            T.TUNE["gemv_u"] = u
+            c, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, skip_quant=True,
+                                 q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
+            assert HK.last_kernel() == "fp8_gemv_wide", HK.last_kernel()
+            got = host_bf16(c)
+            assert np.array_equal(got, want), (cfg, np.argwhere(got != want)[:5].tolist())
+            f, q_ws, s_ws = run_linear(bq, bs, x, M=M, N=N, K=K)
+            assert HK.last_kernel() == "fp8_gemv_wide", HK.last_kernel()
+            check_close(host_bf16(f), ref_b, f"block {cfg}")
+            assert np.array_equal(q_ws.cpu().numpy().reshape(M, K), qo), cfg
+            assert np.array_equal(s_ws.cpu().numpy().reshape(M, K // 128), so), cfg
+            pc, _, _ = run_linear(cq, cs, x, M=M, N=N, K=K, group_k=K)
+            check_close(host_bf16(pc), ref_c, f"per-token {cfg}")
+            pf, _, _ = run_linear(cq, cs, x, M=M, N=N, K=K)
+            check_close(host_bf16(pf), ref_bc, f"per-channel {cfg}")
+            r32 = torch.tensor(f32_of_bf16(res), device="cuda")
+            c, _, _ = run_linear(bq, bs, x, M=M, N=N, K=K, residual=r32)
+            assert HK.last_kernel() == "fp8_gemv_wide", HK.last_kernel()
+            assert max_abs_rel(c.cpu().numpy(), ref_b + f32_of_bf16(res).astype(np.float64)) \
+                <= TOL, cfg
     finally:
         T.TUNE.clear()
 
@@ -877,11 +942,13 @@ def test_large_m_split_k(M, N, K, out, resid):
 @pytest.mark.parametrize("M", [16, 17, 24, 32])
 @pytest.mark.parametrize("name", ["qkv", "gate_up", "down", "o_proj"])
 def test_batched_decode_split_gemm_route(M, name):
-    # With the 64-column split kernel switched off, 16 <= M <= 32 with a
-    # split-capable q_ws: weights of at least 32M elements (gate_up) take
-    # quantizer + K-split GEMM, the rest the GEMV; by default the split
-    # kernel where it routes (M >= 24 below 32M weights, K >= 8192); all
-    # within the tolerance, codes bit-exact.
+    # With the 64-column split and the wide-tile kernels switched off,
+    # 16 <= M <= 32 with a split-capable q_ws: weights of at least 32M
+    # elements (gate_up) take quantizer + K-split GEMM, the rest the GEMV.
+    # By default: the wide-tile kernel up to M = 24 and on small weights;
+    # past M = 24 the split kernel where it routes (K >= 8192), quantizer +
+    # K-split GEMM on weights of 32M elements. All within the tolerance,
+    # codes bit-exact.
     N, K = SHAPES[name]
     x = O.gen_act_bf16(120 + M, M, K)
     qw, sw = O.gen_weight(1000 + N + K, N, K)
@@ -890,6 +957,7 @@ def test_batched_decode_split_gemm_route(M, name):
     q_ws, s_ws = HK.workspace(M, K, n=N)
     try:
         T.TUNE["batch_split"] = -1
+        T.TUNE["wide_tiles"] = -1
         c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K, q_ws=q_ws, s_ws=s_ws)
         big = N * K >= 32 << 20
         assert HK.last_kernel().startswith("fp8_gemm") == big, HK.last_kernel()
@@ -898,8 +966,10 @@ def test_batched_decode_split_gemm_route(M, name):
     finally:
         T.TUNE.clear()
     c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K, q_ws=q_ws, s_ws=s_ws)
-    routed = (M >= 24 and N * K < 32 << 20) or K >= 8192
-    assert HK.last_kernel().startswith("fp8_gemv_split64") == routed, HK.last_kernel()
+    big = N * K >= 32 << 20
+    wide = M <= 24 or not (big or K >= 8192)
+    want = ("fp8_gemv_wide" if wide else "fp8_gemv_split64" if K >= 8192 else "fp8_gemm")
+    assert HK.last_kernel().startswith(want), (want, HK.last_kernel())
     check_close(host_bf16(c), ref, f"{name} M={M} default route")
     assert np.array_equal(q_ws[: M * K].cpu().numpy().reshape(M, K), qo)
 
@@ -919,6 +989,7 @@ def test_batch_split_kernel_config_shapes(M, name):
     outs = []
     try:
         T.TUNE["batch_split"] = 0 if routed else 1
+        T.TUNE["wide_tiles"] = -1
         if not routed:
             q_ws = torch.zeros(((M * K + 255) // 256) * 256 + 64 * M * N * 4, dtype=torch.uint8,
                                device="cuda")
@@ -1017,7 +1088,8 @@ def test_batch_split_flags_graph_replays_and_garbage_workspace():
         want = O.quant_linear(xh[K], *wh[n])
         run_one = torch.zeros(M, N, dtype=torch.bfloat16, device="cuda")
         ws2 = HK.workspace(M, K)
-        HK.linear_fp8(run_one, x[K], w, sw, ws2[0], ws2[1], M, N, K, tune={"batch_split": -1})
+        HK.linear_fp8(run_one, x[K], w, sw, ws2[0], ws2[1], M, N, K,
+                      tune={"batch_split": -1, "wide_tiles": -1})
         check_close(host_bf16(run_one), want, f"{n} gemv")
         ref[n] = want
     run()
