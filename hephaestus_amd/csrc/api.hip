@@ -297,17 +297,21 @@ int heph_bf16_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint16_
     if (flags & ~HEPH_FLAG_ADD_RESIDUAL) return HEPH_ERR_FLAGS;
     if (!c || !x_bf16 || !w_bf16) return HEPH_ERR_NULL;
     if (c_dtype != HEPH_DTYPE_BF16 && c_dtype != HEPH_DTYPE_F32) return HEPH_ERR_DTYPE;
-    if (M < 1 || M > HEPH_SKINNY_MAX_M || N < 16 || N % 16 || K < kChunk || K % kChunk)
+    if (M < 1 || N < 16 || N % 16 || K < kChunk || K % kChunk) return HEPH_ERR_SHAPE;
+    if ((long)N * K > (1L << 40) || (long)M * K > (1L << 40) || (long)M * N > (1L << 40))
         return HEPH_ERR_SHAPE;
-    if ((long)N * K > (1L << 40)) return HEPH_ERR_SHAPE;
     if (!aligned16(c) || !aligned16(x_bf16) || !aligned16(w_bf16)) return HEPH_ERR_ALIGN;
     int st = check_device();
     if (st != HEPH_OK) return st;
     const LaunchTiming t = take_timing();
-    return launch_status(launch_bf16_skinny(c, c_dtype == HEPH_DTYPE_F32,
-                                            flags & HEPH_FLAG_ADD_RESIDUAL, x_bf16, w_bf16,
-                                            M, N, K, static_cast<hipStream_t>(stream), t,
-                                            &g_last_kernel));
+    const bool f32 = c_dtype == HEPH_DTYPE_F32, res = flags & HEPH_FLAG_ADD_RESIDUAL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // up to 32 rows the weight stream bounds the call; beyond, the MFMA GEMM
+    if (M <= HEPH_SKINNY_MAX_M)
+        return launch_status(launch_bf16_skinny(c, f32, res, x_bf16, w_bf16, M, N, K, s, t,
+                                                &g_last_kernel));
+    return launch_status(launch_bf16_gemm(c, f32, res, x_bf16, w_bf16, M, N, K, s, t,
+                                          &g_last_kernel));
 }
 
 const char* heph_strerror(int status)

@@ -148,6 +148,20 @@ hipError_t launch_fp8_gemv_wide(const Fp8Operands& op, hipStream_t stream,
 void gemv_wide_shape(int M, int N, int K, const Tuning& tune, int* tiles, int* waves, int* u);
 bool gemv_wide_routes(int M, int N, int K, bool codes);
 
+// bf16 x [M,K] @ w [N,K]^T, f32 accumulation, M > 32 (bf16_gemm.hip):
+// 128x128 tiles; the residual is the output buffer's contents.
+struct Bf16GemmArgs {
+    void* c;
+    const uint16_t* x;
+    const uint16_t* w;
+    int M, N, K;
+    bool c_f32;
+    bool residual;
+};
+hipError_t launch_bf16_gemm(void* c, bool c_f32, bool residual, const uint16_t* x,
+                            const uint16_t* w, int M, int N, int K, hipStream_t stream,
+                            const LaunchTiming& t, const char** name);
+
 // bf16 x [M,K] @ w [N,K]^T, f32 accumulation, M <= 32.
 hipError_t launch_bf16_skinny(void* c, bool c_f32, bool residual, const uint16_t* x,
                               const uint16_t* w, int M, int N, int K,

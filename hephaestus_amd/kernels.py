@@ -213,7 +213,8 @@ def gemv_fp8(c, a, w, scale, a_fp8_ws, act_scale_ws, n, k, ctx=None, *,
 
 def linear(c, a, b, m, n, k, ctx=None, *, add_residual=False):
     """bf16 C = A @ B^T with f32 accumulation (the lm_head); c is f32
-    (logits, as the reference keeps them) or bf16. M <= 32."""
+    (logits, as the reference keeps them) or bf16. M <= 32 streams the
+    weights; larger M runs the MFMA GEMM."""
     if c.dtype not in _OUT:
         raise TypeError(f"linear: output dtype {c.dtype} not supported")
     if c.numel() < m * n or a.numel() < m * k or b.numel() < n * k:

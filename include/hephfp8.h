@@ -134,8 +134,11 @@ int heph_fp8_linear_rmsnorm(void* c, int c_dtype, const uint16_t* x_bf16,
 /*
  * Unquantized bf16 linear with f32 accumulation: c = x @ w^T.
  * Replaces `linear` for the lm_head (reference
- * src/hephaestus/kernels.mojo:89-121, which keeps F32 logits); accepts
- * M <= 32 (the decode and batched-decode rows). flags: ADD_RESIDUAL only.
+ * src/hephaestus/kernels.mojo:89-121, which keeps F32 logits): M <= 32
+ * streams the weights (the decode rows, as the reference's gemv path),
+ * M > 32 runs an MFMA GEMM (the reference's wmma_gemm_bf16 for M > 1,
+ * src/hephaestus/wmma_gfx12.mojo:428-473). N % 16 == 0, K % 128 == 0.
+ * flags: ADD_RESIDUAL only.
  */
 int heph_bf16_linear(void* c, int c_dtype, const uint16_t* x_bf16,
                      const uint16_t* w_bf16, int M, int N, int K, int flags,

@@ -108,7 +108,10 @@ def test_quant_rejects(lib):
 def test_bf16_rejects(lib):
     b = lib.heph_bf16_linear
     assert b(None, 1, FAKE, FAKE, 1, 151936, 2560, 0, None) == L.HEPH_ERR_NULL
-    assert b(FAKE, 1, FAKE, FAKE, 33, 151936, 2560, 0, None) == L.HEPH_ERR_SHAPE
+    assert b(FAKE, 1, FAKE, FAKE, 0, 151936, 2560, 0, None) == L.HEPH_ERR_SHAPE
+    assert b(FAKE, 1, FAKE, FAKE, 33, 151936, 2600, 0, None) == L.HEPH_ERR_SHAPE
+    # M > 32 is the MFMA GEMM: valid arguments reach the device check
+    assert b(FAKE, 1, FAKE, FAKE, 4096, 151936, 2560, 0, None) == L.HEPH_ERR_DEVICE
     assert b(FAKE, 1, FAKE, FAKE, 1, 151930, 2560, 0, None) == L.HEPH_ERR_SHAPE
     assert b(FAKE, 3, FAKE, FAKE, 1, 151936, 2560, 0, None) == L.HEPH_ERR_DTYPE
     assert b(FAKE, 1, FAKE, FAKE, 1, 151936, 2560, L.FLAG_SKIP_QUANT, None) == L.HEPH_ERR_FLAGS

@@ -624,6 +624,55 @@ def test_bf16_lm_head(M):
         assert g[i] == r[i] or abs(ref[i, g[i]] - ref[i, r[i]]) <= 1e-5 * np.abs(ref).max()
 
 
+@pytest.mark.parametrize("M", [33, 100, 257])
+@pytest.mark.parametrize("N,K", [(16, 128), (1040, 2560), (2576, 1024)])
+@pytest.mark.parametrize("out,resid", [("f32", False), ("bf16", False), ("f32", True),
+                                       ("bf16", True)])
+def test_bf16_gemm(M, N, K, out, resid):
+    # bf16 linear for M > 32 (the MFMA GEMM): ragged row and column tiles
+    # (M, N not multiples of 128), two chunks (K = 128); f32 logits within
+    # 1e-5 of the oracle, bf16 within its rounding; the residual is added
+    # in f32 before the one rounding.
+    x = O.gen_act_bf16(40 + M, M, K)
+    w = bf16_of(O.gen_normal(41 + N, N * K, 0.0, 0.02)).reshape(N, K)
+    ref = O.bf16_linear(x, w)
+    dt = torch.float32 if out == "f32" else torch.bfloat16
+    res = bf16_of(O.gen_normal(43 + M, M * N, 0.0, 1.0)).reshape(M, N)
+    c = (torch.tensor(f32_of_bf16(res), device="cuda").to(dt) if resid
+         else torch.zeros(M, N, dtype=dt, device="cuda"))
+    HK.linear(c, dev(x), dev(w), M, N, K, add_residual=resid)
+    torch.cuda.synchronize()
+    assert HK.last_kernel() == "bf16_gemm_128x128", HK.last_kernel()
+    want = ref + (f32_of_bf16(res).astype(np.float64) if resid else 0.0)
+    if out == "f32":
+        got = c.cpu().numpy()
+        assert max_abs_rel(got, want) < 1e-5, max_abs_rel(got, want)
+    else:
+        got = f32_of_bf16(host_bf16(c)).astype(np.float64)
+        bound = 2.0 ** -8 * np.abs(want) + 1e-5 * np.abs(want).max()
+        bad = np.flatnonzero(np.abs(got - want) > bound)
+        assert bad.size == 0, (bad.size, bad[:5])
+
+
+def test_bf16_gemm_lm_head_rows():
+    # The lm_head (151936 x 2560) over 64 positions: 8 sampled rows against
+    # the oracle (rows of C are independent), greedy argmax agreeing.
+    M, N, K = 64, 151936, 2560
+    x = O.gen_act_bf16(50, M, K)
+    w = bf16_of(O.gen_normal(21, N * K, 0.0, 0.02)).reshape(N, K)
+    c = torch.zeros(M, N, dtype=torch.float32, device="cuda")
+    HK.linear(c, dev(x), dev(w), M, N, K)
+    torch.cuda.synchronize()
+    assert HK.last_kernel() == "bf16_gemm_128x128"
+    rows = np.sort(np.random.default_rng(64).choice(M, 8, replace=False))
+    ref = O.bf16_linear(x[rows], w)
+    got = c.cpu().numpy()[rows]
+    assert max_abs_rel(got, ref) < 1e-5
+    g, r = got.argmax(axis=1), ref.argmax(axis=1)
+    for i in range(len(rows)):
+        assert g[i] == r[i] or abs(ref[i, g[i]] - ref[i, r[i]]) <= 1e-5 * np.abs(ref).max()
+
+
 # ------------------------------------------------------------ errors ----
 
 def test_errors_raise():
