@@ -39,9 +39,10 @@ int launch_status(hipError_t e) { return e == hipSuccess ? HEPH_OK : HEPH_ERR_LA
 int check_quant_args(const void* x, const void* q, const void* s, int M, int K, int group_k)
 {
     if (!x || !q || !s) return HEPH_ERR_NULL;
-    if (M < 1 || K < kChunk || K % kChunk) return HEPH_ERR_SHAPE;
+    if (M < 1 || K < 16 || K % 16) return HEPH_ERR_SHAPE;
     if ((long)M * K > (1L << 40)) return HEPH_ERR_SHAPE;
     if (group_k != kChunk && group_k != K) return HEPH_ERR_GROUP;
+    if (group_k == kChunk && K % kChunk) return HEPH_ERR_SHAPE;
     if (!aligned16(x) || !aligned16(q)) return HEPH_ERR_ALIGN;
     return HEPH_OK;
 }
@@ -166,7 +167,7 @@ int fp8_linear_impl(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
     if (!c || !w || !w_scale || !q_ws || !s_ws) return HEPH_ERR_NULL;
     if (!skip_quant && !x_bf16) return HEPH_ERR_NULL;
     if (c_dtype != HEPH_DTYPE_BF16 && c_dtype != HEPH_DTYPE_F32) return HEPH_ERR_DTYPE;
-    if (M < 1 || N < 16 || K < kChunk || N % 16 || K % kChunk) return HEPH_ERR_SHAPE;
+    if (M < 1 || N < 16 || K < 16 || N % 16 || K % 16) return HEPH_ERR_SHAPE;
     if ((long)M * K > (1L << 40) || (long)N * K > (1L << 40) || (long)M * N > (1L << 40))
         return HEPH_ERR_SHAPE;
     if (group_k != kChunk && group_k != K) return HEPH_ERR_GROUP;
@@ -174,6 +175,13 @@ int fp8_linear_impl(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
     if (w_block_n == kChunk && w_block_k == kChunk) w_block = true;
     else if (w_block_n == 1 && w_block_k == K) w_block = false;
     else return HEPH_ERR_GROUP;
+    // K not a multiple of 128: the reference's own granularity only
+    // (per-token activations, per-channel weights; its kernels need K % 16,
+    // wmma_gfx12.mojo:731-732), through the 128x128 GEMM with the last
+    // chunk's missing pieces read as zeros, any M (the reference loops a
+    // GEMV over the rows there, kernels.mojo:461-470)
+    const bool ragged = K % kChunk != 0;
+    if (ragged && (group_k != K || w_block)) return HEPH_ERR_SHAPE;
     if (q_ws_bytes < heph_fp8_q_ws_bytes(M, K) ||
         s_ws_floats < heph_fp8_s_ws_floats(M, K, group_k))
         return HEPH_ERR_WORKSPACE;
@@ -216,7 +224,8 @@ int fp8_linear_impl(void* c, int c_dtype, const uint16_t* x_bf16, const uint8_t*
     // K-split GEMM on weights of >= 32M elements when scratch allows. Forced
     // K splits or chunk-slot shapes (overrides) keep the wide kernel out.
     // The RMSNorm entry point always takes the GEMV.
-    const bool forced_gemm = flags & HEPH_FLAG_FORCE_GEMM;
+    const bool forced_gemm = (flags & HEPH_FLAG_FORCE_GEMM) || ragged;
+    if (ragged) op.tune.gemm_bm = 1;
     const int wmode = gamma ? -1 : tune.wide_tiles;
     const int bmode = gamma ? -1 : tune.batch_split;
     const bool wide_auto = bmode <= 0 && !tune.gemv_ks && !tune.gemv_waves &&
@@ -319,7 +328,9 @@ const char* heph_strerror(int status)
     switch (status) {
     case HEPH_OK: return "ok";
     case HEPH_ERR_NULL: return "a required pointer is NULL";
-    case HEPH_ERR_SHAPE: return "M, N or K out of range (need M>=1, N%16==0, K%128==0)";
+    case HEPH_ERR_SHAPE:
+        return "M, N or K out of range (need M>=1, N%16==0, K%16==0, and K%128==0 unless "
+               "group_k = K with per-channel weights)";
     case HEPH_ERR_ALIGN: return "pointer not 16-byte aligned";
     case HEPH_ERR_GROUP: return "unsupported activation group or weight block";
     case HEPH_ERR_DTYPE: return "unknown output dtype";

@@ -74,7 +74,9 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8Operands op)
     const int lane = tid & 63, wave = tid >> 6;
     const int r16 = lane & 15, slice = lane >> 4;
     const int wm = wave >> 1, wn = wave & 1;
-    const int M = op.M, N = op.N, K = op.K, KC = K >> 7;
+    // K % 128 != 0 (per-token / per-channel scales only): the last chunk's
+    // 16-byte pieces past K are zeros
+    const int M = op.M, N = op.N, K = op.K, KC = (K + kChunk - 1) >> 7;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     int tm, tn;
     tile_of_block(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
@@ -100,10 +102,11 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8Operands op)
     i32x4 ra[4], rb[4];
     float rs = 0.0f;
     auto gload = [&](int j) {
+        const bool kin = j * kChunk + lcol + 16 <= K;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            ra[r] = aok[r] ? ldg16(ag[r] + (size_t)j * kChunk) : i32x4{0, 0, 0, 0};
-            rb[r] = bok[r] ? ldg16(bg[r] + (size_t)j * kChunk) : i32x4{0, 0, 0, 0};
+            ra[r] = aok[r] && kin ? ldg16(ag[r] + (size_t)j * kChunk) : i32x4{0, 0, 0, 0};
+            rb[r] = bok[r] && kin ? ldg16(bg[r] + (size_t)j * kChunk) : i32x4{0, 0, 0, 0};
         }
         rs = sok ? sg[j * op.s_step] : 0.0f;
     };

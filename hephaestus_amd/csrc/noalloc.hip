@@ -80,8 +80,7 @@ int heph_fp8_linear_noalloc(void* c, int c_dtype, const uint16_t* x_bf16, const 
 {
     // the size checks come first so that an oversized call fails the same
     // way with or without a device
-    if (M < 1 || K < heph::kChunk || K % heph::kChunk || group_k < 1 || K % group_k)
-        return HEPH_ERR_SHAPE;
+    if (M < 1 || K < 16 || K % 16 || group_k < 1 || K % group_k) return HEPH_ERR_SHAPE;
     const size_t q_bytes = round256((size_t)M * (size_t)K);
     const size_t s_floats = (size_t)M * (size_t)(K / group_k);
     const size_t s_bytes = round256(s_floats * sizeof(float));

@@ -70,8 +70,8 @@ extern "C" {
  * Dynamic activation quantization, bf16 [M,K] -> E4M3 codes + f32 scales.
  * Replaces quantize_act_rows_fp8 / quantize_act_fp8_pad
  * (reference src/hephaestus/kernels.mojo:196-211, :270-287); group_k == K is
- * the reference's per-token quantizer, group_k == 128 the 1x128 groups.
- * scales has M * (K / group_k) floats.
+ * the reference's per-token quantizer (K % 16 == 0), group_k == 128 the
+ * 1x128 groups (K % 128 == 0). scales has M * (K / group_k) floats.
  */
 int heph_fp8_quant_act(const uint16_t* x_bf16, uint8_t* q, float* scales,
                        int M, int K, int group_k, void* stream);
@@ -97,7 +97,10 @@ int heph_fp8_quant_weight(const uint16_t* w_bf16, uint8_t* q, float* scale_inv,
  *   w, w_scale           `w`, `scale` (block given by w_block_n/w_block_k:
  *                        (128,128) or (1,K))
  *   q_ws, s_ws           `a_fp8_ws`, `act_scale_ws`; sizes in bytes / floats
- *   M, N, K              `m`, `n`, `k`
+ *   M, N, K              `m`, `n`, `k`: N % 16 == 0, K % 16 == 0; K % 128
+ *                        == 0 except with the reference's own granularity
+ *                        (group_k = K, w block (1,K)), which takes the
+ *                        128x128 GEMM for any M with the K tail zeroed
  *   group_k              activation group: 128 or K
  *   flags                HEPH_FLAG_SKIP_QUANT is the reference's
  *                        do_quantize=False

@@ -62,6 +62,9 @@ def lin(lib, **kw):
     (dict(N=264), L.HEPH_ERR_SHAPE),
     (dict(K=2500), L.HEPH_ERR_SHAPE),
     (dict(K=64, g=64), L.HEPH_ERR_SHAPE),
+    (dict(K=2624), L.HEPH_ERR_SHAPE),                  # K % 128 with 1x128 groups
+    (dict(K=2624, g=2624), L.HEPH_ERR_SHAPE),          # ... or block weights
+    (dict(K=2616, g=2616, bn=1, bk=2616, sn=1), L.HEPH_ERR_SHAPE),   # K % 16
     (dict(g=64), L.HEPH_ERR_GROUP),
     (dict(g=256), L.HEPH_ERR_GROUP),
     (dict(bn=64, bk=64), L.HEPH_ERR_GROUP),
@@ -94,6 +97,12 @@ def test_valid_call_without_gpu_reports_device(lib):
         pytest.skip("a GPU is present")
     assert lin(lib) == L.HEPH_ERR_DEVICE
     assert lin(lib, bn=1, bk=2560, g=2560, sn=1) == L.HEPH_ERR_DEVICE
+    # K % 128 != 0 at the reference's own granularity (per-token, per-channel)
+    assert lin(lib, K=2624, bn=1, bk=2624, g=2624, sn=1) == L.HEPH_ERR_DEVICE
+    assert lin(lib, K=16, bn=1, bk=16, g=16, sn=40, M=40) == L.HEPH_ERR_DEVICE
+    q = lib.heph_fp8_quant_act
+    assert q(FAKE, FAKE, FAKE, 3, 2624, 2624, None) == L.HEPH_ERR_DEVICE
+    assert q(FAKE, FAKE, FAKE, 3, 2624, 128, None) == L.HEPH_ERR_SHAPE
 
 
 def test_quant_rejects(lib):

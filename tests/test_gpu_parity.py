@@ -467,6 +467,41 @@ def test_wide_every_launch_shape(M, N, K):
         T.TUNE.clear()
 
 
+@pytest.mark.parametrize("M", [1, 5, 40, 300])
+@pytest.mark.parametrize("N,K", [(64, 16), (48, 2624), (2560, 2576), (160, 9744)])
+def test_ragged_k_reference_granularity(M, N, K):
+    # K % 128 != 0 (K % 16 == 0, the reference's decode-kernel bound,
+    # wmma_gfx12.mojo:731-732) with the reference's own scales (per-token
+    # activations, per-channel weights): the 128x128 GEMM with the last
+    # chunk's missing pieces zeroed, for every M. Exact-integer inputs stay
+    # bit-exact; random inputs stay within tolerance of the oracle with the
+    # per-token codes and scales bit-exact; f32 output with a residual.
+    ia, qa = lattice(M, K, 1100 + M + K)
+    iw, qw = lattice(N, K, 1200 + N)
+    sa = np.full(M, 2.0 ** -3, np.float32)
+    sw = np.full((N, 1), 2.0 ** -2, np.float32)
+    want = bf16_of(((ia.astype(np.float64) @ iw.astype(np.float64).T) * 2.0 ** -9)
+                   .astype(np.float32))
+    c, _, _ = run_linear(qw, sw, None, M=M, N=N, K=K, group_k=K, skip_quant=True,
+                         q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
+    assert HK.last_kernel() == "fp8_gemm_128x128", HK.last_kernel()
+    got = host_bf16(c)
+    assert np.array_equal(got, want), np.argwhere(got != want)[:5].tolist()
+    x = O.gen_act_bf16(1300 + M + K, M, K)
+    rw = O.gen_normal(1301 + N, N * K, 0.0, 0.02).reshape(N, K)
+    cq, cs = O.quant_weight(rw, 1, K)
+    ref = O.quant_linear(x, cq, cs, group_k=K, bn=1, bk=K)
+    c, q_ws, s_ws = run_linear(cq, cs, x, M=M, N=N, K=K, group_k=K)
+    check_close(host_bf16(c), ref, f"ragged K={K} M={M}")
+    qo, so = O.quant_act(x, K)
+    assert np.array_equal(q_ws.cpu().numpy().reshape(M, K), qo)
+    assert np.array_equal(s_ws.cpu().numpy().reshape(M, 1), so)
+    res = bf16_of(O.gen_normal(1302 + M, M * N, 0.0, 1.0)).reshape(M, N)
+    r32 = torch.tensor(f32_of_bf16(res), device="cuda")
+    c, _, _ = run_linear(cq, cs, x, M=M, N=N, K=K, group_k=K, residual=r32)
+    assert max_abs_rel(c.cpu().numpy(), ref + f32_of_bf16(res).astype(np.float64)) <= TOL
+
+
 # ----------------------------------------------------- random parity ----
 
 @pytest.mark.parametrize("name", sorted(SHAPES))
