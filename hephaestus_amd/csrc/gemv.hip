@@ -36,8 +36,8 @@
 //     reference's own granularity) accumulate unscaled and apply the
 //     reference association at the end: acc*(sa*sw) at M = 1
 //     (wmma_gfx12.mojo:711-712), (acc*sa)*sw otherwise (:973, :848);
-//   * the last wave of a workgroup to finish sums the waves' slot partials
-//     in a fixed order (deterministic) and stores bf16 or f32, optionally
+//   * after one workgroup barrier wave 0 sums the waves' slot partials in
+//     a fixed order (deterministic) and stores bf16 or f32, optionally
 //     adding the residual first (wmma_gfx12.mojo:712-715).
 #include <type_traits>
 
@@ -182,13 +182,11 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
     const int ta = r16 / MR, ma = r16 % MR;
 
     __shared__ float red[WAVES][MT * NE][64];
-    __shared__ int arrive;
     __shared__ __attribute__((aligned(16))) uint8_t qlds[FUSED ? WAVES : 1][FUSED ? U : 1]
                                                         [FUSED ? MT : 1][R * kChunk];
     // NORM: the row and gamma (bf16)
     __shared__ __attribute__((aligned(16))) uint16_t nrow[NORM ? kNormMaxK : 1];
     __shared__ __attribute__((aligned(16))) uint16_t ngam[NORM ? kNormMaxK : 1];
-    if (threadIdx.x == 0) arrive = 0;
 
     const int n = n0 + r16 % TW;
     const uint8_t* wrow = op.w + (size_t)n * K + g * 16;
@@ -401,8 +399,7 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
     // next U steps. With NORM both go out before the norm's prologue (its
     // loads and barriers would otherwise leave one batch's latency exposed:
     // MI355X, fused-norm o_proj 9.45 -> 8.25 us, gate_up 16.3 -> 14.5);
-    // without, the second goes out after the start barrier (issued before
-    // it, the plain gate_up GEMV ran 11.6 -> 12.4 us).
+    // without, one after the other.
     Batch b0, b1;
     // RMSNorm (NORM): the row and gamma are loaded in 16-byte pieces spread
     // over all threads before the weight batches (a wave's loads return in
@@ -436,7 +433,6 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
         }
         __syncthreads();
         // the sum of squares and the fold of the 256 sums, as fold256_wave0
-        // (its barrier also publishes arrive = 0)
         __shared__ float nred[256];
         float ss = 0.0f;
         if (threadIdx.x < 256) {
@@ -447,10 +443,9 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
         }
         rn = rms_inv(fold256_every_wave(ss, nred), K, args.eps);
     } else {
-        // arrive = 0 is seen by every wave before any wave's increment; the
-        // barrier waits here, with the first loads in flight, rather than
-        // before them
-        __syncthreads();
+        // no barrier before the loop: the waves start their batches as they
+        // are dispatched (a workgroup barrier here, with the first batch in
+        // flight, cost 1-2 % on every config shape on MI355X)
         if (sb + U < se) issue(b1, sb + U);
     }
     for (int s = sb; s < se; s += 2 * U) {
@@ -461,17 +456,13 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
         if (s + 3 * U < se) issue(b1, s + 3 * U);
     }
 
-    // ---- the last wave to arrive sums the partials in a fixed order ----
+    // ---- wave 0 sums the partials in a fixed order after one barrier ----
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int i = 0; i < NE; ++i) red[wave][mt * NE + i][lane] = acc[mt][i];
-    int old = 0;
-    if (lane == 0)
-        old = __hip_atomic_fetch_add(&arrive, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
-    old = __builtin_amdgcn_readfirstlane(old);
-    if (old != WAVES - 1) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    __syncthreads();
+    if (wave != 0) return;
 
     // output (token mt*16 + m, column n0 + c2) = sum over waves w and slots
     // ts of C row ts*MR + m, column ts*TW + c2
