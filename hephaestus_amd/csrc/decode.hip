@@ -510,9 +510,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(uint16_t* out, const uint
 {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
-    const float g = f32_of_bf16(gate[i]);
-    const float s = round_bf16(__fdiv_rn(g, 1.0f + expf(-g)));
-    out[i] = f32_to_bf16(s * f32_of_bf16(up[i]));
+    out[i] = (uint16_t)swiglu_bits(gate[i], up[i]);
 }
 
 // argmax over bf16-rounded logits, lowest index on ties, in two kernels:

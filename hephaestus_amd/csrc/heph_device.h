@@ -60,6 +60,15 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f)
     return (uint16_t)(u >> 16);
 }
 
+// SwiGLU of one element from bf16 bits g and u (low 16 bits), as the decode
+// step's silu_mul rounds it: bf16(bf16(g / (1 + exp(-g))) * u).
+__device__ __forceinline__ uint32_t swiglu_bits(uint32_t g16, uint32_t u16)
+{
+    const float g = __uint_as_float(g16 << 16);
+    const float s = __uint_as_float((uint32_t)f32_to_bf16(__fdiv_rn(g, 1.0f + expf(-g))) << 16);
+    return f32_to_bf16(s * __uint_as_float(u16 << 16));
+}
+
 // Four floats -> four E4M3FN codes (byte i = code of value i) with the
 // hardware converter (round to nearest even).
 __device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d)

@@ -122,15 +122,6 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(uint8_t* q, float* s
                        scales + (size_t)blockIdx.x * (cols / group_k));
 }
 
-// SwiGLU value of one element as heph_silu_mul computes it:
-// bf16(bf16(g / (1 + exp(-g))) * up).
-__device__ __forceinline__ uint32_t swiglu_bits(uint16_t g16, uint16_t u16)
-{
-    const float g = f32b(g16);
-    const float s = rbf16(__fdiv_rn(g, 1.0f + expf(-g)));
-    return f32_to_bf16(s * f32b(u16));
-}
-
 __device__ __forceinline__ uint4 swiglu8(const uint4& g, const uint4& u)
 {
     const uint32_t gd[4] = {g.x, g.y, g.z, g.w}, ud[4] = {u.x, u.y, u.z, u.w};
