@@ -494,6 +494,10 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     // 512 qkv 16.4 us from the cache, 29.5 us from HBM with two stages).
     constexpr int NS = T::NS, NB = T::NB;
     constexpr bool SPLIT_B = T::SPLIT_B;
+    // The kernel's only LDS variable: with a second one the LDS accesses get
+    // alias scopes, the compiler then orders every fragment read after all
+    // outstanding DMA (vmcnt(0)), and the pipeline serializes (MI355X: +40 %
+    // per chunk). Extra LDS state goes into this array.
     __shared__ __attribute__((aligned(16))) uint8_t smem[T::BYTES];
 
     const int tid = threadIdx.x;
