@@ -393,18 +393,25 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(float* ws, const uint8_t* 
     // global max and sum per head from the split statistics, computed by
     // every wave on its own (no barrier): lane l takes splits l, l + 64, ...
     // (sum: fma in that order), the max over all lanes, the sum folded as
-    // v[l] += v[l + h], h = 32 .. 1
+    // v[l] += v[l + h], h = 32 .. 1. Up to 64 splits (8192 keys) a lane
+    // holds one split: its max and sum are read together, one round trip
     float mloc[G], inv[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         const size_t base = (size_t)(kh * G + g) * n_splits;
         const int l = t & 63;
-        float m = -3.4e38f;
-        for (int s = l; s < n_splits; s += 64) m = fmaxf(m, w.smax[base + s]);
-        m = wave_max64(m);
-        float a = 0.0f;
-        for (int s = l; s < n_splits; s += 64)
-            a = __builtin_fmaf(w.ssum[base + s], expf(w.smax[base + s] - m), a);
+        float m = -3.4e38f, a = 0.0f;
+        if (n_splits <= 64) {
+            const float ms = l < n_splits ? w.smax[base + l] : -3.4e38f;
+            const float ls = l < n_splits ? w.ssum[base + l] : 0.0f;
+            m = wave_max64(ms);
+            if (l < n_splits) a = __builtin_fmaf(ls, expf(ms - m), 0.0f);
+        } else {
+            for (int s = l; s < n_splits; s += 64) m = fmaxf(m, w.smax[base + s]);
+            m = wave_max64(m);
+            for (int s = l; s < n_splits; s += 64)
+                a = __builtin_fmaf(w.ssum[base + s], expf(w.smax[base + s] - m), a);
+        }
         mloc[g] = m;
         inv[g] = __fdiv_rn(1.0f, wave_sum64(a));
     }
