@@ -66,6 +66,8 @@ SIGNATURES = {
     "heph_noalloc_scratch_bytes": (_sz, []),
     "heph_fp8_linear_rmsnorm": (_i, [_vp, _i, _vp, _vp, ctypes.c_float, _vp, _vp, _i, _i, _vp,
                                      _sz, _vp, _sz, _i, _i, _i, _vp]),
+    "heph_fp8_linear_swiglu": (_i, [_vp, _vp, _vp, ctypes.c_float, _vp, _vp, _i, _i, _vp, _sz,
+                                    _vp, _sz, _i, _i, _vp]),
     "heph_bf16_linear": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _i, _vp]),
     "heph_fp8_q_ws_bytes": (_sz, [_i, _i]),
     "heph_fp8_s_ws_floats": (_sz, [_i, _i, _i]),

@@ -300,6 +300,46 @@ int heph_fp8_linear_rmsnorm(void* c, int c_dtype, const uint16_t* x_bf16,
                            gamma_bf16, eps, nullptr);
 }
 
+int heph_fp8_linear_swiglu(void* act_bf16, const uint16_t* x_bf16, const uint16_t* gamma_bf16,
+                           float eps, const uint8_t* w, const float* w_scale, int w_block_n,
+                           int w_block_k, uint8_t* q_ws, size_t q_ws_bytes, float* s_ws,
+                           size_t s_ws_floats, int N, int K, void* stream)
+{
+    if (!act_bf16 || !x_bf16 || !w || !w_scale || !q_ws || !s_ws) return HEPH_ERR_NULL;
+    if (N < 16 || N % 16 || K < kChunk || K % kChunk) return HEPH_ERR_SHAPE;
+    if ((long)N * K > (1L << 40)) return HEPH_ERR_SHAPE;
+    bool w_block;
+    if (w_block_n == kChunk && w_block_k == kChunk) w_block = true;
+    else if (w_block_n == 1 && w_block_k == K) w_block = false;
+    else return HEPH_ERR_GROUP;
+    if (gamma_bf16 && K > kNormMaxK) return HEPH_ERR_UNSUPPORTED;
+    if (q_ws_bytes < heph_fp8_q_ws_bytes(1, K) ||
+        s_ws_floats < heph_fp8_s_ws_floats(1, K, kChunk))
+        return HEPH_ERR_WORKSPACE;
+    if (!aligned16(act_bf16) || !aligned16(w) || !aligned16(q_ws) || !aligned16(x_bf16) ||
+        (gamma_bf16 && !aligned16(gamma_bf16)))
+        return HEPH_ERR_ALIGN;
+    int st = check_device();
+    if (st != HEPH_OK) return st;
+    Fp8Operands op{};
+    op.w = w;
+    op.sw = w_scale;
+    op.sw_ld = w_block ? K / kChunk : 1;
+    op.w_block = w_block;
+    op.x = x_bf16;
+    op.q = q_ws;
+    op.s = s_ws;
+    op.s_ld = K / kChunk;
+    op.s_step = 1;
+    op.c = act_bf16;
+    op.M = 1;
+    op.N = N;
+    op.K = K;
+    const hipError_t e = launch_fp8_gemv_swiglu(op, static_cast<hipStream_t>(stream),
+                                                take_timing(), &g_last_kernel, gamma_bf16, eps);
+    return launch_status(e);
+}
+
 int heph_bf16_linear(void* c, int c_dtype, const uint16_t* x_bf16, const uint16_t* w_bf16,
                      int M, int N, int K, int flags, void* stream)
 {

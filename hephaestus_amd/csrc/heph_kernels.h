@@ -90,6 +90,14 @@ hipError_t launch_wquant(const uint16_t* w, uint8_t* q, float* scale_inv, int N,
 // heph_rmsnorm_bf16 rounds it.
 // Longest row the GEMV's RMSNorm prologue holds in LDS (with gamma: 32 KB).
 constexpr int kNormMaxK = 8192;
+// M = 1, fused quantization (gamma: RMSNorm first), SwiGLU epilogue: the
+// weight's rows [0, N/2) are the gate, [N/2, N) the up projection, and
+// op.c receives act[N/2] = bf16(bf16(silu(g)) * up) from the bf16-rounded
+// gate and up values, in the plain M = 1 GEMV's launch shape for N x K
+// (bit for bit the GEMV then silu_mul). N % 16 == 0.
+hipError_t launch_fp8_gemv_swiglu(const Fp8Operands& op, hipStream_t stream,
+                                  const LaunchTiming& t, const char** name,
+                                  const uint16_t* gamma, float eps);
 hipError_t launch_fp8_gemv(const Fp8Operands& op, bool fused, hipStream_t stream,
                            const LaunchTiming& t, const char** name,
                            const uint16_t* gamma = nullptr, float eps = 0.0f);

@@ -252,13 +252,24 @@ class Qwen3Decoder:
             rec(li, "attention", self.att)
             self._linear(self.x, self.att, lw.o, Q, residual=True)
             rec(li, "o_residual", self.x)
-            self._norm_linear(self.gu, lw.ffn_norm, lw.gate_up, H, eps, rec, li, "ffn_norm")
-            rec(li, "gate_up", self.gu)
-            # SwiGLU, then down with its quantization fused in the GEMV: for one
-            # row ~1.2 us per layer faster on MI355X than the producer-side
-            # form (heph_silu_mul_quant_fp8), which pays at prefill sizes
-            silu_mul(self.act, self.gu, self.gu[:, I:], I)
-            rec(li, "silu_mul", self.act)
+            if rec.tracing:
+                # the ops one by one, so that the trace holds gate_up's output
+                self._norm_linear(self.gu, lw.ffn_norm, lw.gate_up, H, eps, rec, li, "ffn_norm")
+                rec(li, "gate_up", self.gu)
+                silu_mul(self.act, self.gu, self.gu[:, I:], I)
+                rec(li, "silu_mul", self.act)
+            elif H <= NORM_LINEAR_MAX_K:
+                # RMSNorm, gate/up and SwiGLU in one launch, bit for bit the
+                # three ops
+                HK.linear_fp8_swiglu(self.act, self.x, lw.ffn_norm, eps, lw.gate_up.w,
+                                     lw.gate_up.scale, self.q_ws, self.s_ws, lw.gate_up.N, H)
+            else:
+                rmsnorm(self.xn, self.x, lw.ffn_norm, eps)
+                HK.linear_fp8_swiglu(self.act, self.xn, None, eps, lw.gate_up.w,
+                                     lw.gate_up.scale, self.q_ws, self.s_ws, lw.gate_up.N, H)
+            # down with its quantization fused in the GEMV: for one row ~1.2 us
+            # per layer faster on MI355X than the producer-side form
+            # (heph_silu_mul_quant_fp8), which pays at prefill sizes
             self._linear(self.x, self.act, lw.down, I, residual=True)
             rec(li, "down_residual", self.x)
         self._norm_linear(self.logits, w.final_norm, w.embed, H, eps, rec, -1, "final_norm")

@@ -184,6 +184,27 @@ def linear_fp8_rmsnorm(c, x, gamma, eps, w, scale, a_fp8_ws, act_scale_ws, n, k,
     _check(s, "linear_fp8_rmsnorm")
 
 
+def linear_fp8_swiglu(act, x, gamma, eps, w, scale, a_fp8_ws, act_scale_ws, n, k, ctx=None):
+    """act = silu(g) * u for one row (M = 1), with g and u the gate and up
+    halves of x @ dequant(w)^T (w: gate rows, then up rows; n = 2 *
+    intermediate) and x first RMS-normalized with gamma unless gamma is
+    None; bit for bit the gate/up linear then silu_mul (bf16 act, n / 2)."""
+    bn, bk = _weight_block(scale, n, k)
+    if act.dtype != torch.bfloat16:
+        raise TypeError(f"linear_fp8_swiglu: output dtype {act.dtype} not supported")
+    if act.numel() < n // 2 or w.numel() < n * k or x.numel() < k or \
+            (gamma is not None and gamma.numel() < k):
+        raise HephError(L.HEPH_ERR_SHAPE, "linear_fp8_swiglu")
+    g = _dev(gamma, "gamma", (torch.bfloat16,)) if gamma is not None else None
+    s = L.lib().heph_fp8_linear_swiglu(
+        _dev(act, "act", (torch.bfloat16,)), _dev(x, "x", (torch.bfloat16,)), g, float(eps),
+        _dev(w, "w", _FP8), _dev(scale, "scale", (torch.float32,)), bn, bk,
+        _dev(a_fp8_ws, "a_fp8_ws", _FP8), a_fp8_ws.numel(),
+        _dev(act_scale_ws, "act_scale_ws", (torch.float32,)), act_scale_ws.numel(),
+        n, k, _stream(ctx))
+    _check(s, "linear_fp8_swiglu")
+
+
 def linear_fp8(c, a, w, scale, a_fp8_ws, act_scale_ws, m, n, k, ctx=None, *,
                do_quantize=True, group_k=None, flags=0, tune=None):
     """C = A @ W^T through the W8A8 FP8 path (quantize A, FP8 contraction,

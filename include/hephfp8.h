@@ -135,6 +135,27 @@ int heph_fp8_linear_rmsnorm(void* c, int c_dtype, const uint16_t* x_bf16,
                             size_t s_ws_floats, int N, int K, int flags, void* stream);
 
 /*
+ * Decode-step feed-forward input (M = 1, group 128): act = silu(g) * u
+ * with g = xn @ dequant(w[0:N/2])^T and u = xn @ dequant(w[N/2:N])^T, xn =
+ * rmsnorm(x, gamma, eps) when gamma is given (as heph_fp8_linear_rmsnorm
+ * computes it; K <= 8192, else HEPH_ERR_UNSUPPORTED) or x itself when gamma
+ * is NULL. w holds the gate rows then the up rows ([N, K], N % 16 == 0),
+ * w_scale their 128x128 blocks (w_block_n = w_block_k = 128) or per-row
+ * scales [N, 1] (1, K). act: bf16 [N/2], bf16(bf16(g / (1 + exp(-g))) * u)
+ * of the bf16-rounded g and u: bit for bit the gate/up linear (bf16 output)
+ * followed by heph_silu_mul, in one launch whose workgroups each finish 8
+ * gate and 8 up columns. Replaces rms_norm + linear_fp8(gate_proj) +
+ * linear_fp8(up_proj) + silu_mul of the reference's decode step
+ * (src/hephaestus/forward.mojo:537-578; silu_mul, kernels.mojo:1243-1278).
+ * The workspaces receive xn's codes and scales, as for the other M = 1
+ * entry points.
+ */
+int heph_fp8_linear_swiglu(void* act_bf16, const uint16_t* x_bf16, const uint16_t* gamma_bf16,
+                           float eps, const uint8_t* w, const float* w_scale, int w_block_n,
+                           int w_block_k, uint8_t* q_ws, size_t q_ws_bytes, float* s_ws,
+                           size_t s_ws_floats, int N, int K, void* stream);
+
+/*
  * Unquantized bf16 linear with f32 accumulation: c = x @ w^T.
  * Replaces `linear` for the lm_head (reference
  * src/hephaestus/kernels.mojo:89-121, which keeps F32 logits): M <= 32

@@ -249,3 +249,28 @@ def test_producer_quant_rejects(lib):
     assert sq(FAKE, FAKE, FAKE, FAKE, 1, 9728, 19456, 64, None) == L.HEPH_ERR_GROUP
     assert sq(FAKE, FAKE, FAKE, FAKE, 1, 32768, 32768, 32768, None) == L.HEPH_ERR_UNSUPPORTED
     assert sq(FAKE, FAKE, ODD, FAKE, 1, 9728, 19456, 128, None) == L.HEPH_ERR_ALIGN
+
+
+def test_swiglu_linear_rejects(lib):
+    # heph_fp8_linear_swiglu: M = 1, N % 16, K % 128, the fused norm's 8192
+    # limit, weight granularity and workspace sizes, before any device work
+    sg = lib.heph_fp8_linear_swiglu
+    ok = dict(N=19456, K=2560)
+
+    def call(act=FAKE, x=FAKE, gamma=FAKE, N=19456, K=2560, bn=128, bk=128, qb=1 << 20,
+             sf=1 << 20):
+        return sg(act, x, gamma, 1e-6, FAKE, FAKE, bn, bk, FAKE, qb, FAKE, sf, N, K, None)
+
+    assert call(**ok) in (L.HEPH_ERR_DEVICE, L.HEPH_OK)
+    assert call(gamma=None) in (L.HEPH_ERR_DEVICE, L.HEPH_OK)
+    assert call(act=None) == L.HEPH_ERR_NULL
+    assert call(x=None) == L.HEPH_ERR_NULL
+    assert call(N=19448) == L.HEPH_ERR_SHAPE
+    assert call(K=2500) == L.HEPH_ERR_SHAPE
+    assert call(K=9728) == L.HEPH_ERR_UNSUPPORTED          # fused norm: K <= 8192
+    assert call(K=9728, gamma=None) in (L.HEPH_ERR_DEVICE, L.HEPH_OK)
+    assert call(bn=64, bk=128) == L.HEPH_ERR_GROUP
+    assert call(bn=1, bk=2560) in (L.HEPH_ERR_DEVICE, L.HEPH_OK)
+    assert call(qb=100) == L.HEPH_ERR_WORKSPACE
+    assert call(sf=10) == L.HEPH_ERR_WORKSPACE
+    assert call(act=ODD) == L.HEPH_ERR_ALIGN

@@ -398,6 +398,62 @@ def test_decode_wide_hidden_takes_separate_norm():
     op_by_op(wide, ctx=40, token=77, seed=21)
 
 
+@pytest.mark.parametrize("cfg", [SMALL, Qwen3Config(vocab=512, hidden=8320, n_layers=1, n_heads=2,
+                                                    n_kv_heads=1, head_dim=128, inter=256)],
+                         ids=["small", "wide_hidden"])
+def test_decode_step_fused_ffn_matches_traced_ops(cfg):
+    # An untraced step runs RMSNorm + gate/up + SwiGLU as one launch
+    # (heph_fp8_linear_swiglu; past 8192 hidden, heph_rmsnorm first); a
+    # traced step runs the ops one by one. Same cache position, same
+    # weights: the logits must be the same bits.
+    w, kv = setup_model(cfg, 40, 31)
+    dec_ = DEC.Qwen3Decoder(w, kv)
+    fused_tok = int(dec_.step(77, 40).item())
+    fused = dec_.logits.clone()
+    trace = []
+    traced_tok = int(dec_.step(77, 40, trace=trace).item())
+    assert torch.equal(dec_.logits, fused)
+    assert fused_tok == traced_tok
+
+
+@pytest.mark.parametrize("block", [True, False])
+@pytest.mark.parametrize("gamma", [True, False])
+@pytest.mark.parametrize("I,K", [(9728, 2560), (256, 128), (1024, 8192), (512, 9728)])
+def test_linear_fp8_swiglu_matches_two_ops(I, K, gamma, block):
+    # One launch against the gate/up linear (bf16 output, with or without
+    # the fused RMSNorm) followed by silu_mul: the same bits, block and
+    # per-row weight scales, shapes whose M = 1 launch takes 1, 2, 4 or 8
+    # chunk slots and 4 or 8 waves; the workspaces hold the same codes and
+    # scales
+    from hephaestus_amd import kernels as HK
+    N = 2 * I
+    if gamma and K > DEC.NORM_LINEAR_MAX_K:
+        pytest.skip("the fused norm holds at most 8192 elements")
+    rng = np.random.default_rng(I + K)
+    x = dev(rng_bf16(I + 3 * K, K, 2.0))
+    gam = dev(bf16_np(1.0 + 0.1 * rng.standard_normal(K))) if gamma else None
+    if block:
+        qw, sw = O.gen_weight(I + K, N, K)
+    else:
+        qw, sw = O.quant_weight(O.gen_normal(I + K, N * K, 0.0, 0.02).reshape(N, K), 1, K)
+    w, swd = dev(qw), dev(np.ascontiguousarray(sw, np.float32))
+    q1, s1 = HK.workspace(1, K)
+    q2, s2 = HK.workspace(1, K)
+    act = torch.empty(I, dtype=torch.bfloat16, device="cuda")
+    HK.linear_fp8_swiglu(act, x, gam, 1e-6, w, swd, q1, s1, N, K)
+    assert HK.last_kernel() == ("fp8_gemv_rmsnorm_swiglu_m1" if gamma else "fp8_gemv_swiglu_m1")
+    gu = torch.empty(1, N, dtype=torch.bfloat16, device="cuda")
+    if gamma:
+        HK.linear_fp8_rmsnorm(gu, x, gam, 1e-6, w, swd, q2, s2, N, K)
+    else:
+        HK.linear_fp8(gu, x.view(1, K), w, swd, q2, s2, 1, N, K, group_k=128)
+    ref = torch.empty(I, dtype=torch.bfloat16, device="cuda")
+    DEC.silu_mul(ref, gu[0, :I].contiguous(), gu[0, I:].contiguous(), I)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(act), host(ref)), np.flatnonzero(host(act) != host(ref))[:8]
+    assert torch.equal(q1, q2) and torch.equal(s1, s2)
+
+
 def test_decode_small_model_free_running():
     free_running(SMALL, ctx=300, token=1234, seed=11, name="small_free_running_argmax")
 
