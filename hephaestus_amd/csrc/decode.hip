@@ -147,10 +147,47 @@ __device__ __forceinline__ void rope_cs(int pos, int p, int D, double theta, flo
     s = round_bf16((float)sin((double)freq));
 }
 
-// One wave per head (D = 128): lane l holds elements l and l + 64, which is
-// exactly RoPE's pair (l, l + 64). Waves 0..H-1 take the q heads (normalized
-// and rotated in place), H..H+KVH-1 the k heads (normalized, rotated and
-// quantized into the cache slot), H+KVH.. the v heads (quantized).
+// The RoPE table: row pos holds (cos, sin) of pairs 0..D/2-1 as bf16
+// patterns, the values rope_cs gives. One thread per (pos, pair).
+__global__ __launch_bounds__(256) void rope_table_kernel(uint16_t* table, int n_pos, int D,
+                                                         double theta)
+{
+    const int half = D / 2;
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long)n_pos * half) return;
+    const int pos = (int)(i / half), p = (int)(i % half);
+    float c, s;
+    rope_cs(pos, p, D, theta, c, s);
+    table[2 * i] = f32_to_bf16(c);
+    table[2 * i + 1] = f32_to_bf16(s);
+}
+
+// Per-head RMSNorm and RoPE of a 128-wide head over one wave: lane l holds
+// elements a = x[l] and b = x[l + 64], which is exactly RoPE's pair
+// (l, l + 64); (c, s) are that pair's bf16 cos and sin. On return a and b
+// hold the rotated pair (bf16 values): y = bf16(gamma * bf16(x * r)) with
+// r = 1/sqrt(mean(x^2) + eps), then re = bf16(bf16(a c) - bf16(b s)),
+// im = bf16(bf16(b c) + bf16(a s)).
+__device__ __forceinline__ void head_norm_rope(float& a, float& b, float g_lo, float g_hi,
+                                               float c, float s, float eps)
+{
+    constexpr int D = 128;
+    float ss = a * a;
+    ss = __builtin_fmaf(b, b, ss);
+    ss = wave_sum64(ss);
+    const float r = __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(ss, (float)D) + eps));
+    a = round_bf16(g_lo * round_bf16(a * r));
+    b = round_bf16(g_hi * round_bf16(b * r));
+    const float re_c = round_bf16(a * c), im_s = round_bf16(b * s);
+    const float im_c = round_bf16(b * c), re_s = round_bf16(a * s);
+    a = round_bf16(re_c - im_s);
+    b = round_bf16(im_c + re_s);
+}
+
+// One wave per head (D = 128), lane l holding elements l and l + 64. Waves
+// 0..H-1 take the q heads (normalized and rotated in place), H..H+KVH-1 the
+// k heads (normalized, rotated and quantized into the cache slot),
+// H+KVH.. the v heads (quantized).
 __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
     uint16_t* qkv, const uint16_t* q_gamma, const uint16_t* k_gamma, uint8_t* k_slot,
     uint8_t* v_slot, const float* kv_inv, int n_heads, int n_kv, int pos, double theta, float eps)
@@ -168,25 +205,17 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
         return;
     }
     const uint16_t* gamma = h < n_heads ? q_gamma : k_gamma;
-    float ss = a * a;
-    ss = __builtin_fmaf(b, b, ss);
-    ss = wave_sum64(ss);
-    const float r = __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(ss, (float)D) + eps));
-    a = round_bf16(f32_of_bf16(gamma[l]) * round_bf16(a * r));
-    b = round_bf16(f32_of_bf16(gamma[l + 64]) * round_bf16(b * r));
     float c, s;
     rope_cs(pos, l, D, theta, c, s);
-    const float re_c = round_bf16(a * c), im_s = round_bf16(b * s);
-    const float im_c = round_bf16(b * c), re_s = round_bf16(a * s);
-    const float re = round_bf16(re_c - im_s), im = round_bf16(im_c + re_s);
+    head_norm_rope(a, b, f32_of_bf16(gamma[l]), f32_of_bf16(gamma[l + 64]), c, s, eps);
     if (h < n_heads) {
-        row[l] = f32_to_bf16(re);
-        row[l + 64] = f32_to_bf16(im);
+        row[l] = f32_to_bf16(a);
+        row[l + 64] = f32_to_bf16(b);
     } else {
         const int kh = h - n_heads;
         const float inv = kv_inv[kh];
-        k_slot[kh * D + l] = (uint8_t)e4m3_sat(re * inv);
-        k_slot[kh * D + l + 64] = (uint8_t)e4m3_sat(im * inv);
+        k_slot[kh * D + l] = (uint8_t)e4m3_sat(a * inv);
+        k_slot[kh * D + l + 64] = (uint8_t)e4m3_sat(b * inv);
     }
 }
 
@@ -278,10 +307,37 @@ __device__ __forceinline__ float slots_reduce(float x)
                : __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
 }
 
-template <int G>
+// The token's q/k/v preparation done by the scores kernel in its QKV form
+// (heph_attention_qkv_fp8kv): the raw projection row, the per-head norm
+// gammas, the cache rows of the new key (position n_keys - 1) and the
+// inverse K|V scales.
+struct QkvPrep {
+    const uint16_t* qkv;     // [n_heads + 2 n_kv, 128] bf16: q heads, k heads, v heads
+    const uint16_t* q_gamma;
+    const uint16_t* k_gamma;
+    uint8_t* k_slot;         // [n_kv, 128] codes of the new key
+    uint8_t* v_slot;
+    const float* kv_inv;     // n_kv K entries, then n_kv V entries
+    const uint16_t* rope;    // (cos, sin) bf16 of the 64 pairs at the new key's
+                             // position, or nullptr: computed here (rope_cs)
+    int n_heads;
+    double theta;
+    float eps;
+};
+
+// QKV form: the workgroup first prepares what qk_norm_rope_kv_kernel would
+// have left in memory, with the same arithmetic (head_norm_rope): its G
+// query heads, and in the split holding the new key (the last) that key's
+// k and v rows, quantized into the cache (the values kernel reads v from
+// there). Work items (the G q heads, then k and v) go round-robin to the
+// four waves, every raw load issued before the first reduction; the rotated
+// q heads and the new key's codes meet in LDS after one barrier, and the
+// new key's score uses those codes instead of the cache row loaded at the
+// start. All of it runs while the cache loads are in flight.
+template <int G, bool QKV>
 __global__ __launch_bounds__(256) void attn_scores_kernel(
     float* ws, const uint16_t* q, const uint8_t* kc, const float* kv_scale, int n_kv,
-    int n_keys, int n_splits)
+    int n_keys, int n_splits, QkvPrep prep)
 {
     constexpr int D = 128;
     const int kh = blockIdx.x % n_kv, split = blockIdx.x / n_kv;
@@ -294,15 +350,96 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
     for (int i = 0; i < 4; ++i)
         kv[i] = ldg16u(kc + (size_t)min(j0 + 32 * i, n_keys - 1) * row + kh * D + 16 * c);
     float qv[G][16];
+    if constexpr (QKV) {
+        // items 0..G-1: q heads kh*G + g; G: the new key's k row; G + 1: its
+        // v row (last split only)
+        constexpr int NI = (G + 2 + 3) / 4;
+        __shared__ __attribute__((aligned(16))) uint16_t qs[G][D];
+        __shared__ __attribute__((aligned(16))) uint8_t knew[D];
+        const int wave = t >> 6, l = t & 63;
+        const bool last = split == n_splits - 1;
+        const int items = last ? G + 2 : G;
+        uint32_t rcs = 0;
+        if (prep.rope) rcs = reinterpret_cast<const uint32_t*>(prep.rope)[l];
+        float xa[NI], xb[NI], ga[NI], gb[NI];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const uint16_t* qp = q + (size_t)(kh * G + g) * D + 16 * c;
-        const uint4 a = ldg16u(qp), b = ldg16u(qp + 8);
-        const uint32_t d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        for (int k = 0; k < NI; ++k) {
+            const int it = wave + 4 * k;
+            xa[k] = xb[k] = ga[k] = gb[k] = 0.0f;
+            if (it < items) {
+                const int h = it < G ? kh * G + it
+                                     : prep.n_heads + (it == G ? kh : n_kv + kh);
+                const uint16_t* r = prep.qkv + (size_t)h * D;
+                xa[k] = f32_of_bf16(r[l]);
+                xb[k] = f32_of_bf16(r[l + 64]);
+                if (it <= G) {
+                    const uint16_t* gm = it < G ? prep.q_gamma : prep.k_gamma;
+                    ga[k] = f32_of_bf16(gm[l]);
+                    gb[k] = f32_of_bf16(gm[l + 64]);
+                }
+            }
+        }
+        float cs, sn;
+        if (prep.rope) {
+            cs = bf16lo(rcs);
+            sn = bf16hi(rcs);
+        } else {
+            rope_cs(n_keys - 1, l, D, prep.theta, cs, sn);
+        }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            qv[g][2 * e] = bf16lo(d[e]);
-            qv[g][2 * e + 1] = bf16hi(d[e]);
+        for (int k = 0; k < NI; ++k) {
+            const int it = wave + 4 * k;
+            if (it >= items) break;
+            float a = xa[k], b = xb[k];
+            if (it == G + 1) {                  // v: quantize only
+                const float inv = prep.kv_inv[n_kv + kh];
+                prep.v_slot[kh * D + l] = (uint8_t)e4m3_sat(a * inv);
+                prep.v_slot[kh * D + l + 64] = (uint8_t)e4m3_sat(b * inv);
+                continue;
+            }
+            head_norm_rope(a, b, ga[k], gb[k], cs, sn, prep.eps);
+            if (it < G) {
+                qs[it][l] = f32_to_bf16(a);
+                qs[it][l + 64] = f32_to_bf16(b);
+            } else {
+                const float inv = prep.kv_inv[kh];
+                const uint8_t lo = (uint8_t)e4m3_sat(a * inv), hi = (uint8_t)e4m3_sat(b * inv);
+                prep.k_slot[kh * D + l] = lo;
+                prep.k_slot[kh * D + l + 64] = hi;
+                knew[l] = lo;
+                knew[l + 64] = hi;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const uint4 a = *reinterpret_cast<const uint4*>(&qs[g][16 * c]);
+            const uint4 b = *reinterpret_cast<const uint4*>(&qs[g][16 * c + 8]);
+            const uint32_t d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                qv[g][2 * e] = bf16lo(d[e]);
+                qv[g][2 * e + 1] = bf16hi(d[e]);
+            }
+        }
+        // the new key (and the clamped indices past it) takes the codes
+        // just computed, not the cache row read before they were written
+        if (last) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (j0 + 32 * i >= n_keys - 1) kv[i] = *reinterpret_cast<const uint4*>(&knew[16 * c]);
+        }
+    } else {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const uint16_t* qp = q + (size_t)(kh * G + g) * D + 16 * c;
+            const uint4 a = ldg16u(qp), b = ldg16u(qp + 8);
+            const uint32_t d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                qv[g][2 * e] = bf16lo(d[e]);
+                qv[g][2 * e + 1] = bf16hi(d[e]);
+            }
         }
     }
     const float qk_scale = kv_scale[kh] * 0.08838834764831845f;   // sk * f32(1/sqrt(128))
@@ -582,13 +719,21 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(int32_t* out, const A
 
 int status_of(hipError_t e) { return e == hipSuccess ? HEPH_OK : HEPH_ERR_LAUNCH; }
 
+// prep.qkv set: the QKV form of the scores kernel (q, k and v prepared
+// inside; q is then not read).
 template <int G>
 hipError_t launch_attention(uint16_t* out, const uint16_t* q, const uint8_t* kc, const uint8_t* vc,
-                            const float* kv_scale, int n_kv, int n_keys, float* ws, hipStream_t s)
+                            const float* kv_scale, int n_kv, int n_keys, float* ws, hipStream_t s,
+                            const QkvPrep& prep = QkvPrep{})
 {
     const int splits = (n_keys + kAttnSplit - 1) / kAttnSplit;
     const int blocks = n_kv * splits;
-    attn_scores_kernel<G><<<blocks, 256, 0, s>>>(ws, q, kc, kv_scale, n_kv, n_keys, splits);
+    if (prep.qkv)
+        attn_scores_kernel<G, true><<<blocks, 256, 0, s>>>(ws, q, kc, kv_scale, n_kv, n_keys,
+                                                          splits, prep);
+    else
+        attn_scores_kernel<G, false><<<blocks, 256, 0, s>>>(ws, q, kc, kv_scale, n_kv, n_keys,
+                                                           splits, prep);
     attn_pv_kernel<G><<<blocks, 256, 0, s>>>(ws, vc, n_kv, n_keys, splits);
     attn_combine_kernel<<<n_kv * G, 128, 0, s>>>(out, ws, kv_scale, n_kv * G, n_kv, n_keys, splits);
     return hipGetLastError();
@@ -652,6 +797,18 @@ int heph_qk_norm_rope_kv(void* qkv_bf16, const void* q_gamma, const void* k_gamm
     return status_of(hipGetLastError());
 }
 
+int heph_rope_table_bf16(void* table_bf16, int n_pos, int head_dim, double theta, void* stream)
+{
+    if (!table_bf16) return HEPH_ERR_NULL;
+    if (n_pos < 1 || n_pos > HEPH_ATTN_MAX_KEYS || head_dim != 128) return HEPH_ERR_SHAPE;
+    if (reinterpret_cast<uintptr_t>(table_bf16) % 4) return HEPH_ERR_ALIGN;
+    if (int st = check_device()) return st;
+    const long n = (long)n_pos * (head_dim / 2);
+    rope_table_kernel<<<(unsigned)((n + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+        static_cast<uint16_t*>(table_bf16), n_pos, head_dim, theta);
+    return status_of(hipGetLastError());
+}
+
 size_t heph_attention_ws_bytes(int n_heads, int n_keys)
 {
     if (n_heads < 1 || n_keys < 1) return 0;
@@ -686,6 +843,53 @@ int heph_attention_fp8kv(void* out_bf16, const void* q_bf16, const uint8_t* k_ca
     case 2: e = launch_attention<2>(out, q, k_cache, v_cache, kv_scale, n_kv_heads, n_keys, w, s); break;
     case 4: e = launch_attention<4>(out, q, k_cache, v_cache, kv_scale, n_kv_heads, n_keys, w, s); break;
     default: e = launch_attention<8>(out, q, k_cache, v_cache, kv_scale, n_kv_heads, n_keys, w, s); break;
+    }
+    return status_of(e);
+}
+
+int heph_attention_qkv_fp8kv(void* out_bf16, const void* qkv_bf16, const void* q_gamma,
+                             const void* k_gamma, uint8_t* k_cache, uint8_t* v_cache,
+                             const float* kv_scale, const float* kv_inv_scale,
+                             const void* rope_table, int n_heads, int n_kv_heads, int head_dim,
+                             int pos, double theta, float eps, void* ws, size_t ws_bytes,
+                             void* stream)
+{
+    if (!out_bf16 || !qkv_bf16 || !q_gamma || !k_gamma || !k_cache || !v_cache || !kv_scale ||
+        !kv_inv_scale || !ws)
+        return HEPH_ERR_NULL;
+    if (head_dim != 128 || n_kv_heads < 1 || n_heads < n_kv_heads || n_heads % n_kv_heads ||
+        pos < 0 || pos >= HEPH_ATTN_MAX_KEYS)
+        return HEPH_ERR_SHAPE;
+    const int G = n_heads / n_kv_heads;
+    if (G != 1 && G != 2 && G != 4 && G != 8) return HEPH_ERR_SHAPE;
+    const int n_keys = pos + 1;
+    if (ws_bytes < heph_attention_ws_bytes(n_heads, n_keys)) return HEPH_ERR_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(k_cache) % 16 || reinterpret_cast<uintptr_t>(v_cache) % 16 ||
+        reinterpret_cast<uintptr_t>(ws) % 16 || reinterpret_cast<uintptr_t>(rope_table) % 4)
+        return HEPH_ERR_ALIGN;
+    if (int st = check_device()) return st;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const size_t slot = (size_t)pos * n_kv_heads * 128;
+    QkvPrep prep;
+    prep.qkv = static_cast<const uint16_t*>(qkv_bf16);
+    prep.q_gamma = static_cast<const uint16_t*>(q_gamma);
+    prep.k_gamma = static_cast<const uint16_t*>(k_gamma);
+    prep.k_slot = k_cache + slot;
+    prep.v_slot = v_cache + slot;
+    prep.kv_inv = kv_inv_scale;
+    prep.rope = rope_table ? static_cast<const uint16_t*>(rope_table) + (size_t)pos * 128
+                           : nullptr;
+    prep.n_heads = n_heads;
+    prep.theta = theta;
+    prep.eps = eps;
+    uint16_t* out = static_cast<uint16_t*>(out_bf16);
+    float* w = static_cast<float*>(ws);
+    hipError_t e;
+    switch (G) {
+    case 1: e = launch_attention<1>(out, nullptr, k_cache, v_cache, kv_scale, n_kv_heads, n_keys, w, s, prep); break;
+    case 2: e = launch_attention<2>(out, nullptr, k_cache, v_cache, kv_scale, n_kv_heads, n_keys, w, s, prep); break;
+    case 4: e = launch_attention<4>(out, nullptr, k_cache, v_cache, kv_scale, n_kv_heads, n_keys, w, s, prep); break;
+    default: e = launch_attention<8>(out, nullptr, k_cache, v_cache, kv_scale, n_kv_heads, n_keys, w, s, prep); break;
     }
     return status_of(e);
 }

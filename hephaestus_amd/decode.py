@@ -10,6 +10,7 @@ per (layer, kv head, K|V):
               (norm + quant inside the GEMV; = heph_rmsnorm then heph_fp8_linear)
         q, k, v: per-head q/k norm, RoPE, k/v -> cache   heph_qk_norm_rope_kv
         att = attention(q, K[:pos+1], V[:pos+1])         heph_attention_fp8kv
+              (both in the attention's launches:        heph_attention_qkv_fp8kv)
         x  += att @ Wo^T                                 heph_fp8_linear + ADD_RESIDUAL
         gu  = rmsnorm(x, ffn_norm) @ Wgate_up^T          heph_fp8_linear_rmsnorm
         act = silu(gate) * up                            heph_silu_mul
@@ -75,6 +76,32 @@ def attention_fp8kv(out, q, k_cache, v_cache, kv_scale, n_heads: int, n_kv: int,
         ws = attention_ws(n_heads, n_keys, device=out.device)
     _call("heph_attention_fp8kv", _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache),
           _ptr(kv_scale), n_heads, n_kv, 128, n_keys, _ptr(ws), ws.numel(), _stream())
+
+
+def rope_table(n_pos: int, theta: float = 1e6, device="cuda") -> torch.Tensor:
+    """(cos, sin) bf16 of the 64 RoPE pairs of a 128-wide head at positions
+    0..n_pos-1, [n_pos, 64, 2]: the values qk_norm_rope_kv computes."""
+    t = torch.empty(n_pos, 64, 2, dtype=torch.bfloat16, device=device)
+    _call("heph_rope_table_bf16", _ptr(t), n_pos, 128, theta, _stream())
+    return t
+
+
+def attention_qkv_fp8kv(out, qkv, q_gamma, k_gamma, k_cache, v_cache, kv_scale, kv_inv,
+                        n_heads: int, n_kv: int, pos: int, theta: float = 1e6,
+                        eps: float = 1e-6, ws: torch.Tensor | None = None,
+                        rope: torch.Tensor | None = None) -> None:
+    """qk_norm_rope_kv into cache row pos, then attention_fp8kv over pos + 1
+    keys, in the attention's three launches (the same out and cache bytes;
+    q in qkv is not rotated in place). rope: a rope_table of more than pos
+    rows for this theta, or None to compute pos's cos/sin in the call."""
+    if ws is None:
+        ws = attention_ws(n_heads, pos + 1, device=out.device)
+    if rope is not None and rope.shape[0] <= pos:
+        raise ValueError(f"rope table of {rope.shape[0]} rows has no row {pos}")
+    _call("heph_attention_qkv_fp8kv", _ptr(out), _ptr(qkv), _ptr(q_gamma), _ptr(k_gamma),
+          _ptr(k_cache), _ptr(v_cache), _ptr(kv_scale), _ptr(kv_inv),
+          None if rope is None else _ptr(rope), n_heads, n_kv, 128, pos, theta, eps, _ptr(ws),
+          ws.numel(), _stream())
 
 
 def silu_mul(out, gate, up, n: int) -> None:
@@ -190,6 +217,7 @@ class Qwen3Decoder:
         self.token = torch.zeros(1, dtype=torch.int32, device=dev)
         self.q_ws, self.s_ws = HK.workspace(1, max(H, Q, I), device=dev)
         self.attn_ws = attention_ws(cfg.n_heads, kv.max_ctx, device=dev)
+        self.rope = rope_table(kv.max_ctx, cfg.theta, device=dev)
         self.arg_ws = argmax_ws(cfg.vocab, device=dev)
 
     def _linear(self, c, a, fw: Fp8Weight, K: int, residual: bool = False):
@@ -242,13 +270,20 @@ class Qwen3Decoder:
         for li, lw in enumerate(w.layers):
             self._norm_linear(self.qkv, lw.attn_norm, lw.qkv, H, eps, rec, li, "attn_norm")
             rec(li, "qkv", self.qkv)
-            qk_norm_rope_kv(self.qkv, lw.q_norm, lw.k_norm, kv.k[li, pos], kv.v[li, pos],
-                            kv.inv[li], NH, NKV, pos, cfg.theta, eps)
-            rec(li, "q_rope", self.qkv[:, :Q])
-            rec(li, "k_codes", kv.k[li, pos])
-            rec(li, "v_codes", kv.v[li, pos])
-            attention_fp8kv(self.att, self.qkv, kv.k[li], kv.v[li], kv.scale[li], NH, NKV,
-                            pos + 1, self.attn_ws)
+            if rec.tracing:
+                qk_norm_rope_kv(self.qkv, lw.q_norm, lw.k_norm, kv.k[li, pos], kv.v[li, pos],
+                                kv.inv[li], NH, NKV, pos, cfg.theta, eps)
+                rec(li, "q_rope", self.qkv[:, :Q])
+                rec(li, "k_codes", kv.k[li, pos])
+                rec(li, "v_codes", kv.v[li, pos])
+                attention_fp8kv(self.att, self.qkv, kv.k[li], kv.v[li], kv.scale[li], NH, NKV,
+                                pos + 1, self.attn_ws)
+            else:
+                # q/k norm, RoPE and the K/V write inside the attention's
+                # scores kernel: bit for bit the two ops above
+                attention_qkv_fp8kv(self.att, self.qkv, lw.q_norm, lw.k_norm, kv.k[li],
+                                    kv.v[li], kv.scale[li], kv.inv[li], NH, NKV, pos, cfg.theta,
+                                    eps, self.attn_ws, self.rope)
             rec(li, "attention", self.att)
             self._linear(self.x, self.att, lw.o, Q, residual=True)
             rec(li, "o_residual", self.x)

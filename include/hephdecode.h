@@ -70,6 +70,35 @@ int heph_attention_fp8kv(void* out_bf16, const void* q_bf16, const uint8_t* k_ca
                          void* stream);
 
 /*
+ * RoPE table: table_bf16[pos][p] = (cos, sin) of pair p < head_dim/2 at
+ * position pos < n_pos as bf16 patterns (2 * n_pos * head_dim/2 values,
+ * 4-byte aligned): exactly the values heph_qk_norm_rope_kv computes,
+ * freq = f32(pos * theta^(-2p/head_dim)) in double, cos/sin of it rounded
+ * to f32, then bf16. head_dim 128. The cos/sin of kernels.mojo:709-762,
+ * computed once per position instead of per call.
+ */
+int heph_rope_table_bf16(void* table_bf16, int n_pos, int head_dim, double theta, void* stream);
+
+/*
+ * heph_qk_norm_rope_kv on qkv_bf16 with k_slot / v_slot = cache row `pos`
+ * (k_cache / v_cache + pos * n_kv_heads * 128), then heph_attention_fp8kv
+ * over pos + 1 keys with the rotated q: the same out, the same cache
+ * bytes, in the attention's three launches (the scores kernel prepares q
+ * and the new key's k and v itself). q in qkv_bf16 is left as it was (not
+ * rotated in place). ws: heph_attention_ws_bytes(n_heads, pos + 1) bytes.
+ * rope_table: a heph_rope_table_bf16 table with more than pos rows (for
+ * this theta and head_dim), or NULL to compute pos's cos/sin in the call.
+ * Replaces the q/k norms, RoPE, K/V write and attention call of
+ * src/hephaestus/forward.mojo:474-520 (kernels.mojo:709-796, :923-1035).
+ */
+int heph_attention_qkv_fp8kv(void* out_bf16, const void* qkv_bf16, const void* q_gamma,
+                             const void* k_gamma, uint8_t* k_cache, uint8_t* v_cache,
+                             const float* kv_scale, const float* kv_inv_scale,
+                             const void* rope_table, int n_heads, int n_kv_heads, int head_dim,
+                             int pos, double theta, float eps, void* ws, size_t ws_bytes,
+                             void* stream);
+
+/*
  * out = bf16(bf16(g / (1 + exp(-g))) * up). Replaces silu_mul
  * (src/hephaestus/kernels.mojo:1243-1278).
  */

@@ -214,6 +214,36 @@ def test_decode_ops_reject(lib):
     assert a(FAKE, FAKE, FAKE, FAKE, FAKE, 32, 8, 128, 4097, FAKE, ws - 4, None) == \
         L.HEPH_ERR_WORKSPACE
     assert a(FAKE, FAKE, ODD, FAKE, FAKE, 32, 8, 128, 10, FAKE, ws, None) == L.HEPH_ERR_ALIGN
+    # q/k norm + RoPE + K/V write + attention: the union of both ops' checks,
+    # over pos + 1 keys
+    qa = lib.heph_attention_qkv_fp8kv
+    args = [FAKE] * 9
+    assert qa(*args, 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) in \
+        (L.HEPH_ERR_DEVICE, L.HEPH_OK)
+    assert qa(*args[:7], None, FAKE, 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) == \
+        L.HEPH_ERR_NULL
+    # no table: the call computes the cos/sin of pos itself
+    assert qa(*args[:8], None, 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) in \
+        (L.HEPH_ERR_DEVICE, L.HEPH_OK)
+    assert qa(*args[:8], FAKE + 2, 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) == \
+        L.HEPH_ERR_ALIGN
+    assert qa(*args, 32, 8, 128, 4096, 1e6, 1e-6, None, ws, None) == L.HEPH_ERR_NULL
+    assert qa(*args, 32, 8, 64, 4096, 1e6, 1e-6, FAKE, ws, None) == L.HEPH_ERR_SHAPE
+    assert qa(*args, 24, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) == L.HEPH_ERR_SHAPE
+    assert qa(*args, 32, 2, 128, 4096, 1e6, 1e-6, FAKE, ws, None) == L.HEPH_ERR_SHAPE
+    assert qa(*args, 32, 8, 128, -1, 1e6, 1e-6, FAKE, ws, None) == L.HEPH_ERR_SHAPE
+    assert qa(*args, 32, 8, 128, L.ATTN_MAX_KEYS, 1e6, 1e-6, FAKE, 1 << 40, None) == \
+        L.HEPH_ERR_SHAPE
+    assert qa(*args, 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws - 4, None) == L.HEPH_ERR_WORKSPACE
+    assert qa(*args[:4], ODD, *args[5:], 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) == \
+        L.HEPH_ERR_ALIGN
+    rt = lib.heph_rope_table_bf16
+    assert rt(None, 4097, 128, 1e6, None) == L.HEPH_ERR_NULL
+    assert rt(FAKE, 0, 128, 1e6, None) == L.HEPH_ERR_SHAPE
+    assert rt(FAKE, 4097, 64, 1e6, None) == L.HEPH_ERR_SHAPE
+    assert rt(FAKE, L.ATTN_MAX_KEYS + 1, 128, 1e6, None) == L.HEPH_ERR_SHAPE
+    assert rt(FAKE + 2, 4097, 128, 1e6, None) == L.HEPH_ERR_ALIGN
+    assert rt(FAKE, 4097, 128, 1e6, None) in (L.HEPH_ERR_DEVICE, L.HEPH_OK)
     assert lib.heph_silu_mul(FAKE, FAKE, FAKE, 0, None) == L.HEPH_ERR_SHAPE
     aw = lib.heph_argmax_ws_bytes(151936)
     assert aw == 8 * 75                              # one (value, index) per 2048 logits

@@ -195,6 +195,65 @@ def test_attention_rejects_long_context_and_small_workspace():
         DEC.attention_fp8kv(z, z, z, z, z, 32, 8, 100, ws=z)
 
 
+@pytest.mark.parametrize("nh,nkv", [(32, 8), (8, 8), (8, 4), (16, 2)], ids=["g4", "g1", "g2", "g8"])
+@pytest.mark.parametrize("pos", [0, 1, 127, 128, 300, 4096])
+def test_attention_qkv_matches_separate_ops(pos, nh, nkv):
+    # heph_attention_qkv_fp8kv against heph_qk_norm_rope_kv into cache row
+    # pos followed by heph_attention_fp8kv over pos + 1 keys: the same output
+    # bits and the same cache bytes (the new row included, every other row
+    # untouched), with garbage in the new row beforehand; q in qkv stays raw.
+    rng = np.random.default_rng(1000 + pos + nh)
+    qkv = rng_bf16(pos + 7, (nh + 2 * nkv) * 128, 2.0)
+    qg, kg = rng_bf16(pos + 8, 128), rng_bf16(pos + 9, 128)
+    sc = (rng.random(2 * nkv, dtype=np.float32) * 0.02 + 0.005).astype(np.float32)
+    inv = (np.float32(1.0) / sc).astype(np.float32)
+    kc, vc = codes(rng, (pos + 1, nkv, 128)), codes(rng, (pos + 1, nkv, 128))
+    ws = DEC.attention_ws(nh, pos + 1)
+
+    # separate ops
+    q_sep, k_sep, v_sep = dev(qkv), dev(kc), dev(vc)
+    out_sep = torch.empty(nh * 128, dtype=torch.bfloat16, device="cuda")
+    DEC.qk_norm_rope_kv(q_sep, dev(qg), dev(kg), k_sep[pos], v_sep[pos], dev(inv), nh, nkv, pos,
+                        1e6, 1e-6)
+    DEC.attention_fp8kv(out_sep, q_sep, k_sep, v_sep, dev(sc), nh, nkv, pos + 1, ws)
+    # one call, with the cos/sin from a table and computed in the call
+    for rope in (DEC.rope_table(pos + 1 + 3 * (pos % 2), 1e6), None):
+        q_one, k_one, v_one = dev(qkv), dev(kc), dev(vc)
+        out_one = torch.empty_like(out_sep)
+        DEC.attention_qkv_fp8kv(out_one, q_one, dev(qg), dev(kg), k_one, v_one, dev(sc),
+                                dev(inv), nh, nkv, pos, 1e6, 1e-6, ws, rope)
+        torch.cuda.synchronize()
+        assert np.array_equal(host(out_one), host(out_sep))
+        assert np.array_equal(host(k_one), host(k_sep))
+        assert np.array_equal(host(v_one), host(v_sep))
+        assert np.array_equal(host(q_one), qkv)
+        assert not np.array_equal(host(k_one)[pos], kc[pos])
+
+
+@pytest.mark.parametrize("theta", [1e6, 1e4])
+def test_rope_table_bit_exact(theta):
+    # every (cos, sin) of the table against the oracle's rope_cs at positions
+    # spread over the attention's key range
+    n = 4097
+    t = host(DEC.rope_table(n, theta)).reshape(n, 64, 2)
+    for pos in (0, 1, 2, 127, 128, 1000, 4095, 4096):
+        for p in range(64):
+            c, s = O.rope_cs(pos, p, 128, theta)
+            assert t[pos, p, 0] == bf16_np(np.float32(c)), (pos, p)
+            assert t[pos, p, 1] == bf16_np(np.float32(s)), (pos, p)
+    with pytest.raises(ValueError, match="no row"):
+        z = torch.zeros(16, dtype=torch.uint8, device="cuda")
+        DEC.attention_qkv_fp8kv(z, z, z, z, z, z, z, z, 32, 8, 10, rope=DEC.rope_table(5))
+
+
+def test_attention_qkv_rejects():
+    z = torch.zeros(16, dtype=torch.uint8, device="cuda")
+    with pytest.raises(HephError):
+        DEC.attention_qkv_fp8kv(z, z, z, z, z, z, z, z, 32, 8, L.ATTN_MAX_KEYS, ws=z)
+    with pytest.raises(HephError):
+        DEC.attention_qkv_fp8kv(z, z, z, z, z, z, z, z, 32, 8, 99, ws=z)
+
+
 def test_silu_mul_vs_oracle():
     g, u = rng_bf16(5, 9728, 4.0), rng_bf16(6, 9728)
     out = torch.empty(9728, dtype=torch.bfloat16, device="cuda")
