@@ -127,7 +127,7 @@ int take_overrides(const heph_launch_overrides* ov, Tuning* t)
     if (!ov) return HEPH_OK;
     const int ks = ov->gemv_ks, w = ov->gemv_waves, u = ov->gemv_u, bm = ov->gemm_bm;
     if (ks != 0 && ks != 1 && ks != 2 && ks != 4 && ks != 8) return HEPH_ERR_FLAGS;
-    if (w != 0 && w != 4 && w != 8 && w != 16) return HEPH_ERR_FLAGS;
+    if (w != 0 && w != 4 && w != 5 && w != 8 && w != 10 && w != 16) return HEPH_ERR_FLAGS;
     if (u != 0 && u != 1 && u != 2) return HEPH_ERR_FLAGS;
     if (bm != 0 && bm != 1 && bm != 64 && bm != 128 && bm != 192 && bm != 256)
         return HEPH_ERR_FLAGS;

@@ -774,8 +774,8 @@ hipError_t launch_splitk_reduce(const Fp8Operands& op, hipStream_t stream, const
 }
 
 namespace {
-
 int g_cu_count[64];
+}  // namespace
 
 int cu_count()
 {
@@ -790,6 +790,8 @@ int cu_count()
     }
     return n;
 }
+
+namespace {
 
 template <int BM>
 hipError_t launch_big(const Fp8Operands& op, hipStream_t stream, const LaunchTiming& t)

@@ -87,7 +87,16 @@ int gemv_rows(int M)
     return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16;
 }
 
-// Launch shape. Chunk slots: at M <= 2 the fewest (at most 16 / rows per
+// Launch shape. M = 1 without a fused norm: four chunk slots from K = 1024
+// on (fewer only where N is large enough without them), and waves for one
+// step each, else two, while the workgroups' waves fit the CUs at once (32
+// per CU); past that 4 waves. MI355X, graph-replayed per call over rotated
+// weights, against the norm forms' shape below: gate_up 11.0 against 11.8
+// us (4 slots x 4 waves, 4864 workgroups), down 8.1 against 8.3 (4 x 10),
+// qkv 5.5 against 5.6 (4 x 5), q_proj 4.6 against 4.7 (4 x 5), o_proj
+// unchanged (4 x 8).
+// Otherwise (and for the norm forms) chunk slots: at M <= 2 the fewest
+// (at most 16 / rows per
 // slot) that give >= 600 workgroups (about 2.3 per CU); at 4 and 8 rows
 // per slot one (two at 4 rows when K >= 8192), as every workgroup quantizes
 // all M x K activations again and wider workgroups do that less often
@@ -100,25 +109,42 @@ int gemv_rows(int M)
 // 8 < M <= 16. Steps per batch: at M = 1 two when each wave has exactly
 // 2 steps; at 5..8 rows with K >= 8192 two; else one (wider activation
 // tiles need the registers).
-void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, int* u)
+void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, int* u,
+                bool norm)
 {
     const int mr = gemv_rows(M);
     const int kmax = mr >= 2 ? 16 / mr : 8;
     const int tiles = N / 16, KC = K / kChunk;
+    const bool plain1 = mr == 1 && !norm;
     int k = 1;
     if (mr <= 2)
         while (k < kmax && tiles * k < 600) k *= 2;
     else if (mr == 4 && K >= 8192)
         k = 2;
+    if (plain1 && k < 4 && KC >= 8) k = 4;
     const int fk = tune.gemv_ks;
     if (fk) k = fk < kmax ? fk : kmax;
     const int S = (KC + k - 1) / k;
     int w = mr == 1 ? (S <= 3 ? 4 : 8) : (S < 8 ? 4 : 8);
+    if (plain1) {
+        // the fewest steps per wave (1, then 2) whose wave count, rounded up
+        // to one of 4, 5, 8, 10, fits every workgroup on the CUs at once
+        const long budget = 32L * cu_count(), wgs = (long)tiles * k;
+        w = 4;
+        for (int p = 1; p <= 2; ++p) {
+            int need = (S + p - 1) / p;
+            need = need <= 4 ? 4 : need <= 5 ? 5 : need <= 8 ? 8 : need <= 10 ? 10 : 0;
+            if (need && wgs * need <= budget) {
+                w = need;
+                break;
+            }
+        }
+    }
     if (mr == 16 && M <= 16 && S <= 24) w = 4;
     const int fw = tune.gemv_waves;
-    if (fw) w = fw == 16 && (mr != 16 || M > 16) ? 8 : fw;
+    if (fw) w = (fw == 16 && (mr != 16 || M > 16)) || ((fw == 5 || fw == 10) && mr != 1) ? 8 : fw;
     int uu = 1;
-    if (mr == 1 && (S + w - 1) / w == 2) uu = 2;
+    if (mr == 1 && !plain1 && (S + w - 1) / w == 2) uu = 2;
     if (mr == 8 && K >= 8192) uu = 2;
     const int fu = tune.gemv_u;
     if (fu) uu = fu;
@@ -134,11 +160,18 @@ hipError_t launch_fp8_gemv(const Fp8Operands& op, bool fused, hipStream_t stream
 {
     GemvArgs a{op, fused, gamma, eps};
     int ks, waves, u;
-    gemv_shape(op.M, op.N, op.K, op.tune, &ks, &waves, &u);
+    gemv_shape(op.M, op.N, op.K, op.tune, &ks, &waves, &u, gamma != nullptr);
     const int mr = gemv_rows(op.M);
     if (op.M == 1) *name = gamma ? "fp8_gemv_rmsnorm_m1" : fused ? "fp8_gemv_fused_m1" : "fp8_gemv_m1";
     else if (op.M <= 16) *name = fused ? "fp8_gemv_fused_m16" : "fp8_gemv_m16";
     else *name = fused ? "fp8_gemv_fused_m32" : "fp8_gemv_m32";
+    if (mr == 1 && (waves == 5 || waves == 10)) {
+        if (waves == 5)
+            return u == 2 ? launch_mr<5, 1, 1, 2>(a, fused, ks, stream, t)
+                          : launch_mr<5, 1, 1, 1>(a, fused, ks, stream, t);
+        return u == 2 ? launch_mr<10, 1, 1, 2>(a, fused, ks, stream, t)
+                      : launch_mr<10, 1, 1, 1>(a, fused, ks, stream, t);
+    }
     switch (waves) {
     case 16: return launch_wu<16, 1>(a, fused, ks, mr, stream, t);
     case 8:

@@ -8,9 +8,9 @@
 // up rows; each workgroup finishes TW/2 gate and TW/2 up columns, so the
 // SwiGLU of a column pair runs once, where both sums are, and neither the
 // gate/up output nor a SwiGLU launch exists. The launch shape (chunk
-// slots, waves, steps per batch) is the one the plain M = 1 GEMV takes for
-// the same N x K, so every sum runs in the same order: the output is bit
-// for bit the two-launch form's.
+// slots, waves, steps per batch) is the one the M = 1 GEMV takes for the
+// same N x K (with the norm: the RMSNorm-fused GEMV's), so every sum runs in
+// the same order: the output is bit for bit the two-launch form's.
 #include "gemv_kernel.h"
 
 namespace heph {
@@ -54,12 +54,17 @@ hipError_t launch_fp8_gemv_swiglu(const Fp8Operands& op, hipStream_t stream,
 {
     const GemvArgs a{op, true, gamma, eps};
     int ks, waves, u;
-    gemv_shape(1, op.N, op.K, Tuning{}, &ks, &waves, &u);
+    gemv_shape(1, op.N, op.K, Tuning{}, &ks, &waves, &u, gamma != nullptr);
     *name = gamma ? "fp8_gemv_rmsnorm_swiglu_m1" : "fp8_gemv_swiglu_m1";
-    // M = 1 takes 4 or 8 waves (gemv_shape)
-    if (waves == 4)
+    // M = 1 takes 4, 5, 8 or 10 waves (gemv_shape; 5 and 10 in one-step batches)
+    switch (waves) {
+    case 4:
         return u == 2 ? launch_glu_ks<4, 2>(a, ks, stream, t) : launch_glu_ks<4, 1>(a, ks, stream, t);
-    return u == 2 ? launch_glu_ks<8, 2>(a, ks, stream, t) : launch_glu_ks<8, 1>(a, ks, stream, t);
+    case 5: return launch_glu_ks<5, 1>(a, ks, stream, t);
+    case 10: return launch_glu_ks<10, 1>(a, ks, stream, t);
+    default:
+        return u == 2 ? launch_glu_ks<8, 2>(a, ks, stream, t) : launch_glu_ks<8, 1>(a, ks, stream, t);
+    }
 }
 
 }  // namespace heph

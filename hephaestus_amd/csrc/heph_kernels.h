@@ -104,11 +104,17 @@ hipError_t launch_fp8_gemv(const Fp8Operands& op, bool fused, hipStream_t stream
 
 // Rows per chunk slot for M rows (M rounded up to a power of two, at most
 // 16), and the launch shape (chunk slots, waves, steps per batch) for
-// M x N x K with the overrides of each (0 = automatic).
+// M x N x K with the overrides of each (0 = automatic); norm: the shape of
+// the RMSNorm-fused forms (M = 1), which repeat the norm in every workgroup
+// and so keep fewer of them.
 int gemv_rows(int M);
 // Whether the chunk-slot kernel quantizes x itself for M x N x K (group 128).
 bool gemv_fuses(int M, int N, int K);
-void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, int* u);
+void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, int* u,
+                bool norm = false);
+
+// Compute units of the current device (cached per device).
+int cu_count();
 
 // Tiled MFMA GEMM for any M (prefill); reads q/s from the workspace.
 hipError_t launch_fp8_gemm(const Fp8Operands& op, hipStream_t stream,

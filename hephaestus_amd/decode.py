@@ -226,7 +226,8 @@ class Qwen3Decoder:
 
     def _norm_linear(self, c, gamma, fw: Fp8Weight, K: int, eps: float, rec, li, op):
         """c = rmsnorm(self.x, gamma) @ fw: the norm inside the fused GEMV
-        (heph_fp8_linear_rmsnorm, bit for bit heph_rmsnorm + the linear) for
+        (heph_fp8_linear_rmsnorm: heph_rmsnorm + the linear, bit for bit
+        under the norm form's launch shape) for
         rows up to NORM_LINEAR_MAX_K; longer rows take heph_rmsnorm, then
         the linear. A traced step also writes the normalized row to self.xn,
         for the record only."""

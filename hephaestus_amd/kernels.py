@@ -167,8 +167,9 @@ def _linear_fp8(c, a, w, scale, a_fp8_ws, act_scale_ws, m, n, k, ctx, *,
 def linear_fp8_rmsnorm(c, x, gamma, eps, w, scale, a_fp8_ws, act_scale_ws, n, k, ctx=None, *,
                        add_residual=False):
     """c = rmsnorm(x, gamma, eps) @ dequant(w)^T for one row (M = 1), the
-    norm computed inside the fused GEMV (bit for bit rmsnorm then linear_fp8);
-    the workspaces receive the normalized row's codes and scales."""
+    norm computed inside the fused GEMV (bit for bit rmsnorm then linear_fp8
+    with the norm form's launch shape, norm_shape_tune); the workspaces
+    receive the normalized row's codes and scales."""
     bn, bk = _weight_block(scale, n, k)
     if c.dtype not in _OUT:
         raise TypeError(f"linear_fp8_rmsnorm: output dtype {c.dtype} not supported")
@@ -184,11 +185,27 @@ def linear_fp8_rmsnorm(c, x, gamma, eps, w, scale, a_fp8_ws, act_scale_ws, n, k,
     _check(s, "linear_fp8_rmsnorm")
 
 
+def norm_shape_tune(n: int, k: int) -> dict:
+    """Launch-shape overrides under which linear_fp8 at M = 1 sums in the
+    order of the RMSNorm-fused forms (linear_fp8_rmsnorm, linear_fp8_swiglu
+    with gamma), as include/hephfp8.h states their shape: the fewest K-chunk
+    slots (<= 8) giving >= 600 workgroups of 16 / slots columns, 4 waves up
+    to 3 chunk steps, else 8, two-step batches when each wave has two."""
+    tiles, kc = n // 16, k // 128
+    ks = 1
+    while ks < 8 and tiles * ks < 600:
+        ks *= 2
+    steps = -(-kc // ks)
+    waves = 4 if steps <= 3 else 8
+    return {"gemv_ks": ks, "gemv_waves": waves, "gemv_u": 2 if -(-steps // waves) == 2 else 1}
+
+
 def linear_fp8_swiglu(act, x, gamma, eps, w, scale, a_fp8_ws, act_scale_ws, n, k, ctx=None):
     """act = silu(g) * u for one row (M = 1), with g and u the gate and up
     halves of x @ dequant(w)^T (w: gate rows, then up rows; n = 2 *
     intermediate) and x first RMS-normalized with gamma unless gamma is
-    None; bit for bit the gate/up linear then silu_mul (bf16 act, n / 2)."""
+    None; bit for bit the gate/up linear (linear_fp8_rmsnorm with gamma,
+    linear_fp8 without) then silu_mul (bf16 act, n / 2)."""
     bn, bk = _weight_block(scale, n, k)
     if act.dtype != torch.bfloat16:
         raise TypeError(f"linear_fp8_swiglu: output dtype {act.dtype} not supported")

@@ -119,9 +119,15 @@ int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16,
  * rmsnorm(x, gamma, eps) @ dequant(w)^T, where the norm is
  * bf16(gamma * bf16(x * r)) with r = 1/sqrt(mean(x^2) + eps) summed as
  * heph_rmsnorm sums it, computed by every workgroup of the fused GEMV
- * before its quantization, so the normalized row is never written. Bit for
- * bit heph_rmsnorm followed by heph_fp8_linear; the workspaces hold the
- * normalized row's codes and scales. Replaces the pair rms_norm + linear_fp8
+ * before its quantization, so the normalized row is never written. Its
+ * launch shape keeps fewer workgroups than heph_fp8_linear's at M = 1 (each
+ * repeats the norm): the fewest K-chunk slots (<= 8) giving >= 600
+ * workgroups, 4 waves up to 3 chunk steps, else 8 (two-step batches when
+ * each wave has two steps). Bit for bit heph_rmsnorm followed by
+ * heph_fp8_linear_with that shape (gemv_ks, gemv_waves, gemv_u); plain
+ * heph_fp8_linear may sum in another order (within the linear's tolerance).
+ * The workspaces hold the normalized row's codes and scales. Replaces the
+ * pair rms_norm + linear_fp8
  * of the reference's decode step (src/hephaestus/forward.mojo:359-615,
  * kernels.mojo:653-762). flags: HEPH_FLAG_ADD_RESIDUAL only; gamma 16-byte
  * aligned (HEPH_ERR_ALIGN); K <= 8192 (the row and gamma sit in the
@@ -142,9 +148,10 @@ int heph_fp8_linear_rmsnorm(void* c, int c_dtype, const uint16_t* x_bf16,
  * is NULL. w holds the gate rows then the up rows ([N, K], N % 16 == 0),
  * w_scale their 128x128 blocks (w_block_n = w_block_k = 128) or per-row
  * scales [N, 1] (1, K). act: bf16 [N/2], bf16(bf16(g / (1 + exp(-g))) * u)
- * of the bf16-rounded g and u: bit for bit the gate/up linear (bf16 output)
- * followed by heph_silu_mul, in one launch whose workgroups each finish 8
- * gate and 8 up columns. Replaces rms_norm + linear_fp8(gate_proj) +
+ * of the bf16-rounded g and u: bit for bit the gate/up linear (bf16 output;
+ * heph_fp8_linear_rmsnorm with gamma, heph_fp8_linear without) followed by
+ * heph_silu_mul, in one launch whose workgroups each finish as many gate as
+ * up columns. Replaces rms_norm + linear_fp8(gate_proj) +
  * linear_fp8(up_proj) + silu_mul of the reference's decode step
  * (src/hephaestus/forward.mojo:537-578; silu_mul, kernels.mojo:1243-1278).
  * The workspaces receive xn's codes and scales, as for the other M = 1
@@ -269,8 +276,8 @@ const char* heph_last_kernel(void);
  * overrides applied to that call only. No counterpart in the reference.
  *   gemv_ks      K-chunk slots per MFMA of the M <= 32 chunk-slot GEMV:
  *                1, 2, 4 or 8 (capped at 16 / rows per slot, i.e. 1 for M > 8)
- *   gemv_waves   its waves per workgroup: 4, 8 or 16 (16 only for
- *                8 < M <= 16; 8 is used otherwise)
+ *   gemv_waves   its waves per workgroup: 4, 5, 8, 10 or 16 (5 and 10 only
+ *                for M = 1, 16 only for 8 < M <= 16; 8 is used otherwise)
  *   gemv_u       its steps per load batch: 1 or 2 (1 with 16 waves)
  *   gemm_bm      tile height of the large-M GEMM: 64, 128, 192, 256; 1 selects
  *                the 128x128 GEMM (otherwise used only when M*K or N*K

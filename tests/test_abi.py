@@ -136,11 +136,13 @@ def with_overrides(lib, **ov):
 def test_launch_overrides_validate(lib):
     # heph_fp8_linear_with checks every override before anything else; a
     # valid set leaves the call to the device check (no GPU here).
-    ok = [dict(gemv_ks=8), dict(gemv_waves=4), dict(gemv_waves=16), dict(gemv_u=2),
+    ok = [dict(gemv_ks=8), dict(gemv_waves=4), dict(gemv_waves=5), dict(gemv_waves=10),
+          dict(gemv_waves=16), dict(gemv_u=2),
           dict(gemm_bm=192), dict(gemm_bm=64), dict(gemm_bm=1), dict(batch_split=-1),
           dict(batch_split=64), dict(wide_tiles=-1), dict(wide_tiles=4),
           dict(wide_tiles=2, wide_waves=16), dict()]
-    bad = [dict(gemv_ks=16), dict(gemv_ks=3), dict(gemv_waves=2), dict(gemv_u=4),
+    bad = [dict(gemv_ks=16), dict(gemv_ks=3), dict(gemv_waves=2), dict(gemv_waves=6),
+           dict(gemv_u=4),
            dict(gemm_bm=96), dict(batch_split=-2), dict(batch_split=65), dict(wide_tiles=3),
            dict(wide_tiles=8), dict(wide_tiles=-2), dict(wide_waves=2), dict(wide_waves=12)]
     for ov in ok:

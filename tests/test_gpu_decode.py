@@ -74,8 +74,9 @@ def test_embed_bit_exact():
                                            (2560, 8192, 3.0, "bf16")])
 def test_fused_rmsnorm_linear_bit_exact(N, K, scale, out):
     # heph_fp8_linear_rmsnorm (the norm inside the fused M = 1 GEMV) gives
-    # the bits of heph_rmsnorm followed by heph_fp8_linear, leaves the same
-    # codes and scales in the workspaces, and adds the residual alike.
+    # the bits of heph_rmsnorm followed by heph_fp8_linear under the norm
+    # form's launch shape, leaves the same codes and scales in the
+    # workspaces, and adds the residual alike.
     from hephaestus_amd import kernels as HK
     x = rng_bf16(K + N, K, scale)
     g = rng_bf16(8, K, 0.5)
@@ -90,7 +91,7 @@ def test_fused_rmsnorm_linear_bit_exact(N, K, scale, out):
         c1, c2 = res.clone(), res.clone()
         DEC.rmsnorm(xn, xd, gd)
         fn = HK.linear_add_residual_fp8 if resid else HK.linear_fp8
-        fn(c1, xn, wd, sd, q1, s1, 1, N, K)
+        fn(c1, xn, wd, sd, q1, s1, 1, N, K, tune=HK.norm_shape_tune(N, K))
         HK.linear_fp8_rmsnorm(c2, xd, gd, 1e-6, wd, sd, q2, s2, N, K, add_residual=resid)
         assert HK.last_kernel() == "fp8_gemv_rmsnorm_m1"
         torch.cuda.synchronize()
