@@ -95,9 +95,9 @@ int gemv_rows(int M)
 // us (4 slots x 4 waves, 4864 workgroups), down 8.1 against 8.3 (4 x 10),
 // qkv 5.5 against 5.6 (4 x 5), q_proj 4.6 against 4.7 (4 x 5), o_proj
 // unchanged (4 x 8).
-// Otherwise (and for the norm forms) chunk slots: at M <= 2 the fewest
-// (at most 16 / rows per
-// slot) that give >= 600 workgroups (about 2.3 per CU); at 4 and 8 rows
+// Otherwise chunk slots: at M <= 2 the fewest (at most 16 / rows per
+// slot) that give >= 600 workgroups (about 2.3 per CU; the norm forms
+// >= 256); at 4 and 8 rows
 // per slot one (two at 4 rows when K >= 8192), as every workgroup quantizes
 // all M x K activations again and wider workgroups do that less often
 // (MI355X, graph-replayed, fused: M = 8 qkv 7.6 against 9.1 us with two
@@ -117,8 +117,12 @@ void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, in
     const int tiles = N / 16, KC = K / kChunk;
     const bool plain1 = mr == 1 && !norm;
     int k = 1;
+    // the norm forms: enough workgroups for one per CU (each repeats the
+    // norm; MI355X decode step with qkv at 384 workgroups instead of 768:
+    // -17 us per token); else >= 600
+    const int min_wgs = mr == 1 && norm ? 256 : 600;
     if (mr <= 2)
-        while (k < kmax && tiles * k < 600) k *= 2;
+        while (k < kmax && tiles * k < min_wgs) k *= 2;
     else if (mr == 4 && K >= 8192)
         k = 2;
     if (plain1 && k < 4 && KC >= 8) k = 4;

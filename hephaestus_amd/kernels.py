@@ -189,11 +189,11 @@ def norm_shape_tune(n: int, k: int) -> dict:
     """Launch-shape overrides under which linear_fp8 at M = 1 sums in the
     order of the RMSNorm-fused forms (linear_fp8_rmsnorm, linear_fp8_swiglu
     with gamma), as include/hephfp8.h states their shape: the fewest K-chunk
-    slots (<= 8) giving >= 600 workgroups of 16 / slots columns, 4 waves up
+    slots (<= 8) giving >= 256 workgroups of 16 / slots columns, 4 waves up
     to 3 chunk steps, else 8, two-step batches when each wave has two."""
     tiles, kc = n // 16, k // 128
     ks = 1
-    while ks < 8 and tiles * ks < 600:
+    while ks < 8 and tiles * ks < 256:
         ks *= 2
     steps = -(-kc // ks)
     waves = 4 if steps <= 3 else 8

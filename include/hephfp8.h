@@ -121,7 +121,7 @@ int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16,
  * heph_rmsnorm sums it, computed by every workgroup of the fused GEMV
  * before its quantization, so the normalized row is never written. Its
  * launch shape keeps fewer workgroups than heph_fp8_linear's at M = 1 (each
- * repeats the norm): the fewest K-chunk slots (<= 8) giving >= 600
+ * repeats the norm): the fewest K-chunk slots (<= 8) giving >= 256
  * workgroups, 4 waves up to 3 chunk steps, else 8 (two-step batches when
  * each wave has two steps). Bit for bit heph_rmsnorm followed by
  * heph_fp8_linear_with that shape (gemv_ks, gemv_waves, gemv_u); plain
