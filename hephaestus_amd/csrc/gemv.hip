@@ -98,17 +98,18 @@ int gemv_rows(int M)
 // Otherwise chunk slots: at M <= 2 the fewest (at most 16 / rows per
 // slot) that give >= 600 workgroups (about 2.3 per CU; the norm forms
 // >= 256); at 4 and 8 rows
-// per slot one (two at 4 rows when K >= 8192), as every workgroup quantizes
-// all M x K activations again and wider workgroups do that less often
-// (MI355X, graph-replayed, fused: M = 8 qkv 7.6 against 9.1 us with two
-// slots, o_proj 6.3 against 7.6, down 13.3 against 16.5); 16 rows: one.
-// Waves: at M = 1, 8 from 4 steps on (o_proj 4.85 against 5.06 us with 4
-// waves of 2-step batches, q_proj 4.70 against 4.97); at M >= 2, 4 when
-// there are fewer than 8 steps, else 8, and at 9..16 rows 4 up to 24
-// steps (M = 16 qkv 9.9 against 10.9 us); 16 only when forced, for
-// 8 < M <= 16. Steps per batch: at M = 1 two when each wave has exactly
-// 2 steps; at 5..8 rows with K >= 8192 two; else one (wider activation
-// tiles need the registers).
+// per slot one, as every workgroup quantizes all M x K activations again
+// and wider workgroups do that less often (MI355X, graph-replayed, fused:
+// M = 8 qkv 7.6 against 9.1 us with two slots, o_proj 6.3 against 7.6,
+// down 13.3 against 16.5); 16 rows: one.
+// Waves: at M = 1 (norm forms), 8 from 4 steps on (o_proj 4.85 against
+// 5.06 us with 4 waves of 2-step batches, q_proj 4.70 against 4.97); at
+// M >= 2, 4 when there are fewer than 8 steps, else 8; at 4 and 8 rows per
+// slot 10 when K >= 8192, at 4 rows 4 from 1024 workgroups on (below); at 9..16
+// rows 4 up to 24 steps (M = 16 qkv 9.9 against 10.9 us); 16 only when
+// forced, for 8 < M <= 16. Steps per batch: at M = 1 (norm forms) two
+// when each wave has exactly 2 steps; at 3..4 rows with K >= 8192 two;
+// else one (wider activation tiles need the registers).
 void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, int* u,
                 bool norm)
 {
@@ -126,10 +127,20 @@ void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, in
     else if (mr == 4 && K >= 8192)
         k = 2;
     if (plain1 && k < 4 && KC >= 8) k = 4;
+    // 4 and 8 rows per slot with K >= 8192: one slot (10 waves below)
+    const bool long_k = (mr == 4 || mr == 8) && K >= 8192;
+    if (long_k) k = 1;
     const int fk = tune.gemv_ks;
     if (fk) k = fk < kmax ? fk : kmax;
     const int S = (KC + k - 1) / k;
     int w = mr == 1 ? (S <= 3 ? 4 : 8) : (S < 8 ? 4 : 8);
+    // 4 and 8 rows per slot: 10 waves over a long K; at 4 rows 4 waves
+    // where there are >= 1024 workgroups (MI355X, bf16 rows, graph-replayed,
+    // interleaved repeats: M = 4 down 10.8 against 11.5 us, gate_up 12.5
+    // against 13.8; M = 8 down 13.2 against 13.3; M = 8 gate_up unchanged
+    // by 4 waves)
+    if (long_k) w = 10;
+    else if (mr == 4 && (long)tiles * k >= 1024) w = 4;
     if (plain1) {
         // the fewest steps per wave (1, then 2) whose wave count, rounded up
         // to one of 4, 5, 8, 10, fits every workgroup on the CUs at once
@@ -146,10 +157,14 @@ void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, in
     }
     if (mr == 16 && M <= 16 && S <= 24) w = 4;
     const int fw = tune.gemv_waves;
-    if (fw) w = (fw == 16 && (mr != 16 || M > 16)) || ((fw == 5 || fw == 10) && mr != 1) ? 8 : fw;
+    if (fw)
+        w = (fw == 16 && (mr != 16 || M > 16)) || (fw == 5 && mr != 1) ||
+                    (fw == 10 && mr != 1 && mr != 4 && mr != 8)
+                ? 8
+                : fw;
     int uu = 1;
     if (mr == 1 && !plain1 && (S + w - 1) / w == 2) uu = 2;
-    if (mr == 8 && K >= 8192) uu = 2;
+    if (long_k && mr == 4) uu = 2;
     const int fu = tune.gemv_u;
     if (fu) uu = fu;
     if (w == 16) uu = 1;    // two-step batches would not fit 128 VGPRs
@@ -169,6 +184,13 @@ hipError_t launch_fp8_gemv(const Fp8Operands& op, bool fused, hipStream_t stream
     if (op.M == 1) *name = gamma ? "fp8_gemv_rmsnorm_m1" : fused ? "fp8_gemv_fused_m1" : "fp8_gemv_m1";
     else if (op.M <= 16) *name = fused ? "fp8_gemv_fused_m16" : "fp8_gemv_m16";
     else *name = fused ? "fp8_gemv_fused_m32" : "fp8_gemv_m32";
+    if ((mr == 4 || mr == 8) && waves == 10) {
+        if (mr == 4)
+            return u == 2 ? launch_mr<10, 4, 1, 2>(a, fused, ks, stream, t)
+                          : launch_mr<10, 4, 1, 1>(a, fused, ks, stream, t);
+        return u == 2 ? launch_mr<10, 8, 1, 2>(a, fused, ks, stream, t)
+                      : launch_mr<10, 8, 1, 1>(a, fused, ks, stream, t);
+    }
     if (mr == 1 && (waves == 5 || waves == 10)) {
         if (waves == 5)
             return u == 2 ? launch_mr<5, 1, 1, 2>(a, fused, ks, stream, t)

@@ -276,8 +276,9 @@ const char* heph_last_kernel(void);
  * overrides applied to that call only. No counterpart in the reference.
  *   gemv_ks      K-chunk slots per MFMA of the M <= 32 chunk-slot GEMV:
  *                1, 2, 4 or 8 (capped at 16 / rows per slot, i.e. 1 for M > 8)
- *   gemv_waves   its waves per workgroup: 4, 5, 8, 10 or 16 (5 and 10 only
- *                for M = 1, 16 only for 8 < M <= 16; 8 is used otherwise)
+ *   gemv_waves   its waves per workgroup: 4, 5, 8, 10 or 16 (5 only for
+ *                M = 1, 10 for M = 1 and 3 <= M <= 8, 16 only for
+ *                8 < M <= 16; 8 is used otherwise)
  *   gemv_u       its steps per load batch: 1 or 2 (1 with 16 waves)
  *   gemm_bm      tile height of the large-M GEMM: 64, 128, 192, 256; 1 selects
  *                the 128x128 GEMM (otherwise used only when M*K or N*K

@@ -342,14 +342,15 @@ def test_gemv_every_launch_shape(N, K):
 def gemv_shapes(M):
     """Distinct (chunk slots, waves, steps per batch) launch shapes of the
     chunk-slot kernel at M rows: slots are capped at 16 / rows-per-slot,
-    16 waves serve 8 < M <= 16 only and always take 1-step batches."""
+    16 waves serve 8 < M <= 16 only and always take 1-step batches, 10
+    waves 2 < M <= 8."""
     mr = 1 if M == 1 else 2 if M <= 2 else 4 if M <= 4 else 8 if M <= 8 else 16
     kmax = 8 if mr == 1 else 16 // mr
     out = []
     for ks in (1, 2, 4, 8):
         if ks > kmax:
             continue
-        for waves in (4, 8, 16) if 8 < M <= 16 else (4, 8):
+        for waves in (4, 8, 16) if 8 < M <= 16 else (4, 8, 10) if 2 < M <= 8 else (4, 8):
             for u in ((1,) if waves == 16 else (1, 2)):
                 out.append((ks, waves, u))
     return out
