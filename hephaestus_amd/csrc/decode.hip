@@ -168,13 +168,12 @@ __global__ __launch_bounds__(256) void rope_table_kernel(uint16_t* table, int n_
 // hold the rotated pair (bf16 values): y = bf16(gamma * bf16(x * r)) with
 // r = 1/sqrt(mean(x^2) + eps), then re = bf16(bf16(a c) - bf16(b s)),
 // im = bf16(bf16(b c) + bf16(a s)).
-__device__ __forceinline__ void head_norm_rope(float& a, float& b, float g_lo, float g_hi,
-                                               float c, float s, float eps)
+// head_norm_rope after the sum of squares: ss = the wave's fold of
+// a*a + b*b (fma), as wave_sum64 forms it.
+__device__ __forceinline__ void head_finish(float& a, float& b, float g_lo, float g_hi,
+                                            float c, float s, float eps, float ss)
 {
     constexpr int D = 128;
-    float ss = a * a;
-    ss = __builtin_fmaf(b, b, ss);
-    ss = wave_sum64(ss);
     const float r = __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(ss, (float)D) + eps));
     a = round_bf16(g_lo * round_bf16(a * r));
     b = round_bf16(g_hi * round_bf16(b * r));
@@ -182,6 +181,14 @@ __device__ __forceinline__ void head_norm_rope(float& a, float& b, float g_lo, f
     const float im_c = round_bf16(b * c), re_s = round_bf16(a * s);
     a = round_bf16(re_c - im_s);
     b = round_bf16(im_c + re_s);
+}
+
+__device__ __forceinline__ void head_norm_rope(float& a, float& b, float g_lo, float g_hi,
+                                               float c, float s, float eps)
+{
+    float ss = a * a;
+    ss = __builtin_fmaf(b, b, ss);
+    head_finish(a, b, g_lo, g_hi, c, s, eps, wave_sum64(ss));
 }
 
 // One wave per head (D = 128), lane l holding elements l and l + 64. Waves
@@ -329,8 +336,9 @@ struct QkvPrep {
 // have left in memory, with the same arithmetic (head_norm_rope): its G
 // query heads, and in the split holding the new key (the last) that key's
 // k and v rows, quantized into the cache (the values kernel reads v from
-// there). Work items (the G q heads, then k and v) go round-robin to the
-// four waves, every raw load issued before the first reduction; the rotated
+// there). The G q heads and the new key's k go round-robin to the four
+// waves, every raw load issued before the first reduction, a wave's heads
+// folded together; v takes one element per thread; the rotated
 // q heads and the new key's codes meet in LDS after one barrier, and the
 // new key's score uses those codes instead of the cache row loaded at the
 // start. All of it runs while the cache loads are in flight.
@@ -351,32 +359,34 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
         kv[i] = ldg16u(kc + (size_t)min(j0 + 32 * i, n_keys - 1) * row + kh * D + 16 * c);
     float qv[G][16];
     if constexpr (QKV) {
-        // items 0..G-1: q heads kh*G + g; G: the new key's k row; G + 1: its
-        // v row (last split only)
-        constexpr int NI = (G + 2 + 3) / 4;
+        // normalized heads: items 0..G-1 the q heads kh*G + g, item G the
+        // new key's k row (last split only), round-robin over the four
+        // waves; a wave's heads fold their sums of squares together (the
+        // same per-head order as wave_sum64). The new key's v row is
+        // quantized one element per thread.
+        constexpr int NI = (G + 1 + 3) / 4;
         __shared__ __attribute__((aligned(16))) uint16_t qs[G][D];
         __shared__ __attribute__((aligned(16))) uint8_t knew[D];
         const int wave = t >> 6, l = t & 63;
         const bool last = split == n_splits - 1;
-        const int items = last ? G + 2 : G;
+        const int items = last ? G + 1 : G;
         uint32_t rcs = 0;
         if (prep.rope) rcs = reinterpret_cast<const uint32_t*>(prep.rope)[l];
+        float vx = 0.0f;
+        if (last && t < D) vx = f32_of_bf16(prep.qkv[(size_t)(prep.n_heads + n_kv + kh) * D + t]);
         float xa[NI], xb[NI], ga[NI], gb[NI];
 #pragma unroll
         for (int k = 0; k < NI; ++k) {
             const int it = wave + 4 * k;
             xa[k] = xb[k] = ga[k] = gb[k] = 0.0f;
             if (it < items) {
-                const int h = it < G ? kh * G + it
-                                     : prep.n_heads + (it == G ? kh : n_kv + kh);
+                const int h = it < G ? kh * G + it : prep.n_heads + kh;
                 const uint16_t* r = prep.qkv + (size_t)h * D;
+                const uint16_t* gm = it < G ? prep.q_gamma : prep.k_gamma;
                 xa[k] = f32_of_bf16(r[l]);
                 xb[k] = f32_of_bf16(r[l + 64]);
-                if (it <= G) {
-                    const uint16_t* gm = it < G ? prep.q_gamma : prep.k_gamma;
-                    ga[k] = f32_of_bf16(gm[l]);
-                    gb[k] = f32_of_bf16(gm[l + 64]);
-                }
+                ga[k] = f32_of_bf16(gm[l]);
+                gb[k] = f32_of_bf16(gm[l + 64]);
             }
         }
         float cs, sn;
@@ -386,18 +396,19 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
         } else {
             rope_cs(n_keys - 1, l, D, prep.theta, cs, sn);
         }
+        float ss[NI];
+#pragma unroll
+        for (int k = 0; k < NI; ++k) ss[k] = __builtin_fmaf(xb[k], xb[k], xa[k] * xa[k]);
+        for (int h = 32; h > 0; h >>= 1) {
+#pragma unroll
+            for (int k = 0; k < NI; ++k) ss[k] += __shfl_down(ss[k], h, 64);
+        }
 #pragma unroll
         for (int k = 0; k < NI; ++k) {
             const int it = wave + 4 * k;
             if (it >= items) break;
             float a = xa[k], b = xb[k];
-            if (it == G + 1) {                  // v: quantize only
-                const float inv = prep.kv_inv[n_kv + kh];
-                prep.v_slot[kh * D + l] = (uint8_t)e4m3_sat(a * inv);
-                prep.v_slot[kh * D + l + 64] = (uint8_t)e4m3_sat(b * inv);
-                continue;
-            }
-            head_norm_rope(a, b, ga[k], gb[k], cs, sn, prep.eps);
+            head_finish(a, b, ga[k], gb[k], cs, sn, prep.eps, __shfl(ss[k], 0, 64));
             if (it < G) {
                 qs[it][l] = f32_to_bf16(a);
                 qs[it][l + 64] = f32_to_bf16(b);
@@ -410,6 +421,7 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
                 knew[l + 64] = hi;
             }
         }
+        if (last && t < D) prep.v_slot[kh * D + t] = (uint8_t)e4m3_sat(vx * prep.kv_inv[n_kv + kh]);
         __syncthreads();
 #pragma unroll
         for (int g = 0; g < G; ++g) {
