@@ -649,15 +649,26 @@ __global__ __launch_bounds__(128) void attn_combine_kernel(uint16_t* out, const 
     const AttnWs w = attn_ws(const_cast<float*>(ws), n_heads, n_keys, n_splits);
     const float* p = w.partial + (size_t)h * n_splits * 128 + d;
     float v = 0.0f;
-    int s = 0;
-    for (; s + 8 <= n_splits; s += 8) {      // eight loads in flight, summed in order
-        float x[8];
+    if (n_splits <= 64) {
+        // up to 8192 keys: every split's partial in flight at once (one
+        // round trip), then summed in split order
+        float x[64];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) x[u] = p[(s + u) * 128];
+        for (int u = 0; u < 64; ++u) x[u] = u < n_splits ? p[u * 128] : 0.0f;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v += x[u];
+        for (int u = 0; u < 64; ++u)
+            if (u < n_splits) v += x[u];
+    } else {
+        int s = 0;
+        for (; s + 8 <= n_splits; s += 8) {  // eight loads in flight, summed in order
+            float x[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) x[u] = p[(s + u) * 128];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v += x[u];
+        }
+        for (; s < n_splits; ++s) v += p[s * 128];
     }
-    for (; s < n_splits; ++s) v += p[s * 128];
     out[(size_t)h * 128 + d] = f32_to_bf16(v * kv_scale[n_kv + h / (n_heads / n_kv)]);
 }
 
