@@ -85,7 +85,7 @@ SIGNATURES = {
     "heph_attention_fp8kv": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "heph_rope_table_bf16": (_i, [_vp, _i, _i, ctypes.c_double, _vp]),
     "heph_attention_qkv_fp8kv": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i,
-                                      _i, ctypes.c_double, ctypes.c_float, _vp, _sz, _vp]),
+                                      _i, _i, ctypes.c_double, ctypes.c_float, _vp, _sz, _vp]),
     "heph_silu_mul": (_i, [_vp, _vp, _vp, _i, _vp]),
     "heph_argmax_ws_bytes": (_sz, [_i]),
     "heph_argmax_bf16": (_i, [_vp, _vp, _i, _vp, _sz, _vp]),

@@ -873,9 +873,9 @@ int heph_attention_fp8kv(void* out_bf16, const void* q_bf16, const uint8_t* k_ca
 int heph_attention_qkv_fp8kv(void* out_bf16, const void* qkv_bf16, const void* q_gamma,
                              const void* k_gamma, uint8_t* k_cache, uint8_t* v_cache,
                              const float* kv_scale, const float* kv_inv_scale,
-                             const void* rope_table, int n_heads, int n_kv_heads, int head_dim,
-                             int pos, double theta, float eps, void* ws, size_t ws_bytes,
-                             void* stream)
+                             const void* rope_table, int n_rope_pos, int n_heads,
+                             int n_kv_heads, int head_dim, int pos, double theta, float eps,
+                             void* ws, size_t ws_bytes, void* stream)
 {
     if (!out_bf16 || !qkv_bf16 || !q_gamma || !k_gamma || !k_cache || !v_cache || !kv_scale ||
         !kv_inv_scale || !ws)
@@ -883,6 +883,8 @@ int heph_attention_qkv_fp8kv(void* out_bf16, const void* qkv_bf16, const void* q
     if (head_dim != 128 || n_kv_heads < 1 || n_heads < n_kv_heads || n_heads % n_kv_heads ||
         pos < 0 || pos >= HEPH_ATTN_MAX_KEYS)
         return HEPH_ERR_SHAPE;
+    // the table's row pos is read on the device: it must exist
+    if (rope_table && pos >= n_rope_pos) return HEPH_ERR_SHAPE;
     const int G = n_heads / n_kv_heads;
     if (G != 1 && G != 2 && G != 4 && G != 8) return HEPH_ERR_SHAPE;
     const int n_keys = pos + 1;

@@ -86,17 +86,18 @@ int heph_rope_table_bf16(void* table_bf16, int n_pos, int head_dim, double theta
  * bytes, in the attention's three launches (the scores kernel prepares q
  * and the new key's k and v itself). q in qkv_bf16 is left as it was (not
  * rotated in place). ws: heph_attention_ws_bytes(n_heads, pos + 1) bytes.
- * rope_table: a heph_rope_table_bf16 table with more than pos rows (for
- * this theta and head_dim), or NULL to compute pos's cos/sin in the call.
+ * rope_table: a heph_rope_table_bf16 table of n_rope_pos rows (for this
+ * theta and head_dim), or NULL to compute pos's cos/sin in the call
+ * (n_rope_pos is then ignored); HEPH_ERR_SHAPE when pos >= n_rope_pos.
  * Replaces the q/k norms, RoPE, K/V write and attention call of
  * src/hephaestus/forward.mojo:474-520 (kernels.mojo:709-796, :923-1035).
  */
 int heph_attention_qkv_fp8kv(void* out_bf16, const void* qkv_bf16, const void* q_gamma,
                              const void* k_gamma, uint8_t* k_cache, uint8_t* v_cache,
                              const float* kv_scale, const float* kv_inv_scale,
-                             const void* rope_table, int n_heads, int n_kv_heads, int head_dim,
-                             int pos, double theta, float eps, void* ws, size_t ws_bytes,
-                             void* stream);
+                             const void* rope_table, int n_rope_pos, int n_heads,
+                             int n_kv_heads, int head_dim, int pos, double theta, float eps,
+                             void* ws, size_t ws_bytes, void* stream);
 
 /*
  * out = bf16(bf16(g / (1 + exp(-g))) * up). Replaces silu_mul

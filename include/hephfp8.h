@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define HEPH_ABI_VERSION 3
+#define HEPH_ABI_VERSION 4
 
 /* status codes */
 #define HEPH_OK                 0

@@ -26,7 +26,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_version_and_strerror(lib):
-    assert lib.heph_abi_version() == 3
+    assert lib.heph_abi_version() == 4
     for code in range(0, -12, -1):
         msg = L.strerror(code)
         assert msg and msg != "unknown status", code
@@ -220,24 +220,25 @@ def test_decode_ops_reject(lib):
     # over pos + 1 keys
     qa = lib.heph_attention_qkv_fp8kv
     args = [FAKE] * 9
-    assert qa(*args, 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) in \
+    NR = 1 << 20          # rows of the RoPE table
+    assert qa(*args, NR, 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) in \
         (L.HEPH_ERR_DEVICE, L.HEPH_OK)
-    assert qa(*args[:7], None, FAKE, 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) == \
+    assert qa(*args[:7], None, FAKE, NR, 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) == \
         L.HEPH_ERR_NULL
     # no table: the call computes the cos/sin of pos itself
-    assert qa(*args[:8], None, 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) in \
+    assert qa(*args[:8], None, 0, 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) in \
         (L.HEPH_ERR_DEVICE, L.HEPH_OK)
-    assert qa(*args[:8], FAKE + 2, 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) == \
+    assert qa(*args[:8], FAKE + 2, NR, 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) == \
         L.HEPH_ERR_ALIGN
-    assert qa(*args, 32, 8, 128, 4096, 1e6, 1e-6, None, ws, None) == L.HEPH_ERR_NULL
-    assert qa(*args, 32, 8, 64, 4096, 1e6, 1e-6, FAKE, ws, None) == L.HEPH_ERR_SHAPE
-    assert qa(*args, 24, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) == L.HEPH_ERR_SHAPE
-    assert qa(*args, 32, 2, 128, 4096, 1e6, 1e-6, FAKE, ws, None) == L.HEPH_ERR_SHAPE
-    assert qa(*args, 32, 8, 128, -1, 1e6, 1e-6, FAKE, ws, None) == L.HEPH_ERR_SHAPE
-    assert qa(*args, 32, 8, 128, L.ATTN_MAX_KEYS, 1e6, 1e-6, FAKE, 1 << 40, None) == \
+    assert qa(*args, NR, 32, 8, 128, 4096, 1e6, 1e-6, None, ws, None) == L.HEPH_ERR_NULL
+    assert qa(*args, NR, 32, 8, 64, 4096, 1e6, 1e-6, FAKE, ws, None) == L.HEPH_ERR_SHAPE
+    assert qa(*args, NR, 24, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) == L.HEPH_ERR_SHAPE
+    assert qa(*args, NR, 32, 2, 128, 4096, 1e6, 1e-6, FAKE, ws, None) == L.HEPH_ERR_SHAPE
+    assert qa(*args, NR, 32, 8, 128, -1, 1e6, 1e-6, FAKE, ws, None) == L.HEPH_ERR_SHAPE
+    assert qa(*args, NR, 32, 8, 128, L.ATTN_MAX_KEYS, 1e6, 1e-6, FAKE, 1 << 40, None) == \
         L.HEPH_ERR_SHAPE
-    assert qa(*args, 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws - 4, None) == L.HEPH_ERR_WORKSPACE
-    assert qa(*args[:4], ODD, *args[5:], 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) == \
+    assert qa(*args, NR, 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws - 4, None) == L.HEPH_ERR_WORKSPACE
+    assert qa(*args[:4], ODD, *args[5:], NR, 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) == \
         L.HEPH_ERR_ALIGN
     rt = lib.heph_rope_table_bf16
     assert rt(None, 4097, 128, 1e6, None) == L.HEPH_ERR_NULL
@@ -253,6 +254,10 @@ def test_decode_ops_reject(lib):
     assert lib.heph_argmax_bf16(FAKE, FAKE, 10, None, aw, None) == L.HEPH_ERR_NULL
     assert lib.heph_argmax_bf16(FAKE, FAKE, 0, FAKE, aw, None) == L.HEPH_ERR_SHAPE
     assert lib.heph_argmax_bf16(FAKE, FAKE, 151936, FAKE, aw - 8, None) == L.HEPH_ERR_WORKSPACE
+    # a table without row pos is refused before anything reads it
+    assert qa(*args, 4096, 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) == L.HEPH_ERR_SHAPE
+    assert qa(*args, 4097, 32, 8, 128, 4096, 1e6, 1e-6, FAKE, ws, None) in \
+        (L.HEPH_ERR_DEVICE, L.HEPH_OK)
 
 
 def test_noalloc_limits(lib):
