@@ -100,8 +100,8 @@ def attention_qkv_fp8kv(out, qkv, q_gamma, k_gamma, k_cache, v_cache, kv_scale, 
         raise ValueError(f"rope table of {rope.shape[0]} rows has no row {pos}")
     _call("heph_attention_qkv_fp8kv", _ptr(out), _ptr(qkv), _ptr(q_gamma), _ptr(k_gamma),
           _ptr(k_cache), _ptr(v_cache), _ptr(kv_scale), _ptr(kv_inv),
-          None if rope is None else _ptr(rope), n_heads, n_kv, 128, pos, theta, eps, _ptr(ws),
-          ws.numel(), _stream())
+          None if rope is None else _ptr(rope), 0 if rope is None else rope.shape[0],
+          n_heads, n_kv, 128, pos, theta, eps, _ptr(ws), ws.numel(), _stream())
 
 
 def silu_mul(out, gate, up, n: int) -> None:
@@ -122,31 +122,64 @@ def argmax_bf16(out_idx, logits, ws: torch.Tensor | None = None) -> None:
 
 # ---------------------------------------------------------------- weights ----
 
-def _rand_fp8(g: torch.Generator, N: int, K: int, device) -> Fp8Weight:
-    w = (torch.randn(N, K, generator=g, device=device) * 0.02).to(torch.bfloat16)
+def _rand_fp8(g: torch.Generator, N: int, K: int, device, std: float = 0.02) -> Fp8Weight:
+    w = (torch.randn(N, K, generator=g, device=device) * std).to(torch.bfloat16)
     q, s = quantize_weight_fp8(w)
     return Fp8Weight(q, s, True)
 
 
-def _rand_gamma(g: torch.Generator, n: int, device) -> torch.Tensor:
-    return (1.0 + 0.1 * torch.randn(n, generator=g, device=device)).to(torch.bfloat16)
+def _rand_gamma(g: torch.Generator, n: int, device, centre: float = 1.0,
+                std: float = 0.1) -> torch.Tensor:
+    return (centre + std * torch.randn(n, generator=g, device=device)).to(torch.bfloat16)
 
 
-def random_init(cfg: Qwen3Config, seed: int = 0, device="cuda") -> Qwen3Fp8Weights:
+# Std of the residual-branch output projections (o_proj, down_proj) relative
+# to the other linears in conditioned_init: with it the 36 branches make up
+# ~1 % of the final residual stream of the configs[4] model.
+CONDITIONED_BRANCH_SCALE = 3e-5
+
+
+def random_init(cfg: Qwen3Config, seed: int = 0, device="cuda",
+                branch_scale: float = 1.0, final_gamma_centre: float = 1.0,
+                final_gamma_std: float = 0.1) -> Qwen3Fp8Weights:
     """Random-init Qwen3 weights: every linear ~N(0, 0.02) quantized per
-    128x128 block on the GPU (tied FP8 embedding), norm gammas 1 + 0.1 N(0,1)."""
+    128x128 block on the GPU (tied FP8 embedding), norm gammas 1 + 0.1 N(0,1).
+    branch_scale multiplies the std of o_proj and down_proj (the projections
+    that write into the residual stream); the final norm's gamma is
+    final_gamma_centre + final_gamma_std * N(0,1)."""
     g = torch.Generator(device=device).manual_seed(seed)
     H, I = cfg.hidden, cfg.inter
-    out = Qwen3Fp8Weights(cfg, _rand_fp8(g, cfg.vocab, H, device), _rand_gamma(g, H, device))
+    bstd = 0.02 * branch_scale
+    out = Qwen3Fp8Weights(cfg, _rand_fp8(g, cfg.vocab, H, device),
+                          _rand_gamma(g, H, device, final_gamma_centre, final_gamma_std))
     for _ in range(cfg.n_layers):
         out.layers.append(Qwen3Layer(
             attn_norm=_rand_gamma(g, H, device), q_norm=_rand_gamma(g, cfg.head_dim, device),
             k_norm=_rand_gamma(g, cfg.head_dim, device), ffn_norm=_rand_gamma(g, H, device),
             qkv=_rand_fp8(g, cfg.q_out + 2 * cfg.kv_out, H, device),
-            o=_rand_fp8(g, H, cfg.q_out, device),
+            o=_rand_fp8(g, H, cfg.q_out, device, bstd),
             gate_up=_rand_fp8(g, 2 * I, H, device),
-            down=_rand_fp8(g, H, I, device)))
+            down=_rand_fp8(g, H, I, device, bstd)))
     return out
+
+
+def conditioned_init(cfg: Qwen3Config, seed: int = 0, device="cuda") -> Qwen3Fp8Weights:
+    """The random init the end-to-end argmax check runs on.
+
+    With every linear ~N(0, 0.02) the residual stream is made of the layers'
+    branch outputs (~1 per element against 0.02 for the embedding), each
+    layer re-normalizes it, and a W8A8 step is chaotic: two correct
+    implementations whose fp32 sums differ in the last bit flip E4M3 codes
+    at rounding boundaries, and after 36 layers their logits differ by a
+    third of their spread, far more than the top-2 gap of 151936 random
+    logits (~1/5 of it). Here o_proj and down_proj are drawn with
+    CONDITIONED_BRANCH_SCALE times that std, so the embedding carries the
+    stream and the branches stay a small, bounded share of it; the final
+    norm's gamma is N(0, 1) (zero mean), since with gamma near 1 the tied
+    lm_head would return the input token itself by a margin of ~50
+    standard deviations."""
+    return random_init(cfg, seed, device, branch_scale=CONDITIONED_BRANCH_SCALE,
+                       final_gamma_centre=0.0, final_gamma_std=1.0)
 
 
 # --------------------------------------------------------------- KV cache ----

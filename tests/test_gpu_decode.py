@@ -9,9 +9,10 @@ identical, the rest within one bf16 step. The FP8 linears are within the
 linear path's tolerance (MFMA sums are not fp32-exact). End to end, every
 op of every layer is recomputed by the oracle from the GPU's own inputs
 and held to those bars, and the argmax is compared on identical logits.
-The free-running step must give the oracle's token unless the oracle's own
-top-2 gap is below its measured sensitivity (a named near-tie exception,
-recorded with its numbers under gpurun_out/test_records/).
+Teacher-forced over many positions, the GPU's greedy token must equal the
+oracle's at >= 95 % of the positions that are not bf16 ties, with most
+positions decidable; the same gate must fail against an oracle with a
+planted mistake. Observations are recorded under gpurun_out/test_records/.
 """
 import json
 import os
@@ -279,13 +280,13 @@ def test_argmax_bit_exact_and_ties():
 
 # ------------------------------------------------------------- end to end ----
 #
-# A random-init W8A8 stack is chaotic: one bf16 ulp added to three embedding
-# elements moves the oracle's own logits by ~8% of their range (E4M3 codes
-# flip at rounding boundaries and the layers amplify it). So the strong
-# check is op by op: every op of every layer is recomputed by the oracle
-# from the GPU's own inputs and must match to that op's bar; the final
-# argmax is then compared on identical logits. The free-running step is
-# checked against the oracle's measured sensitivity.
+# With every linear ~N(0, 0.02) a W8A8 stack is chaotic: one bf16 ulp added
+# to three embedding elements moves the oracle's own logits by ~8% of their
+# range (E4M3 codes flip at rounding boundaries and the layers amplify it).
+# So the precise check is op by op, on that init: every op of every layer
+# is recomputed by the oracle from the GPU's own inputs and must match to
+# that op's bar; the final argmax is then compared on identical logits. The
+# teacher-forced argmax gate runs on decode.conditioned_init.
 
 EXACT = {"embed", "attn_norm", "q_rope", "k_codes", "v_codes", "ffn_norm", "final_norm",
          "argmax"}
@@ -400,44 +401,138 @@ def record(name: str, data: dict) -> None:
     warnings.warn(f"{name}: " + json.dumps(data, sort_keys=True))
 
 
-def free_running(cfg, ctx, token, seed, name):
-    """The north star's end-to-end check: the GPU's free-running greedy token
-    must equal the oracle's. The one named exception is a near-tie the
-    oracle itself cannot resolve: its bf16 top-2 gap below its own measured
-    sensitivity (the largest logit change when one embedding block scale
-    moves by one bf16 step, 2^-8, i.e. 128 inputs by at most one bf16 step
-    each). Then the GPU's token must still be one the oracle ranks within
-    that sensitivity of its top logit. The observations are recorded
-    either way."""
-    w, kv = setup_model(cfg, ctx, seed)
-    kvh = DEC.host_kv(kv)
+# The north star's end-to-end check, in the reference's protocol
+# (bench/1b-fp8-wmma-decode.md:15-25): teacher-forced decode, both sides fed
+# the same token at every position (a seeded token stream), each side
+# appending its own K/V rows; the GPU's greedy token must equal the oracle's
+# at >= 95 % of the positions that are not ties. A tie is fixed by bf16
+# rounding alone: the oracle's top-2 f32 gap below one bf16 ulp of its top
+# logit (the argmax compares bf16-rounded logits, kernels.mojo:1424-1428).
+# The model is decode.conditioned_init, on which W8A8 rounding noise stays
+# below the top-2 gaps; most positions (at least 60 %) must be decidable
+# (random logits put ~14 % of top-2 gaps under one bf16 ulp).
+TF_MIN_MATCH = 0.95
+TF_MIN_DECIDABLE = 0.60
+
+
+def token_stream(vocab: int, n: int, seed: int) -> list[int]:
+    return [int(t) for t in np.random.default_rng(seed).integers(0, vocab, n)]
+
+
+def bf16_ulp(v: float) -> float:
+    return 2.0 ** (np.floor(np.log2(abs(v))) - 7) if v != 0 else 2.0 ** -133
+
+
+def top2(c):
+    o = np.argsort(-c, kind="stable")[:2]
+    return int(o[0]), int(o[1]), float(c[o[0]] - c[o[1]])
+
+
+def setup_conditioned(cfg, ctx, n_pos, seed):
+    w = DEC.conditioned_init(cfg, seed=seed)
+    kv = DEC.KVCache(cfg, ctx + n_pos)
+    kv.fill_synthetic(ctx, seed=seed + 1)
+    return w, kv
+
+
+def gpu_teacher_forced(w, kv, ctx, toks):
+    """GPU argmax and f32 logits at positions ctx, ctx + 1, ... fed toks."""
     dec_ = DEC.Qwen3Decoder(w, kv)
-    g_idx = int(dec_.step(token, ctx).item())
-    g = dec_.logits[0].cpu().numpy().astype(np.float64)
+    out = []
+    for p, t in enumerate(toks):
+        a = int(dec_.step(t, ctx + p).item())
+        out.append((a, dec_.logits[0].cpu().numpy().astype(np.float64)))
+    return out
+
+
+def oracle_gate(gpu, model, kvh, ctx, toks, plant=None):
+    """Run the oracle teacher-forced over toks (its own copy of the cache),
+    model_for(position, token) = plant(model, token) when a mistake is
+    planted; compare with the GPU's tokens. Returns (passes, summary,
+    per-position rows)."""
+    kvc = {k: v.copy() for k, v in kvh.items()}
+    rows = []
+    for p, t in enumerate(toks):
+        m = plant(model, t) if plant is not None else model
+        c, ci = O.decode_step(m, kvc, t, ctx + p)
+        c = c.astype(np.float64)
+        i0, i1, gap = top2(c)
+        g_idx, g = gpu[p]
+        gi0, gi1, _ = top2(g)
+        tie = gap < bf16_ulp(c[i0])
+        rows.append({"pos": ctx + p, "token": t, "oracle": ci, "gpu": g_idx,
+                     "match": g_idx == ci, "tie": bool(tie), "oracle_top2_gap": round(gap, 6),
+                     "bf16_ulp": bf16_ulp(c[i0]),
+                     # how far the GPU moves the oracle's top-2 difference
+                     "gpu_gap_shift": round(float((g[i0] - g[i1]) - gap), 6),
+                     "gpu_vs_oracle_max_abs": float(np.abs(g - c).max())})
+    non_ties = [r for r in rows if not r["tie"]]
+    rate = sum(r["match"] for r in non_ties) / max(len(non_ties), 1)
+    decidable = len(non_ties) / len(rows)
+    summary = {"positions": len(rows), "non_ties": len(non_ties),
+               "matches_non_ties": sum(r["match"] for r in non_ties),
+               "match_rate_non_ties": rate, "decidable": decidable,
+               "matches_all": sum(r["match"] for r in rows)}
+    return rate >= TF_MIN_MATCH and decidable >= TF_MIN_DECIDABLE, summary, rows
+
+
+def teacher_forced(cfg, ctx, n_pos, seed, name):
+    w, kv = setup_conditioned(cfg, ctx, n_pos, seed)
+    kvh = DEC.host_kv(kv)
+    toks = token_stream(cfg.vocab, n_pos, seed + 7)
+    t0 = time.time()
+    gpu = gpu_teacher_forced(w, kv, ctx, toks)
+    ok, summary, rows = oracle_gate(gpu, DEC.host_model(w), kvh, ctx, toks)
+    summary.update(layers=cfg.n_layers, context=ctx, seed=seed, seconds=round(time.time() - t0, 1))
+    record(name, {"summary": summary, "positions": rows})
+    print(f"{name}: {summary}", flush=True)
+    assert ok, summary
+
+
+def _with_embed_scale(model, factor_of):
+    m = dict(model)
+    m["embed_scale"] = model["embed_scale"].copy()
+    factor_of(m["embed_scale"])
+    return m
+
+
+def controls(cfg, ctx, seed, name):
+    """The gate against mistakes planted in the oracle, on the CPU: it must
+    fail for a weight-scale block off by 2x and for a layer's down_proj
+    scales used inverted (weight_scale for weight_scale_inv), and must pass
+    for a one-ulp change of one embedding scale block (the perturbation that
+    makes the N(0, 0.02) init chaotic)."""
+    n_pos = 16
+    w, kv = setup_conditioned(cfg, ctx, n_pos, seed)
+    kvh = DEC.host_kv(kv)
     model = DEC.host_model(w)
-    c, c_idx = O.decode_step(model, {k: v.copy() for k, v in kvh.items()}, token, ctx)
-    m2 = dict(model)
-    m2["embed_scale"] = model["embed_scale"].copy()
-    m2["embed_scale"][token // 128, 0] *= np.float32(1 + 2.0 ** -8)
-    p, p_idx = O.decode_step(m2, {k: v.copy() for k, v in kvh.items()}, token, ctx)
-    c = c.astype(np.float64)
-    err, sens = np.abs(g - c).max(), np.abs(p.astype(np.float64) - c).max()
-    cb = f32(bf16_np(c))
-    order = np.argsort(-cb, kind="stable")
-    gap = float(cb[order[0]] - cb[order[1]])
-    near_tie = gap < sens
-    obs = {"argmax_gpu": g_idx, "argmax_oracle": c_idx, "argmax_oracle_perturbed": int(p_idx),
-           "oracle_top2_gap": gap, "oracle_sensitivity": float(sens),
-           "gpu_vs_oracle_max_abs": float(err), "max_abs_logit": float(np.abs(c).max()),
-           "match": g_idx == c_idx, "named_exception_near_tie": bool(near_tie and g_idx != c_idx),
-           "gpu_rank_in_oracle": int(np.flatnonzero(order == g_idx)[0]),
-           "oracle_logit_gap_to_gpu_pick": float(cb[c_idx] - cb[g_idx]),
-           "layers": cfg.n_layers, "context": ctx, "token": token, "seed": seed}
-    record(name, obs)
-    if not near_tie:
-        assert g_idx == c_idx, obs
-    else:
-        assert g_idx == c_idx or cb[c_idx] - cb[g_idx] <= sens, obs
+    toks = token_stream(cfg.vocab, n_pos, seed + 7)
+    gpu = gpu_teacher_forced(w, kv, ctx, toks)
+
+    def one_ulp(m, t):
+        return _with_embed_scale(m, lambda s: s.__setitem__((t // 128, 0),
+                                                             s[t // 128, 0] * np.float32(1 + 2.0 ** -8)))
+
+    def block_2x(m, t):
+        # the one block scale (fed token's row block, first K block) doubled
+        return _with_embed_scale(m, lambda s: s.__setitem__((t // 128, 0), s[t // 128, 0] * 2))
+
+    inv = dict(model)
+    inv["layers"] = list(model["layers"])
+    l0 = dict(model["layers"][0])
+    l0["down_scale"] = (np.float32(1.0) / model["layers"][0]["down_scale"]).astype(np.float32)
+    inv["layers"][0] = l0
+    out = {}
+    for label, plant, want in (("one_ulp_embed_scale", one_ulp, True),
+                               ("embed_scale_block_x2", block_2x, False)):
+        ok, summary, rows = oracle_gate(gpu, model, kvh, ctx, toks, plant)
+        out[label] = {"passes": ok, "expected": want, **summary}
+    ok, summary, rows = oracle_gate(gpu[:8], inv, kvh, ctx, toks[:8])
+    out["layer0_down_scale_inverted"] = {"passes": ok, "expected": False, **summary}
+    record(name, out)
+    print(f"{name}: {out}", flush=True)
+    for label, r in out.items():
+        assert r["passes"] == r["expected"], (label, r)
 
 
 SMALL = Qwen3Config(vocab=4096, hidden=512, n_layers=3, n_heads=4, n_kv_heads=2, head_dim=128,
@@ -514,8 +609,8 @@ def test_linear_fp8_swiglu_matches_two_ops(I, K, gamma, block):
     assert torch.equal(q1, q2) and torch.equal(s1, s2)
 
 
-def test_decode_small_model_free_running():
-    free_running(SMALL, ctx=300, token=1234, seed=11, name="small_free_running_argmax")
+def test_decode_small_model_teacher_forced():
+    teacher_forced(SMALL, ctx=300, n_pos=32, seed=11, name="small_teacher_forced_argmax")
 
 
 def test_decode_qwen3_4b_config4_op_by_op():
@@ -526,5 +621,10 @@ def test_decode_qwen3_4b_config4_op_by_op():
     op_by_op(Qwen3Config(), ctx=4096, token=12345, seed=4)
 
 
-def test_decode_qwen3_4b_config4_free_running():
-    free_running(Qwen3Config(), ctx=4096, token=12345, seed=4, name="config4_free_running_argmax")
+def test_decode_qwen3_4b_config4_teacher_forced():
+    # configs[4] on decode.conditioned_init: 48 positions from 4096
+    teacher_forced(Qwen3Config(), ctx=4096, n_pos=48, seed=4, name="config4_teacher_forced_argmax")
+
+
+def test_decode_qwen3_4b_config4_gate_controls():
+    controls(Qwen3Config(), ctx=4096, seed=4, name="config4_teacher_forced_controls")
