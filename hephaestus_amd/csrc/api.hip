@@ -135,6 +135,8 @@ int take_overrides(const heph_launch_overrides* ov, Tuning* t)
     const int wt = ov->wide_tiles, ww = ov->wide_waves;
     if (wt != -1 && wt != 0 && wt != 1 && wt != 2 && wt != 4) return HEPH_ERR_FLAGS;
     if (ww != 0 && ww != 4 && ww != 8 && ww != 16) return HEPH_ERR_FLAGS;
+    if (ov->split_spin_limit < -1) return HEPH_ERR_FLAGS;
+    t->split_spin_limit = ov->split_spin_limit;
     t->wide_tiles = wt;
     t->wide_waves = ww;
     t->gemv_ks = ks;

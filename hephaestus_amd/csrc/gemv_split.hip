@@ -39,12 +39,19 @@
 //     (both written through to the coherent level, the flag after the
 //     partials have completed). Split S-1 holds the tile's highest workgroup index,
 //     so it is dispatched after every workgroup it waits for: it polls the
-//     S-1 flags (bounded; on expiry the tile's outputs become NaN), sums
-//     the partials in split order with its own sum last (the order of the
-//     large-M GEMM's reduction kernel), adds the residual, stores, and
-//     clears the flags. Flags left by earlier calls hold other epochs; a
-//     replayed HIP graph repeats one epoch, and the clearing puts the flags
-//     back into the waiting state between replays.
+//     S-1 flags, sums the partials in split order with its own sum last
+//     (the order of the large-M GEMM's reduction kernel), adds the
+//     residual, stores, and clears the flags. Flags left by earlier calls
+//     hold other epochs; a replayed HIP graph repeats one epoch, and the
+//     clearing puts the flags back into the waiting state between replays.
+//     The wait is bounded. When it gives up, the last split swaps a
+//     give-up mark into each flag it did not see (a flag that arrived in
+//     between is taken back to the waiting state instead), writes NaN to
+//     the tile, and counts the tile in the status word at the end of the
+//     caller's workspace; a split that later finds the give-up mark in its
+//     flag's place puts the flag back to the waiting state. So when the
+//     launch ends every flag is waiting again: no later call, and no graph
+//     replay of an earlier epoch, can take a stale flag for its own.
 
 #include <atomic>
 #include <chrono>
@@ -68,6 +75,8 @@ constexpr int kSpinLimit = 1 << 18;
 // the in-launch sum saved ~2 us at 3 splits (qkv) and lost 1-2 us at 4 and
 // 10 (o_proj, down), where one workgroup per tile reads all the partials.
 constexpr int kInLaunchMaxSplits = 3;
+// A flag whose waiting split gave up (never an epoch: next_epoch skips it).
+constexpr uint64_t kSplitGaveUp = 0xB5AD4ECEDA1CE2A9ull;
 }  // namespace
 
 // Max over each aligned run of 8 lanes (unsigned), left in all 8.
@@ -127,6 +136,13 @@ __device__ __forceinline__ void wait_vmem()
 __device__ __forceinline__ uint64_t* split_flags(const Fp8Operands& op, int S)
 {
     return reinterpret_cast<uint64_t*>(op.part + (size_t)(S - 1) * op.M * op.N);
+}
+// Count of tiles whose wait gave up: the last 8-byte-aligned word of the
+// scratch (HEPH_SPLIT_STATUS_OFFSET of the caller's q_ws_bytes).
+__device__ __forceinline__ uint64_t* split_status(const Fp8Operands& op)
+{
+    return reinterpret_cast<uint64_t*>(reinterpret_cast<uint8_t*>(op.part) +
+                                       ((op.part_bytes - 8) & ~(size_t)7));
 }
 
 // MT: 16-row tiles (1: M <= 16, 2: M <= 32). SM: 0 = 128x128 weight
@@ -281,34 +297,53 @@ __global__ __launch_bounds__(256) void fp8_gemv_split_kernel(Fp8Operands op)
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         wait_vmem();
         __syncthreads();
-        if (tid == 0)
-            __hip_atomic_store(split_flags(op, S) + (size_t)split * tiles_n + tn, op.epoch,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) {
+            uint64_t* f = split_flags(op, S) + (size_t)split * tiles_n + tn;
+            // the tile's last split gave up on this flag: back to waiting
+            if (__hip_atomic_exchange(f, op.epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) ==
+                kSplitGaveUp)
+                __hip_atomic_store(f, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         return;
     }
 
     // 6. the last split (or the only one): wait for the other splits of the
-    //    tile (lanes of wave 0 poll one flag each), then sum in split order
+    //    tile (lane sp of wave 0 polls split sp's flag; S - 1 <= 2), then
+    //    sum in split order
+    static_assert(kInLaunchMaxSplits - 1 <= 64, "one flag per lane of wave 0");
     bool ok = true;
+    bool got = false;   // lane sp of wave 0: split sp's flag came
     if (S > 1) {
         uint64_t* flags = split_flags(op, S) + tn;
         if (wave == 0) {
             bool seen = true;
-            for (int sp = lane; sp < S - 1; sp += 64) {
-                int spins = 0;
-                while (__hip_atomic_load(flags + (size_t)sp * tiles_n, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT) != op.epoch) {
-                    if (++spins == kSpinLimit) {
-                        seen = false;
+            if (lane < S - 1) {
+                uint64_t* f = flags + (size_t)lane * tiles_n;
+                const int limit = op.tune.split_spin_limit ? op.tune.split_spin_limit : kSpinLimit;
+                for (int spins = 0; limit > 0 && spins < limit; ++spins) {
+                    if (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                        op.epoch) {
+                        got = true;
                         break;
                     }
                     __builtin_amdgcn_s_sleep(2);
                 }
+                if (!got) {
+                    // give up: leave the mark for the late split, or take
+                    // back a flag that arrived meanwhile; the tile is NaN
+                    if (__hip_atomic_exchange(f, kSplitGaveUp, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT) == op.epoch)
+                        __hip_atomic_store(f, (uint64_t)0, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                    seen = false;
+                }
             }
-            wait_vmem();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-            const bool all = __builtin_amdgcn_ballot_w64(!seen) == 0;
-            if (lane == 0) tile_ok = all;
+            const bool any_missing = __builtin_amdgcn_ballot_w64(!seen) != 0;
+            if (any_missing && lane == 0)
+                __hip_atomic_fetch_add(split_status(op), (uint64_t)1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            if (lane == 0) tile_ok = !any_missing;
         }
         __syncthreads();
         ok = tile_ok;
@@ -377,13 +412,11 @@ __global__ __launch_bounds__(256) void fp8_gemv_split_kernel(Fp8Operands op)
             }
         }
     }
-    // the flags back to the waiting state (a flag that never came is left)
-    if (S > 1 && wave == 0 && ok) {
-        uint64_t* flags = split_flags(op, S) + tn;
-        for (int sp = lane; sp < S - 1; sp += 64)
-            __hip_atomic_store(flags + (size_t)sp * tiles_n, (uint64_t)0, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    }
+    // the flags seen back to the waiting state, whether or not the tile
+    // completed (one given up on is reset by its late split, or was above)
+    if (S > 1 && wave == 0 && got)
+        __hip_atomic_store(split_flags(op, S) + tn + (size_t)lane * tiles_n, (uint64_t)0,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // K splits for M x N x K: the fewest that keep every split at 8 chunks or
@@ -402,14 +435,14 @@ int gemv_split_count(int M, int N, int K, int forced)
     return s < KC ? s : KC;
 }
 
-// Scratch of an S-split launch: summed in the launch, S-1 partial slices
-// and (S-1) x tiles flags; otherwise S partial slices.
+// Scratch of an S-split launch: summed in the launch, S-1 partial slices,
+// (S-1) x tiles flags and the status word; otherwise S partial slices.
 static size_t split_scratch(int S, int M, int N)
 {
     const size_t tiles = (size_t)(N + kSplitCols - 1) / kSplitCols;
     if (S <= 1) return 0;
     if (S > kInLaunchMaxSplits) return (size_t)S * M * N * 4;
-    return (size_t)(S - 1) * M * N * 4 + (size_t)(S - 1) * tiles * 8;
+    return (size_t)(S - 1) * M * N * 4 + (size_t)(S - 1) * tiles * 8 + 8;
 }
 
 size_t gemv_split_bytes(int M, int N, int K)
@@ -428,7 +461,7 @@ static uint64_t next_epoch()
     }()};
     uint64_t e;
     do e = ctr.fetch_add(1, std::memory_order_relaxed);
-    while (e == 0);
+    while (e == 0 || e == kSplitGaveUp);
     return e;
 }
 

@@ -44,6 +44,7 @@ struct Tuning {
     int batch_split = 0;
     int wide_tiles = 0;
     int wide_waves = 0;
+    int split_spin_limit = 0;   // 0: the kernel's own bound
 };
 
 // Activation scale addressing shared by the kernels: chunk j of row m uses

@@ -24,8 +24,9 @@
  * Activation quantization per group: scale = amax/448 (1.0 when below
  * 1e-12), q = e4m3_rne(x * (1/scale)).
  *
- * Requirements: K % 128 == 0, N % 16 == 0, M >= 1, 16-byte aligned
- * pointers for x, w, q and c.
+ * Requirements: N % 16 == 0, K % 16 == 0, M >= 1, 16-byte aligned
+ * pointers for x, w, q and c; K % 128 == 0 with 1x128 activation groups or
+ * 128x128 weight blocks (heph_fp8_linear below lists the domain).
  */
 #ifndef HEPHFP8_H
 #define HEPHFP8_H
@@ -107,7 +108,18 @@ int heph_fp8_quant_weight(const uint16_t* w_bf16, uint8_t* q, float* scale_inv,
  *   stream               the stream of the reference's DeviceContext
  * On return the workspaces hold x's codes and scales (unless SKIP_QUANT),
  * so later calls on the same x can pass SKIP_QUANT.
+ * Past the codes (from the next 256-byte boundary) q_ws is K-split scratch
+ * when q_ws_bytes >= heph_fp8_linear_ws_bytes(M, N, K). At M <= 32 the
+ * 64-column kernel may sum 2 or 3 K splits inside one launch, where the last
+ * split of each column tile waits for the others' completion flags for a
+ * bounded time (~0.3 s). If a wait ever gives up, that tile's outputs are
+ * NaN, the call still returns HEPH_OK (nothing waits for the device), and
+ * the 64-bit word at byte HEPH_SPLIT_STATUS_OFFSET(q_ws_bytes) of q_ws is
+ * incremented: a count of tiles given up since the caller last zeroed it,
+ * for the caller to read after synchronizing. The flags are left ready, so
+ * later calls and graph replays on the workspace are unaffected.
  */
+#define HEPH_SPLIT_STATUS_OFFSET(q_ws_bytes) (((size_t)(q_ws_bytes) - 8) & ~(size_t)7)
 int heph_fp8_linear(void* c, int c_dtype, const uint16_t* x_bf16,
                     const uint8_t* w, const float* w_scale, int w_block_n,
                     int w_block_k, uint8_t* q_ws, size_t q_ws_bytes,
@@ -289,6 +301,10 @@ const char* heph_last_kernel(void);
  *                1, 2 or 4 always, with 16 x that many output columns per
  *                workgroup (halved until it divides N / 16)
  *   wide_waves   its waves per workgroup: 4, 8 or 16 (16: one column tile)
+ *   split_spin_limit  polls of a completion flag before the 64-column
+ *                kernel's in-launch split sum gives up (that tile's outputs
+ *                are then NaN, see HEPH_SPLIT_STATUS): n > 0 polls, -1 give
+ *                up without polling (to exercise that path in tests)
  * Values outside these sets give HEPH_ERR_FLAGS.
  */
 typedef struct heph_launch_overrides {
@@ -299,6 +315,7 @@ typedef struct heph_launch_overrides {
     int batch_split;
     int wide_tiles;
     int wide_waves;
+    int split_spin_limit;
 } heph_launch_overrides;
 
 int heph_fp8_linear_with(void* c, int c_dtype, const uint16_t* x_bf16,

@@ -1209,6 +1209,67 @@ def test_batch_split_flags_graph_replays_and_garbage_workspace():
             assert torch.equal(outs[n], eager[n]), (n, rep, "eager")
 
 
+def test_batch_split_give_up_is_counted_and_leaves_flags_ready():
+    # The in-launch split sum's bounded wait, forced to give up from the host
+    # (split_spin_limit -1: no polling; every kernel still ends normally):
+    # every tile's outputs are NaN and the status word at
+    # HEPH_SPLIT_STATUS_OFFSET(q_ws_bytes) counts the tiles given up. The
+    # flags are then back in the waiting state: eager calls and replays of a
+    # graph captured before (which repeat their epoch) give the bits of a
+    # call on a fresh workspace.
+    M, N, K = 32, 6144, 2560                  # qkv: 3 splits summed in the launch
+    tiles = N // 64
+    xh = O.gen_act_bf16(41, M, K)
+    qw, sw = O.gen_weight(42, N, K)
+    x, w, swd = dev(xh), dev(qw), dev(sw)
+    q_ws = torch.zeros(L.lib().heph_fp8_linear_ws_bytes(M, N, K), dtype=torch.uint8,
+                       device="cuda")
+    s_ws = torch.empty(M * (K // 128), dtype=torch.float32, device="cuda")
+    status_at = (q_ws.numel() - 8) & ~7
+    c = torch.zeros(M, N, dtype=torch.bfloat16, device="cuda")
+
+    def status():
+        torch.cuda.synchronize()
+        return int(q_ws[status_at:status_at + 8].cpu().numpy().view(np.uint64)[0])
+
+    def call(**extra):
+        HK.linear_fp8(c, x, w, swd, q_ws, s_ws, M, N, K, tune={"batch_split": 1, **extra})
+
+    call()
+    assert HK.last_kernel() == "fp8_gemv_split64_fused_splitk", HK.last_kernel()
+    torch.cuda.synchronize()
+    ref = c.clone()
+    check_close(host_bf16(ref), O.quant_linear(xh, qw, sw), "split")
+    assert status() == 0
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        call()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            call()
+    for rep in range(3):
+        c.zero_()
+        call(split_spin_limit=-1)
+        torch.cuda.synchronize()
+        assert torch.isnan(c.float()).all(), rep
+        assert status() == tiles * (rep + 1), rep
+        c.zero_()
+        graph.replay()                        # the epoch of the capture
+        torch.cuda.synchronize()
+        assert torch.equal(c, ref), rep
+        c.zero_()
+        call()                                # a new epoch
+        torch.cuda.synchronize()
+        assert torch.equal(c, ref), rep
+    # a bounded wait long enough for the others' flags completes normally
+    call(split_spin_limit=1 << 16)
+    torch.cuda.synchronize()
+    assert torch.equal(c, ref) and status() == 3 * tiles
+    with pytest.raises(HK.HephError):
+        call(split_spin_limit=-2)
+
+
 @pytest.mark.parametrize("out,resid", [("bf16", False), ("f32", True)])
 def test_large_m_split_k_every_tile(out, resid, tile_m):
     # Few tiles (M = 200, N = 272) and 17 chunks: every forced tile height
