@@ -774,24 +774,6 @@ hipError_t launch_splitk_reduce(const Fp8Operands& op, hipStream_t stream, const
 }
 
 namespace {
-int g_cu_count[64];
-}  // namespace
-
-int cu_count()
-{
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    int n = __atomic_load_n(&g_cu_count[dev], __ATOMIC_RELAXED);
-    if (n <= 0) {
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            n <= 0)
-            n = 256;
-        __atomic_store_n(&g_cu_count[dev], n, __ATOMIC_RELAXED);
-    }
-    return n;
-}
-
-namespace {
 
 template <int BM>
 hipError_t launch_big(const Fp8Operands& op, hipStream_t stream, const LaunchTiming& t)
@@ -856,7 +838,9 @@ static double gemm_estimate(int M, int N, int K, int bm, long cycles, int s, lon
 // down in 128 rows and 6 splits.
 GemmPlan gemm_plan(int M, int N, int K, bool can_split, int forced)
 {
-    const long cus = cu_count();
+    // MI355X's 256 CUs, not the visible count: the plan (and the K-split
+    // summation order with it) does not change under a CU mask or partition
+    const long cus = kPlanCUs;
     const int KC = K / kChunk;
     GemmPlan best{0, 1};
     double best_t = -1.0;

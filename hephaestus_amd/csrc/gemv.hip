@@ -144,7 +144,7 @@ void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, in
     if (plain1) {
         // the fewest steps per wave (1, then 2) whose wave count, rounded up
         // to one of 4, 5, 8, 10, fits every workgroup on the CUs at once
-        const long budget = 32L * cu_count(), wgs = (long)tiles * k;
+        const long budget = 32L * kPlanCUs, wgs = (long)tiles * k;
         w = 4;
         for (int p = 1; p <= 2; ++p) {
             int need = (S + p - 1) / p;

@@ -114,8 +114,10 @@ bool gemv_fuses(int M, int N, int K);
 void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, int* u,
                 bool norm = false);
 
-// Compute units of the current device (cached per device).
-int cu_count();
+// Compute units the launch shapes are planned for: MI355X's 256. A fixed
+// count, so that shapes, summation orders and output bits do not depend on
+// how many CUs a mask or partition leaves visible.
+constexpr int kPlanCUs = 256;
 
 // Tiled MFMA GEMM for any M (prefill); reads q/s from the workspace.
 hipError_t launch_fp8_gemm(const Fp8Operands& op, hipStream_t stream,
