@@ -247,7 +247,7 @@ def achievable_mfma(blocks=1024, iters=16384):
 
 def vendor_fp8_gemm(M=4096, calls=10):
     """hipBLASLt's FP8 GEMM through torch._scaled_mm on the configs[3] shapes
-    at M = 4096: E4M3 operands with one fp32 scale per tensor (the vendor
+    at M rows (4096 or 512): E4M3 operands with one fp32 scale per tensor (the vendor
     library has no 128x128 block-scale mode), bf16 out, weights rotated past
     the Infinity Cache as for this library's GEMM; per call (HIP events
     around `calls` calls after ~20 ms of the same calls). A comparison, not
@@ -316,6 +316,8 @@ def parse():
                          "shape 100 + --steps GEMM launches on quantized activations, then "
                          "--steps quantizer launches; for rocprofv3 traces and counters); "
                          "prints no JSON")
+    ap.add_argument("--prefill-m", type=int, default=4096,
+                    help="rows of the --prefill-pass launches (configs[3]: 512 or 4096)")
     ap.add_argument("--decode-pass", action="store_true",
                     help="only run configs[4] decode steps eagerly (random-init Qwen3-4B, "
                          "4096 cached tokens; for rocprofv3 traces); prints no JSON")
@@ -324,11 +326,13 @@ def parse():
                          "HIP graph of --steps calls replayed 4 times, per shape) plus a 256 "
                          "MiB device copy (for rocprofv3 --pmc traffic counts and kernel "
                          "traces); prints no JSON")
+    ap.add_argument("--pmc-m", default="1,16,32",
+                    help="comma-separated row counts of the --pmc-pass launches")
     return ap.parse_args()
 
 
-def prefill_pass(steps):
-    """configs[3] at M = 4096, per shape: the activations quantized once,
+def prefill_pass(steps, M=4096):
+    """configs[3] at M rows (4096 or 512), per shape: the activations quantized once,
     then the GEMM alone (SKIP_QUANT, as the bench's kernel-only prefill
     figure) eagerly over the rotated weight copies (weights come from HBM,
     not the Infinity Cache), 100 launches before the `steps` counted ones so
@@ -337,7 +341,6 @@ def prefill_pass(steps):
     import torch
     from hephaestus_amd import kernels as HK
     torch.cuda.set_device(0)
-    M = 4096
     for i, (name, N, K) in enumerate(SHAPES):
         lin = Linear(name, N, K, M, seed=WEIGHT_SEEDS[name])
         x = act(M, K, seed=M + 1, outliers=True)
@@ -382,10 +385,10 @@ def decode_pass(steps):
           f"argmax={int(dec.next_token.item())}", flush=True)
 
 
-def pmc_pass(steps):
+def pmc_pass(steps, Ms=(1, 16, 32)):
     """Launches of every shape at M = 1, then the configs[2] batched decode
-    sizes M = 16 and 32 (bf16 rows, default route), and one plain copy of
-    known size.
+    sizes (by default M = 16 and 32; bf16 rows, default route), and one
+    plain copy of known size.
 
     Under rocprofv3 --pmc FETCH_SIZE (or WRITE_SIZE) the copy kernel's count
     calibrates the counter: bytes = count * (copy bytes / copy count)."""
@@ -395,7 +398,7 @@ def pmc_pass(steps):
     lins = [Linear(n, N, K, 32, seed=WEIGHT_SEEDS[n]) for i, (n, N, K) in enumerate(SHAPES)]
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
-    for M in (1, 16, 32):
+    for M in Ms:
         for lin in lins:
             x = act(M, lin.K, seed=lin.K + M)
             c = torch.empty(M, lin.N, dtype=torch.bfloat16, device="cuda")
@@ -513,10 +516,10 @@ def main():
               "(the FP8 linear path has no multi-GPU mode here)", file=sys.stderr)
         sys.exit(2)
     if args.pmc_pass:
-        pmc_pass(max(1, min(args.steps, 20)))
+        pmc_pass(max(1, min(args.steps, 20)), tuple(int(m) for m in args.pmc_m.split(",")))
         return
     if args.prefill_pass:
-        prefill_pass(max(1, min(args.steps, 20)))
+        prefill_pass(max(1, min(args.steps, 20)), args.prefill_m)
         return
     if args.decode_pass:
         decode_pass(max(1, min(args.steps, 20)))
@@ -662,19 +665,25 @@ def main():
         "detail": detail,
     }
     pk = detail.get("prefill_m4096_kernel")
-    if pk:
+    path_tf = detail.get("prefill_m4096_TFLOPs")
+    if pk and path_tf:
+        # headline: the path (activation quantizer + GEMM, graph-replayed per
+        # call), the work BASELINE's metric counts; the GEMM alone beside it
         line["prefill_roofline"] = {
-            "bound": "mfma", "achieved": pk["TFLOPs"], "peak": FP8_PEAK_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(pk["TFLOPs"] / FP8_PEAK_TFLOPS, 4),
+            "bound": "mfma", "achieved": path_tf, "peak": FP8_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(path_tf / FP8_PEAK_TFLOPS, 4),
+            "what": "quantizer + GEMM per call",
+            "kernel_only_TFLOPs": pk["TFLOPs"],
+            "kernel_only_frac": round(pk["TFLOPs"] / FP8_PEAK_TFLOPS, 4),
             "traffic": profiled_traffic(PREFILL_TRAFFIC_PROFILE),
             "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE per 4-shape step, "
                               "profiles/fp8_gemm_m4096_pmc_traffic.md",
             "kernel": ", ".join(sorted(set(pk["kernels"]))),
             "flops_per_step": pk["flops_per_step"],
-            "workload": "configs[3] M=4096 over the 4 config-1 shapes, GEMM kernel only "
-                        "(activations quantized beforehand), weights rotated past the "
-                        "Infinity Cache",
-            "path_TFLOPs_quant_plus_gemm": detail.get("prefill_m4096_TFLOPs")}
+            "workload": "configs[3] M=4096 over the 4 config-1 shapes: per call the "
+                        "activation quantizer then the GEMM (kernel_only: the GEMM "
+                        "alone on activations quantized beforehand), weights rotated "
+                        "past the Infinity Cache"}
         am = detail.get("achievable_mfma")
         if am and am.get("TFLOPs"):
             line["prefill_roofline"]["frac_of_achievable_mfma"] = round(pk["TFLOPs"] / am["TFLOPs"], 4)
@@ -777,6 +786,7 @@ def detail_sweeps(lins):
     out["prefill_m4096_kernel"] = prefill_kernel_times(lins)
     out["achievable_mfma"] = achievable_mfma()
     out["vendor_fp8_gemm_m4096"] = vendor_fp8_gemm()
+    out["vendor_fp8_gemm_m512"] = vendor_fp8_gemm(M=512, calls=20)
     out["prefill_producer_path"] = prefill_producer_path(lins)
     out["decode_step_config4"] = decode_step_timing()
     t4096 = sum(2.0 * 4096 * l.N * l.K for l in lins)
