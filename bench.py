@@ -686,10 +686,12 @@ def main():
                         "past the Infinity Cache"}
         am = detail.get("achievable_mfma")
         if am and am.get("TFLOPs"):
-            line["prefill_roofline"]["frac_of_achievable_mfma"] = round(pk["TFLOPs"] / am["TFLOPs"], 4)
+            line["prefill_roofline"]["kernel_only_frac_of_achievable_mfma"] = round(
+                pk["TFLOPs"] / am["TFLOPs"], 4)
         vg = (detail.get("vendor_fp8_gemm_m4096") or {}).get("all")
         if vg:
-            line["prefill_roofline"]["vs_hipblaslt_per_tensor_fp8"] = round(pk["TFLOPs"] / vg["TFLOPs"], 3)
+            line["prefill_roofline"]["kernel_only_vs_hipblaslt_per_tensor_fp8"] = round(
+                pk["TFLOPs"] / vg["TFLOPs"], 3)
     print(json.dumps(line))
 
 
