@@ -46,7 +46,8 @@ class LaunchOverrides(ctypes.Structure):
     _fields_ = [("gemv_ks", ctypes.c_int), ("gemv_waves", ctypes.c_int),
                 ("gemv_u", ctypes.c_int), ("gemm_bm", ctypes.c_int),
                 ("batch_split", ctypes.c_int), ("wide_tiles", ctypes.c_int),
-                ("wide_waves", ctypes.c_int), ("split_spin_limit", ctypes.c_int)]
+                ("wide_waves", ctypes.c_int), ("split_spin_limit", ctypes.c_int),
+                ("gemv_groups", ctypes.c_int)]
 
 
 _vp = ctypes.c_void_p

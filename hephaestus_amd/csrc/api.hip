@@ -136,7 +136,10 @@ int take_overrides(const heph_launch_overrides* ov, Tuning* t)
     if (wt != -1 && wt != 0 && wt != 1 && wt != 2 && wt != 4) return HEPH_ERR_FLAGS;
     if (ww != 0 && ww != 4 && ww != 8 && ww != 16) return HEPH_ERR_FLAGS;
     if (ov->split_spin_limit < -1) return HEPH_ERR_FLAGS;
+    if (ov->gemv_groups != 0 && ov->gemv_groups != 1 && ov->gemv_groups != 2)
+        return HEPH_ERR_FLAGS;
     t->split_spin_limit = ov->split_spin_limit;
+    t->gemv_groups = ov->gemv_groups;
     t->wide_tiles = wt;
     t->wide_waves = ww;
     t->gemv_ks = ks;

@@ -70,6 +70,20 @@ hipError_t launch_wu(const GemvArgs& a, bool fused, int ks, int mr, hipStream_t 
     return launch_ks<WAVES, 1, 16, 1, U>(a, fused, stream, t);
 }
 
+// Two column groups per workgroup (fused, M = 1, four chunk slots: 8
+// columns a workgroup).
+template <int WAVES, int U>
+hipError_t launch_groups2(const GemvArgs& a, hipStream_t stream, const LaunchTiming& t)
+{
+    const dim3 grid(a.op.N / 8);
+    const dim3 block(WAVES * 64);
+    if (a.op.w_block)
+        return launch(fp8_gemv_kernel<WAVES, 4, 1, 1, U, true, kGemvBlock, false, false, 2>, grid,
+                      block, 0, stream, t, a);
+    return launch(fp8_gemv_kernel<WAVES, 4, 1, 1, U, true, kGemvChannel, false, false, 2>, grid,
+                  block, 0, stream, t, a);
+}
+
 }  // namespace
 
 // Fused quantization re-quantizes x in every workgroup (N*KS/16 of them).
@@ -111,7 +125,7 @@ int gemv_rows(int M)
 // when each wave has exactly 2 steps; at 3..4 rows with K >= 8192 two;
 // else one (wider activation tiles need the registers).
 void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, int* u,
-                bool norm)
+                bool norm, int* groups)
 {
     const int mr = gemv_rows(M);
     const int kmax = mr >= 2 ? 16 / mr : 8;
@@ -141,10 +155,20 @@ void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, in
     // by 4 waves)
     if (long_k) w = 10;
     else if (mr == 4 && (long)tiles * k >= 1024) w = 4;
+    // Column groups (fused M = 1 with four slots): two where that still
+    // leaves >= 640 workgroups. Every workgroup reads all K activations for
+    // its columns, 2 bytes each: with four columns that is half as many
+    // bytes again as its weights, and a one-pass read of the weights with
+    // those activation loads beside them took (MI355X, graph-replayed)
+    // 5.1 against 4.5 us (qkv) and 10.8 against 9.5 (gate_up); with eight
+    // columns 4.4 and 9.9.
+    int cg = 1;
+    if (groups && plain1 && k == 4 && (long)tiles * k / 2 >= 640) cg = 2;
+    if (groups && tune.gemv_groups) cg = plain1 && k == 4 ? tune.gemv_groups : 1;
     if (plain1) {
         // the fewest steps per wave (1, then 2) whose wave count, rounded up
         // to one of 4, 5, 8, 10, fits every workgroup on the CUs at once
-        const long budget = 32L * kPlanCUs, wgs = (long)tiles * k;
+        const long budget = 32L * kPlanCUs, wgs = (long)tiles * k / cg;
         w = 4;
         for (int p = 1; p <= 2; ++p) {
             int need = (S + p - 1) / p;
@@ -171,6 +195,7 @@ void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, in
     *ks = k;
     *waves = w;
     *u = uu;
+    if (groups) *groups = cg;
 }
 
 hipError_t launch_fp8_gemv(const Fp8Operands& op, bool fused, hipStream_t stream,
@@ -178,12 +203,21 @@ hipError_t launch_fp8_gemv(const Fp8Operands& op, bool fused, hipStream_t stream
                            float eps)
 {
     GemvArgs a{op, fused, gamma, eps};
-    int ks, waves, u;
-    gemv_shape(op.M, op.N, op.K, op.tune, &ks, &waves, &u, gamma != nullptr);
+    int ks, waves, u, cg = 1;
+    gemv_shape(op.M, op.N, op.K, op.tune, &ks, &waves, &u, gamma != nullptr,
+               fused && !gamma ? &cg : nullptr);
     const int mr = gemv_rows(op.M);
     if (op.M == 1) *name = gamma ? "fp8_gemv_rmsnorm_m1" : fused ? "fp8_gemv_fused_m1" : "fp8_gemv_m1";
     else if (op.M <= 16) *name = fused ? "fp8_gemv_fused_m16" : "fp8_gemv_m16";
     else *name = fused ? "fp8_gemv_fused_m32" : "fp8_gemv_m32";
+    if (cg == 2) {
+        switch (waves) {
+        case 5: return u == 2 ? launch_groups2<5, 2>(a, stream, t) : launch_groups2<5, 1>(a, stream, t);
+        case 8: return u == 2 ? launch_groups2<8, 2>(a, stream, t) : launch_groups2<8, 1>(a, stream, t);
+        case 10: return u == 2 ? launch_groups2<10, 2>(a, stream, t) : launch_groups2<10, 1>(a, stream, t);
+        default: return u == 2 ? launch_groups2<4, 2>(a, stream, t) : launch_groups2<4, 1>(a, stream, t);
+        }
+    }
     if ((mr == 4 || mr == 8) && waves == 10) {
         if (mr == 4)
             return u == 2 ? launch_mr<10, 4, 1, 2>(a, fused, ks, stream, t)

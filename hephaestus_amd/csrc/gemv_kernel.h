@@ -152,8 +152,14 @@ __device__ __forceinline__ float pick(const f32x4& p, int e)
 // stores act[j] = bf16(bf16(g / (1 + exp(-g))) * up) of their bf16-rounded
 // values: with the launch shape of the plain kernel, the GEMV output and
 // silu_mul of the two-launch form bit for bit.
+//
+// CG: column groups per workgroup (1 or 2). With 2, every step of a wave
+// contracts the same A tile (the quantized activations of its chunks) with
+// the weights of two groups of TW columns, so a workgroup owns 2 TW columns
+// and reads the activations once for both: the activation bytes a workgroup
+// reads per weight byte halve, and so do the workgroups.
 template <int WAVES, int KS, int MR, int MT, int U, bool FUSED, int SM, bool NORM = false,
-          bool GLU = false>
+          bool GLU = false, int CG = 1>
 __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
 {
     static_assert(!NORM || (FUSED && MR == 1 && MT == 1 && WAVES >= 4),
@@ -165,6 +171,7 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
     static_assert(KS * MR <= 16, "slots x rows must fit the 16 MFMA rows");
     static_assert(MT == 1 || (MT == 2 && MR == 16 && KS == 1), "two row tiles: one slot of 16");
     static_assert(!(FUSED && SM == kGemvConst), "fused quantization: 1x128 groups");
+    static_assert(CG == 1 || (CG == 2 && MT == 1 && !GLU), "two column groups: one row tile");
     constexpr int R = KS * MR;           // A rows in use
     constexpr int TW = 16 / KS;          // output columns per workgroup
     constexpr int LPR = 64 / R;          // quantizing lanes per A row
@@ -183,7 +190,7 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
     const int M = op.M, K = op.K;
     const int KC = K >> 7;
     const int S = (KC + KS - 1) / KS;    // steps of KS chunks
-    const int n0 = blockIdx.x * TW;
+    const int n0 = blockIdx.x * (TW * CG);
     const int per = (S + WAVES - 1) / WAVES;
     const int sb = min(S, wave * per);
     const int se = min(S, sb + per);
@@ -193,7 +200,7 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
     // separate quantization: this lane loads A row r16 (slot ta, row ma)
     const int ta = r16 / MR, ma = r16 % MR;
 
-    __shared__ float red[WAVES][MT * NE][64];
+    __shared__ float red[WAVES][CG * MT * NE][64];
     __shared__ __attribute__((aligned(16))) uint8_t qlds[FUSED ? WAVES : 1][FUSED ? U : 1]
                                                         [FUSED ? MT : 1][R * kChunk];
     // NORM: the row and gamma (bf16)
@@ -207,14 +214,18 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
     const int n = !GLU ? n0 + cw
                 : cw < HALF ? HALF * (int)blockIdx.x + cw
                             : op.N / 2 + HALF * (int)blockIdx.x + cw - HALF;
+    // column group h reads the rows h*TW further on
     const uint8_t* wrow = op.w + (size_t)n * K + g * 16;
     // the 128-row block of the workgroup's columns (GLU: of the lane's
-    // half, so a per-lane load)
+    // half, so a per-lane load); with two groups both lie in it (2 TW
+    // divides 128)
     const float* swb = op.sw + (size_t)((GLU ? n : n0) >> 7) * op.sw_ld;
-    const float swc = SM == kGemvBlock ? 0.0f : op.sw[n];
+    float swc[CG];
+#pragma unroll
+    for (int h = 0; h < CG; ++h) swc[h] = SM == kGemvBlock ? 0.0f : op.sw[n + h * TW];
 
     struct Batch {
-        i32x4 blo[U], bhi[U];
+        i32x4 blo[U][CG], bhi[U][CG];
         i32x4 alo[FUSED ? 1 : U][MT], ahi[FUSED ? 1 : U][MT];
         XVec<E> xv[FUSED ? U : 1][MT];
         float sw[U];
@@ -278,27 +289,32 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
             const int st = min(s + u, se - 1);
             const int jb = min(st * KS + t, KC - 1);
             const uint8_t* p = wrow + (size_t)jb * kChunk;
-            b.blo[u] = ldg16(p);
-            b.bhi[u] = ldg16(p + 64);
+#pragma unroll
+            for (int h = 0; h < CG; ++h) {
+                b.blo[u][h] = ldg16(p + (size_t)h * TW * K);
+                b.bhi[u][h] = ldg16(p + (size_t)h * TW * K + 64);
+            }
             if constexpr (SM == kGemvBlock) b.sw[u] = swb[jb];
         }
     };
 
-    float acc[MT][NE];
+    float acc[CG][MT][NE];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int h = 0; h < CG; ++h)
 #pragma unroll
-        for (int i = 0; i < NE; ++i) acc[mt][i] = 0.0f;
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < NE; ++i) acc[h][mt][i] = 0.0f;
     float rn = 1.0f;    // RMSNorm factor (NORM)
 
-    auto contract = [&](int mt, const i32x4& alo, const i32x4& ahi, const i32x4& blo,
+    auto contract = [&](int h, int mt, const i32x4& alo, const i32x4& ahi, const i32x4& blo,
                         const i32x4& bhi, const float* scl) {
         const f32x4 p = mfma_e4m3(join(alo, ahi), join(blo, bhi), f32x4{0, 0, 0, 0});
 #pragma unroll
         for (int i = 0; i < NE; ++i) {
             const float v = MR >= 4 ? p[i] : pick(p, e0 + i);
-            if constexpr (SM == kGemvConst) acc[mt][i] += v;
-            else acc[mt][i] += v * scl[i];
+            if constexpr (SM == kGemvConst) acc[h][mt][i] += v;
+            else acc[h][mt][i] += v * scl[i];
         }
     };
 
@@ -370,7 +386,6 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 if (s + u >= se) break;
-                const float sw = SM == kGemvBlock ? b.sw[u] : swc;
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
                     const uint8_t* tile = qlds[wave][u][mt];
@@ -379,16 +394,20 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
                         lo = *reinterpret_cast<const i32x4*>(tile + r16 * kChunk + g * 16);
                         hi = *reinterpret_cast<const i32x4*>(tile + r16 * kChunk + 64 + g * 16);
                     }
-                    float scl[NE];
+                    float sa[NE];
 #pragma unroll
-                    for (int i = 0; i < NE; ++i) {
-                        const float sa =
-                            R == 1 ? sc[u][mt]
-                                   : __int_as_float(__builtin_amdgcn_ds_bpermute(
-                                         (rho + i) * LPR * 4, __float_as_int(sc[u][mt])));
-                        scl[i] = sa * sw;
+                    for (int i = 0; i < NE; ++i)
+                        sa[i] = R == 1 ? sc[u][mt]
+                                       : __int_as_float(__builtin_amdgcn_ds_bpermute(
+                                             (rho + i) * LPR * 4, __float_as_int(sc[u][mt])));
+#pragma unroll
+                    for (int h = 0; h < CG; ++h) {
+                        const float sw = SM == kGemvBlock ? b.sw[u] : swc[h];
+                        float scl[NE];
+#pragma unroll
+                        for (int i = 0; i < NE; ++i) scl[i] = sa[i] * sw;
+                        contract(h, mt, lo, hi, b.blo[u][h], b.bhi[u][h], scl);
                     }
-                    contract(mt, lo, hi, b.blo[u], b.bhi[u], scl);
                 }
             }
             __builtin_amdgcn_wave_barrier();
@@ -396,20 +415,26 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 if (s + u >= se) break;
-                const float sw = SM == kGemvBlock ? b.sw[u] : swc;
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
-                    float scl[NE];
+                    float sa[NE];
 #pragma unroll
                     for (int i = 0; i < NE; ++i) {
-                        float sa = 0.0f;
+                        sa[i] = 0.0f;
                         if constexpr (SM != kGemvConst)
-                            sa = MR == 1 ? b.sa[u][mt]
-                                         : __int_as_float(__builtin_amdgcn_ds_bpermute(
-                                               (rho + i) * 4, __float_as_int(b.sa[u][mt])));
-                        scl[i] = sa * sw;
+                            sa[i] = MR == 1 ? b.sa[u][mt]
+                                            : __int_as_float(__builtin_amdgcn_ds_bpermute(
+                                                  (rho + i) * 4, __float_as_int(b.sa[u][mt])));
                     }
-                    contract(mt, b.alo[u][mt], b.ahi[u][mt], b.blo[u], b.bhi[u], scl);
+#pragma unroll
+                    for (int h = 0; h < CG; ++h) {
+                        const float sw = SM == kGemvBlock ? b.sw[u] : swc[h];
+                        float scl[NE];
+#pragma unroll
+                        for (int i = 0; i < NE; ++i) scl[i] = sa[i] * sw;
+                        contract(h, mt, b.alo[u][mt], b.ahi[u][mt], b.blo[u][h], b.bhi[u][h],
+                                 scl);
+                    }
                 }
             }
         }
@@ -481,9 +506,11 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
 
     // ---- wave 0 sums the partials in a fixed order after one barrier ----
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int h = 0; h < CG; ++h)
 #pragma unroll
-        for (int i = 0; i < NE; ++i) red[wave][mt * NE + i][lane] = acc[mt][i];
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < NE; ++i) red[wave][(h * MT + mt) * NE + i][lane] = acc[h][mt][i];
     __syncthreads();
     if (wave != 0) return;
 
@@ -504,11 +531,12 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
         return;
     }
 
-    // output (token mt*16 + m, column n0 + c2) = sum over waves w and slots
-    // ts of C row ts*MR + m, column ts*TW + c2
-    constexpr int OUTS = MT * MR * TW;
+    // output (token mt*16 + m, column n0 + h*TW + c2) = sum over waves w and
+    // slots ts of C row ts*MR + m, column ts*TW + c2 of group h
+    constexpr int OUTS = CG * MT * MR * TW;
     for (int o = lane; o < OUTS; o += 64) {
-        const int c2 = o % TW, m = (o / TW) % MR, mt = o / (TW * MR);
+        const int c2 = o % TW, m = (o / TW) % MR, mt = (o / (TW * MR)) % MT;
+        const int h = o / (TW * MR * MT);
         const int tok = mt * 16 + m;
         if (tok >= M) continue;
         float v = 0.0f;
@@ -517,9 +545,10 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemv_kernel(GemvArgs args)
 #pragma unroll
             for (int ts = 0; ts < KS; ++ts) {
                 const int rr = ts * MR + m;
-                v += red[w][mt * NE + (MR >= 4 ? (rr & 3) : m)][(rr >> 2) * 16 + ts * TW + c2];
+                v += red[w][(h * MT + mt) * NE + (MR >= 4 ? (rr & 3) : m)]
+                         [(rr >> 2) * 16 + ts * TW + c2];
             }
-        const int col = n0 + c2;
+        const int col = n0 + h * TW + c2;
         if constexpr (SM == kGemvConst) {
             const float sa = op.s[(size_t)tok * op.s_ld], sw = op.sw[col];
             v = M == 1 ? v * (sa * sw) : (v * sa) * sw;

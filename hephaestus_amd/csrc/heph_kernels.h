@@ -45,6 +45,7 @@ struct Tuning {
     int wide_tiles = 0;
     int wide_waves = 0;
     int split_spin_limit = 0;   // 0: the kernel's own bound
+    int gemv_groups = 0;
 };
 
 // Activation scale addressing shared by the kernels: chunk j of row m uses
@@ -111,8 +112,10 @@ hipError_t launch_fp8_gemv(const Fp8Operands& op, bool fused, hipStream_t stream
 int gemv_rows(int M);
 // Whether the chunk-slot kernel quantizes x itself for M x N x K (group 128).
 bool gemv_fuses(int M, int N, int K);
+// groups (when not null): column groups per workgroup, planned for the
+// fused route (1 or 2; see fp8_gemv_kernel's CG).
 void gemv_shape(int M, int N, int K, const Tuning& tune, int* ks, int* waves, int* u,
-                bool norm = false);
+                bool norm = false, int* groups = nullptr);
 
 // Compute units the launch shapes are planned for: MI355X's 256. A fixed
 // count, so that shapes, summation orders and output bits do not depend on

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define HEPH_ABI_VERSION 4
+#define HEPH_ABI_VERSION 5
 
 /* status codes */
 #define HEPH_OK                 0
@@ -305,6 +305,10 @@ const char* heph_last_kernel(void);
  *                kernel's in-launch split sum gives up (that tile's outputs
  *                are then NaN, see HEPH_SPLIT_STATUS): n > 0 polls, -1 give
  *                up without polling (to exercise that path in tests)
+ *   gemv_groups  column groups per workgroup of the chunk-slot GEMV at M = 1
+ *                with bf16 rows and four chunk slots: 1 or 2 (2: each
+ *                workgroup covers 8 columns and quantizes x once for both
+ *                groups); ignored by every other shape
  * Values outside these sets give HEPH_ERR_FLAGS.
  */
 typedef struct heph_launch_overrides {
@@ -316,6 +320,7 @@ typedef struct heph_launch_overrides {
     int wide_tiles;
     int wide_waves;
     int split_spin_limit;
+    int gemv_groups;
 } heph_launch_overrides;
 
 int heph_fp8_linear_with(void* c, int c_dtype, const uint16_t* x_bf16,

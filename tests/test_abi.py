@@ -26,7 +26,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_version_and_strerror(lib):
-    assert lib.heph_abi_version() == 4
+    assert lib.heph_abi_version() == 5
     for code in range(0, -12, -1):
         msg = L.strerror(code)
         assert msg and msg != "unknown status", code
@@ -141,12 +141,12 @@ def test_launch_overrides_validate(lib):
           dict(gemm_bm=192), dict(gemm_bm=64), dict(gemm_bm=1), dict(batch_split=-1),
           dict(batch_split=64), dict(wide_tiles=-1), dict(wide_tiles=4),
           dict(wide_tiles=2, wide_waves=16), dict(split_spin_limit=-1),
-          dict(split_spin_limit=1000), dict()]
+          dict(split_spin_limit=1000), dict(gemv_groups=1), dict(gemv_groups=2), dict()]
     bad = [dict(gemv_ks=16), dict(gemv_ks=3), dict(gemv_waves=2), dict(gemv_waves=6),
            dict(gemv_u=4),
            dict(gemm_bm=96), dict(batch_split=-2), dict(batch_split=65), dict(wide_tiles=3),
            dict(wide_tiles=8), dict(wide_tiles=-2), dict(wide_waves=2), dict(wide_waves=12),
-           dict(split_spin_limit=-2)]
+           dict(split_spin_limit=-2), dict(gemv_groups=3), dict(gemv_groups=-1)]
     for ov in ok:
         assert with_overrides(lib, **ov) != L.HEPH_ERR_FLAGS, ov
     for ov in bad:

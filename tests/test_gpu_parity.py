@@ -293,8 +293,8 @@ def test_reference_granularity_random_cross_kernel():
 
 @pytest.mark.parametrize("N,K", [(16, 128), (48, 384), (2560, 1152), (2560, 9728)])
 def test_gemv_every_launch_shape(N, K):
-    # The M = 1 kernel at every chunk-slot count, wave count (4, 5, 8, 10)
-    # and batch depth,
+    # The M = 1 kernel at every chunk-slot count, wave count (4, 5, 8, 10),
+    # batch depth and (four slots, fused) one or two column groups,
     # including step counts that leave a ragged last step (K/128 = 1, 3, 9,
     # 76 chunks) and grids of a single workgroup: exact-integer inputs stay
     # bit-exact, fused quantization stays within tolerance of the oracle and
@@ -314,13 +314,14 @@ def test_gemv_every_launch_shape(N, K):
     ref_c = O.quant_linear(x, cq, cs, group_k=K, bn=1, bk=K)
     ref_bc = O.quant_linear(x, cq, cs, group_k=128, bn=1, bk=K)
     try:
-        for ks in (1, 2, 4, 8):
+        for ks, groups in ((1, 1), (2, 1), (4, 1), (4, 2), (8, 1)):
             for waves in (4, 5, 8, 10):
                 for u in (1, 2):
                     T.TUNE["gemv_ks"] = ks
                     T.TUNE["gemv_waves"] = waves
                     T.TUNE["gemv_u"] = u
-                    cfg = (ks, waves, u)
+                    T.TUNE["gemv_groups"] = groups
+                    cfg = (ks, waves, u, groups)
                     c, _, _ = run_linear(qw, sw, None, M=1, N=N, K=K, skip_quant=True,
                                          q_ws=dev(qa.reshape(-1)), s_ws=dev(sa))
                     assert HK.last_kernel() == "fp8_gemv_m1"
