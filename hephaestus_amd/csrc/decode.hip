@@ -59,18 +59,10 @@ __device__ __forceinline__ float block_sum256(float v, float* s)
 
 // Sum over the 64 lanes of a wave, folded as v[l] += v[l + h] for
 // h = 32, 16, ..., 1; the result is lane 0's.
-__device__ __forceinline__ float wave_sum64(float v)
-{
-    for (int h = 32; h > 0; h >>= 1) v += __shfl_down(v, h, 64);
-    return __shfl(v, 0, 64);
-}
+__device__ __forceinline__ float wave_sum64(float v) { return wave_fold_sum64(v); }
 
 // Max over the 64 lanes of a wave (exact in any order), in every lane.
-__device__ __forceinline__ float wave_max64(float v)
-{
-    for (int h = 32; h > 0; h >>= 1) v = fmaxf(v, __shfl_xor(v, h, 64));
-    return v;
-}
+__device__ __forceinline__ float wave_max64(float v) { return wave_fold_max64(v); }
 
 // A token id outside [0, vocab) gives a zero row instead of a read past
 // the table (the host cannot see device-side ids).
@@ -267,6 +259,13 @@ __device__ __forceinline__ void decode16(const uint4& w, float* f)
 // split's scores are read back on the XCD (L2) that wrote them. The CPU
 // restatement repeats every order above.
 constexpr int kAttnSplit = 128;
+// Keys per thread of the scores and values kernels: the split's 128 keys
+// sit in 128 / kAttnKPT key slots of 8 lanes, a workgroup of 1024 /
+// kAttnKPT threads. The summation orders (and the CPU restatement) follow
+// kAttnKPT = 4; 2 (eight waves, half the work each) measured slower on
+// MI355X (20.9 against 20.4 us for the three launches at 4097 keys): the
+// VALU work per SIMD is the same and one workgroup already sits on each CU.
+constexpr int kAttnKPT = 4;
 
 struct AttnWs {
     float* scores;   // [n_heads][n_keys]
@@ -342,21 +341,28 @@ struct QkvPrep {
 // q heads and the new key's codes meet in LDS after one barrier, and the
 // new key's score uses those codes instead of the cache row loaded at the
 // start. All of it runs while the cache loads are in flight.
-template <int G, bool QKV>
-__global__ __launch_bounds__(256) void attn_scores_kernel(
+template <int G, bool QKV, int KPT>
+__global__ __launch_bounds__(1024 / KPT) void attn_scores_kernel(
     float* ws, const uint16_t* q, const uint8_t* kc, const float* kv_scale, int n_kv,
     int n_keys, int n_splits, QkvPrep prep)
 {
     constexpr int D = 128;
+    constexpr int SLOTS = kAttnSplit / KPT, NW = SLOTS / 8;   // key slots, waves
     const int kh = blockIdx.x % n_kv, split = blockIdx.x / n_kv;
     const int t = threadIdx.x, ks = t >> 3, c = t & 7;
     const AttnWs w = attn_ws(ws, n_kv * G, n_keys, n_splits);
     const size_t row = (size_t)n_kv * D;
     const int j0 = split * kAttnSplit + ks;
-    uint4 kv[4];
+    // The cache rows go out after the loads of q (or of the raw projection
+    // row and the norm gammas): a wave's loads complete in issue order, and
+    // the q preparation, which needs only those, then runs while the cache
+    // rows are in flight.
+    uint4 kv[KPT];
+    auto load_keys = [&]() {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        kv[i] = ldg16u(kc + (size_t)min(j0 + 32 * i, n_keys - 1) * row + kh * D + 16 * c);
+        for (int i = 0; i < KPT; ++i)
+            kv[i] = ldg16u(kc + (size_t)min(j0 + SLOTS * i, n_keys - 1) * row + kh * D + 16 * c);
+    };
     float qv[G][16];
     if constexpr (QKV) {
         // normalized heads: items 0..G-1 the q heads kh*G + g, item G the
@@ -364,7 +370,7 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
         // waves; a wave's heads fold their sums of squares together (the
         // same per-head order as wave_sum64). The new key's v row is
         // quantized one element per thread.
-        constexpr int NI = (G + 1 + 3) / 4;
+        constexpr int NI = (G + 1 + NW - 1) / NW;
         __shared__ __attribute__((aligned(16))) uint16_t qs[G][D];
         __shared__ __attribute__((aligned(16))) uint8_t knew[D];
         const int wave = t >> 6, l = t & 63;
@@ -377,7 +383,7 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
         float xa[NI], xb[NI], ga[NI], gb[NI];
 #pragma unroll
         for (int k = 0; k < NI; ++k) {
-            const int it = wave + 4 * k;
+            const int it = wave + NW * k;
             xa[k] = xb[k] = ga[k] = gb[k] = 0.0f;
             if (it < items) {
                 const int h = it < G ? kh * G + it : prep.n_heads + kh;
@@ -389,6 +395,7 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
                 gb[k] = f32_of_bf16(gm[l + 64]);
             }
         }
+        load_keys();
         float cs, sn;
         if (prep.rope) {
             cs = bf16lo(rcs);
@@ -398,17 +405,14 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
         }
         float ss[NI];
 #pragma unroll
-        for (int k = 0; k < NI; ++k) ss[k] = __builtin_fmaf(xb[k], xb[k], xa[k] * xa[k]);
-        for (int h = 32; h > 0; h >>= 1) {
-#pragma unroll
-            for (int k = 0; k < NI; ++k) ss[k] += __shfl_down(ss[k], h, 64);
-        }
+        for (int k = 0; k < NI; ++k)
+            ss[k] = wave_sum64(__builtin_fmaf(xb[k], xb[k], xa[k] * xa[k]));
 #pragma unroll
         for (int k = 0; k < NI; ++k) {
-            const int it = wave + 4 * k;
+            const int it = wave + NW * k;
             if (it >= items) break;
             float a = xa[k], b = xb[k];
-            head_finish(a, b, ga[k], gb[k], cs, sn, prep.eps, __shfl(ss[k], 0, 64));
+            head_finish(a, b, ga[k], gb[k], cs, sn, prep.eps, ss[k]);
             if (it < G) {
                 qs[it][l] = f32_to_bf16(a);
                 qs[it][l + 64] = f32_to_bf16(b);
@@ -438,14 +442,22 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
         // just computed, not the cache row read before they were written
         if (last) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (j0 + 32 * i >= n_keys - 1) kv[i] = *reinterpret_cast<const uint4*>(&knew[16 * c]);
+            for (int i = 0; i < KPT; ++i)
+                if (j0 + SLOTS * i >= n_keys - 1)
+                    kv[i] = *reinterpret_cast<const uint4*>(&knew[16 * c]);
         }
     } else {
+        uint4 qa[G], qb[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const uint16_t* qp = q + (size_t)(kh * G + g) * D + 16 * c;
-            const uint4 a = ldg16u(qp), b = ldg16u(qp + 8);
+            qa[g] = ldg16u(qp);
+            qb[g] = ldg16u(qp + 8);
+        }
+        load_keys();
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const uint4 a = qa[g], b = qb[g];
             const uint32_t d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -455,9 +467,9 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
         }
     }
     const float qk_scale = kv_scale[kh] * 0.08838834764831845f;   // sk * f32(1/sqrt(128))
-    float sc[4][G];
+    float sc[KPT][G];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < KPT; ++i) {
         float k16[16];
         decode16(kv[i], k16);
 #pragma unroll
@@ -472,23 +484,23 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
         }
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int j = j0 + 32 * i;
+    for (int i = 0; i < KPT; ++i) {
+        const int j = j0 + SLOTS * i;
 #pragma unroll
         for (int g = 0; g < G; ++g)
             if (c == g && j < n_keys) w.scores[(size_t)(kh * G + g) * n_keys + j] = sc[i][g];
     }
     // split max and sum of exp(s - m_s): within a wave over its 8 key slots
-    // (all 8 lanes of a slot hold its scores), then over the 4 waves in LDS
-    __shared__ float wst[2][4][G];
+    // (all 8 lanes of a slot hold its scores), then over the NW waves in LDS
+    __shared__ float wst[2][NW][G];
     const int wave = t >> 6;
     float mw[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         float m = -3.4e38f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (j0 + 32 * i < n_keys) m = fmaxf(m, sc[i][g]);
+        for (int i = 0; i < KPT; ++i)
+            if (j0 + SLOTS * i < n_keys) m = fmaxf(m, sc[i][g]);
         mw[g] = slots_reduce<true>(m);
     }
     if ((t & 63) == 0) {
@@ -499,11 +511,13 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
     float aw[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const float m = fmaxf(fmaxf(wst[0][0][g], wst[0][1][g]), fmaxf(wst[0][2][g], wst[0][3][g]));
+        float m = wst[0][0][g];
+#pragma unroll
+        for (int v = 1; v < NW; ++v) m = fmaxf(m, wst[0][v][g]);
         float a = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (j0 + 32 * i < n_keys) a += expf(sc[i][g] - m);
+        for (int i = 0; i < KPT; ++i)
+            if (j0 + SLOTS * i < n_keys) a += expf(sc[i][g] - m);
         aw[g] = slots_reduce<false>(a);
         if (t == g) w.smax[(size_t)(kh * G + g) * n_splits + split] = m;
     }
@@ -512,49 +526,66 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
         for (int g = 0; g < G; ++g) wst[1][wave][g] = aw[g];
     }
     __syncthreads();
-    if (t < G)
-        w.ssum[(size_t)(kh * G + t) * n_splits + split] =
-            ((wst[1][0][t] + wst[1][1][t]) + wst[1][2][t]) + wst[1][3][t];
+    if (t < G) {
+        float l = wst[1][0][t];
+#pragma unroll
+        for (int v = 1; v < NW; ++v) l += wst[1][v][t];
+        w.ssum[(size_t)(kh * G + t) * n_splits + split] = l;
+    }
 }
 
-template <int G>
-__global__ __launch_bounds__(256) void attn_pv_kernel(float* ws, const uint8_t* vc, int n_kv,
-                                                      int n_keys, int n_splits)
+template <int G, int KPT>
+__global__ __launch_bounds__(1024 / KPT) void attn_pv_kernel(float* ws, const uint8_t* vc,
+                                                            int n_kv, int n_keys, int n_splits)
 {
     constexpr int D = 128;
+    constexpr int NT = 1024 / KPT, SLOTS = kAttnSplit / KPT, NW = SLOTS / 8;
     const int kh = blockIdx.x % n_kv, split = blockIdx.x / n_kv;
     const int t = threadIdx.x, ks = t >> 3, c = t & 7, wave = t >> 6;
     const AttnWs w = attn_ws(ws, n_kv * G, n_keys, n_splits);
     const size_t row = (size_t)n_kv * D;
     const int j0 = split * kAttnSplit + ks;
 
-    // this thread's V rows and scores go out first
-    uint4 vv[4];
-    float sj[4][G];
+    // Loads in the order their data is needed: a wave's loads complete in
+    // issue order, so the split statistics and this thread's scores (written
+    // by the scores kernel, near in the cache hierarchy) go out before the V
+    // rows (HBM), and the statistics and probabilities are worked out while
+    // the V rows are in flight. Up to 64 splits (8192 keys) lane l holds
+    // split l's max and sum.
+    const int l = t & 63;
+    float ms[G], ls[G];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int j = min(j0 + 32 * i, n_keys - 1);
-        vv[i] = ldg16u(vc + (size_t)j * row + kh * D + 16 * c);
+    for (int g = 0; g < G; ++g) {
+        const size_t base = (size_t)(kh * G + g) * n_splits;
+        ms[g] = l < n_splits ? w.smax[base + l] : -3.4e38f;
+        ls[g] = l < n_splits ? w.ssum[base + l] : 0.0f;
+    }
+    float sj[KPT][G];
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+        const int j = min(j0 + SLOTS * i, n_keys - 1);
 #pragma unroll
         for (int g = 0; g < G; ++g) sj[i][g] = w.scores[(size_t)(kh * G + g) * n_keys + j];
+    }
+    uint4 vv[KPT];
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+        const int j = min(j0 + SLOTS * i, n_keys - 1);
+        vv[i] = ldg16u(vc + (size_t)j * row + kh * D + 16 * c);
     }
 
     // global max and sum per head from the split statistics, computed by
     // every wave on its own (no barrier): lane l takes splits l, l + 64, ...
     // (sum: fma in that order), the max over all lanes, the sum folded as
-    // v[l] += v[l + h], h = 32 .. 1. Up to 64 splits (8192 keys) a lane
-    // holds one split: its max and sum are read together, one round trip
+    // v[l] += v[l + h], h = 32 .. 1
     float mloc[G], inv[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         const size_t base = (size_t)(kh * G + g) * n_splits;
-        const int l = t & 63;
         float m = -3.4e38f, a = 0.0f;
         if (n_splits <= 64) {
-            const float ms = l < n_splits ? w.smax[base + l] : -3.4e38f;
-            const float ls = l < n_splits ? w.ssum[base + l] : 0.0f;
-            m = wave_max64(ms);
-            if (l < n_splits) a = __builtin_fmaf(ls, expf(ms - m), 0.0f);
+            m = wave_max64(ms[g]);
+            if (l < n_splits) a = __builtin_fmaf(ls[g], expf(ms[g] - m), 0.0f);
         } else {
             for (int s = l; s < n_splits; s += 64) m = fmaxf(m, w.smax[base + s]);
             m = wave_max64(m);
@@ -572,10 +603,10 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(float* ws, const uint8_t* 
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[g][e] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < KPT; ++i) {
         float v16[16];
         decode16(vv[i], v16);
-        const bool live = j0 + 32 * i < n_keys;
+        const bool live = j0 + SLOTS * i < n_keys;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const float pj = live ? round_bf16(expf(sj[i][g] - mloc[g]) * inv[g]) : 0.0f;
@@ -592,7 +623,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(float* ws, const uint8_t* 
     // holds the 4G sums o = 8G * (row & 1) + 4G * (lane >= 32) + i, i < 4G,
     // of the flattened (head, dim) index g * 16 + e: a third of the
     // cross-lane work of reducing every value everywhere, same sums.
-    __shared__ float wsum[4][G][D];
+    __shared__ float wsum[NW][G][D];
     if constexpr (G >= 4) {
         constexpr int V = 16 * G;
         float* f = &acc[0][0];
@@ -634,9 +665,11 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(float* ws, const uint8_t* 
         }
     }
     __syncthreads();
-    for (int o = t; o < G * D; o += 256) {
+    for (int o = t; o < G * D; o += NT) {
         const int g = o / D, d = o % D;
-        const float r = ((wsum[0][g][d] + wsum[1][g][d]) + wsum[2][g][d]) + wsum[3][g][d];
+        float r = wsum[0][g][d];
+#pragma unroll
+        for (int v = 1; v < NW; ++v) r += wsum[v][g][d];
         w.partial[((size_t)(kh * G + g) * n_splits + split) * D + d] = r;
     }
 }
@@ -751,13 +784,14 @@ hipError_t launch_attention(uint16_t* out, const uint16_t* q, const uint8_t* kc,
 {
     const int splits = (n_keys + kAttnSplit - 1) / kAttnSplit;
     const int blocks = n_kv * splits;
+    constexpr int NT = 1024 / kAttnKPT;
     if (prep.qkv)
-        attn_scores_kernel<G, true><<<blocks, 256, 0, s>>>(ws, q, kc, kv_scale, n_kv, n_keys,
-                                                          splits, prep);
+        attn_scores_kernel<G, true, kAttnKPT><<<blocks, NT, 0, s>>>(ws, q, kc, kv_scale, n_kv,
+                                                                   n_keys, splits, prep);
     else
-        attn_scores_kernel<G, false><<<blocks, 256, 0, s>>>(ws, q, kc, kv_scale, n_kv, n_keys,
-                                                           splits, prep);
-    attn_pv_kernel<G><<<blocks, 256, 0, s>>>(ws, vc, n_kv, n_keys, splits);
+        attn_scores_kernel<G, false, kAttnKPT><<<blocks, NT, 0, s>>>(ws, q, kc, kv_scale, n_kv,
+                                                                    n_keys, splits, prep);
+    attn_pv_kernel<G, kAttnKPT><<<blocks, NT, 0, s>>>(ws, vc, n_kv, n_keys, splits);
     attn_combine_kernel<<<n_kv * G, 128, 0, s>>>(out, ws, kv_scale, n_kv * G, n_kv, n_keys, splits);
     return hipGetLastError();
 }

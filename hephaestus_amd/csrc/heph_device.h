@@ -172,6 +172,42 @@ __device__ __forceinline__ i32x4 ldg16(const void* p)
     return *reinterpret_cast<const i32x4*>(p);
 }
 
+// The fold v[l] += v[l + h], h = 32, 16, ..., 1, over the 64 lanes of a
+// wave, lane 0's result broadcast. Every level stays in the VALU: h = 32
+// and 16 by v_permlane32_swap / v_permlane16_swap (lane l < h receives lane
+// l + h), 8 and 4 by DPP row_ror (within a 16-lane row, lane l < h reads
+// lane l + h), 2 and 1 by DPP quad_perm (lane l ^ h). Lane 0 forms exactly
+// the sums the fold's lane 0 forms (float addition commutes), without the
+// LDS round trip of each level that ds_bpermute (__shfl_down) takes.
+__device__ __forceinline__ float wave_fold_sum64(float v)
+{
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+}
+
+// Max over the 64 lanes of a wave (exact in any order), in every lane: the
+// same six exchanges; each level leaves equal values in the lanes the next
+// one pairs, so every lane ends with the maximum.
+__device__ __forceinline__ float wave_fold_max64(float v)
+{
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false)));
+    return v;
+}
+
 // RMSNorm's sum of squares over one row: thread t < 256 of the workgroup
 // brings v = its fma chain over elements t, t + 256, ...; the 256 sums are
 // folded as s[t] += s[t + h] for h = 128, 64, ..., 1, the first two levels
@@ -184,9 +220,9 @@ __device__ __forceinline__ float fold256_wave0(float v, float* red, float* out)
     if (t < 256) red[t] = v;
     __syncthreads();
     if (t < 64) {
-        float a = (red[t] + red[t + 128]) + (red[t + 64] + red[t + 192]);
-        for (int h = 32; h > 0; h >>= 1) a += __shfl_down(a, h, 64);
-        if (t == 0) *out = a;
+        const float a = (red[t] + red[t + 128]) + (red[t + 64] + red[t + 192]);
+        const float r = wave_fold_sum64(a);
+        if (t == 0) *out = r;
     }
     __syncthreads();
     return *out;
@@ -200,9 +236,8 @@ __device__ __forceinline__ float fold256_every_wave(float v, float* red)
     const int t = threadIdx.x, l = t & 63;
     if (t < 256) red[t] = v;
     __syncthreads();
-    float a = (red[l] + red[l + 128]) + (red[l + 64] + red[l + 192]);
-    for (int h = 32; h > 0; h >>= 1) a += __shfl_down(a, h, 64);
-    return __shfl(a, 0, 64);
+    const float a = (red[l] + red[l + 128]) + (red[l + 64] + red[l + 192]);
+    return wave_fold_sum64(a);
 }
 
 // sqrt(a) rounded to nearest, for the RMS factors. __fsqrt_rn compiles to
