@@ -47,7 +47,7 @@ class LaunchOverrides(ctypes.Structure):
                 ("gemv_u", ctypes.c_int), ("gemm_bm", ctypes.c_int),
                 ("batch_split", ctypes.c_int), ("wide_tiles", ctypes.c_int),
                 ("wide_waves", ctypes.c_int), ("split_spin_limit", ctypes.c_int),
-                ("gemv_groups", ctypes.c_int)]
+                ("gemv_groups", ctypes.c_int), ("gemm_bn", ctypes.c_int)]
 
 
 _vp = ctypes.c_void_p

@@ -138,6 +138,9 @@ int take_overrides(const heph_launch_overrides* ov, Tuning* t)
     if (ov->split_spin_limit < -1) return HEPH_ERR_FLAGS;
     if (ov->gemv_groups != 0 && ov->gemv_groups != 1 && ov->gemv_groups != 2)
         return HEPH_ERR_FLAGS;
+    if (ov->gemm_bn != 0 && ov->gemm_bn != 192 && ov->gemm_bn != 256 && ov->gemm_bn != 320)
+        return HEPH_ERR_FLAGS;
+    t->gemm_bn = ov->gemm_bn;
     t->split_spin_limit = ov->split_spin_limit;
     t->gemv_groups = ov->gemv_groups;
     t->wide_tiles = wt;

@@ -246,38 +246,44 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8Operands op)
 // 16-byte row pieces. f32 output or a residual: staged in f32, BM/2 rows at
 // a time, the residual added before the one rounding.
 namespace {
-constexpr int L_BN = 256, L_WN = 64, L_NT = L_WN / 16;
-constexpr int L_STAGE_B = L_BN * kChunk;
 
 // Tile height BM in {64, 128, 192, 256}: the 8 waves form a 2 x 4 grid of
 // (BM/2) x 64 wave tiles. A smaller BM trades MFMA work per chunk for a
 // tile count that fills the CUs (e.g. 220 tiles of 192 x 256 instead of
 // 160 of 256 x 256 at M = 4096, N = 2560).
-template <int BM>
+template <int BM, int BN>
 struct BigTile {
     static_assert(BM == 64 || BM == 128 || BM == 192 || BM == 256, "tile height");
-    static constexpr int WM = BM / 2, MT = WM / 16;
-    static constexpr int STAGE_A = BM * kChunk, STAGE_S = BM * 4;
-    static constexpr int STAGE = STAGE_A + L_STAGE_B + STAGE_S;
+    static_assert(BN == 192 || BN == 256 || BN == 320, "tile width");
+    // 8 waves in a 2 x 4 grid of WM x WN wave tiles, MT x NT MFMA blocks
+    static constexpr int WM = BM / 2, MT = WM / 16, WN = BN / 4, NT = WN / 16;
+    // B rows (DMA instructions of 8 rows) per wave
+    static constexpr int NBP = BN / 64;
+    // the WN columns of every wave lie in one 128-column weight block
+    static constexpr bool ONE_BLOCK = 128 % WN == 0 && BN % WN == 0;
+    static constexpr int STAGE_A = BM * kChunk, STAGE_B = BN * kChunk, STAGE_S = BM * 4;
+    static constexpr int STAGE = STAGE_A + STAGE_B + STAGE_S;
     // LDS stages. A short chunk is below the loaded HBM latency, so where
-    // LDS allows, the DMA runs two chunks ahead: three whole stages at 64
-    // and 128 rows (149 KB at 128); at 192 rows two A/scale stages and
-    // three B stages (149 KB: the weights, streamed from HBM in a real
-    // prefill, get the extra chunk); at 256 rows two stages (133 KB).
-    static constexpr bool SPLIT_B = BM == 192;
-    static constexpr int NS = BM <= 128 ? 3 : 2;    // A and row-scale stages
-    static constexpr int NB = SPLIT_B ? 3 : NS;      // B stages
+    // LDS allows, the DMA runs two chunks ahead: three whole stages (64 and
+    // 128 rows by 256 columns); else two A/scale stages and three B stages
+    // (the weights, streamed from HBM in a real prefill, get the extra
+    // chunk: 192 x 256, 256 x 192, 128 x 320); else two (256 x 256).
+    static constexpr int kLds = 160 * 1024;
+    static constexpr bool FULL3 = 3 * STAGE <= kLds;
+    static constexpr bool SPLIT_B = !FULL3 && 2 * (STAGE_A + STAGE_S) + 3 * STAGE_B <= kLds;
+    static constexpr int NS = FULL3 ? 3 : 2;                  // A and row-scale stages
+    static constexpr int NB = FULL3 || SPLIT_B ? 3 : 2;       // B stages
     static constexpr int BYTES =
-        SPLIT_B ? 2 * STAGE_A + 2 * STAGE_S + 3 * L_STAGE_B : NS * STAGE;
+        SPLIT_B ? 2 * STAGE_A + 2 * STAGE_S + 3 * STAGE_B : NS * STAGE;
     // Byte offsets of A, B and row-scale stage k.
     static constexpr int a_at(int k) { return SPLIT_B ? k * STAGE_A : k * STAGE; }
     static constexpr int s_at(int k)
     {
-        return SPLIT_B ? 2 * STAGE_A + k * STAGE_S : k * STAGE + STAGE_A + L_STAGE_B;
+        return SPLIT_B ? 2 * STAGE_A + k * STAGE_S : k * STAGE + STAGE_A + STAGE_B;
     }
     static constexpr int b_at(int k)
     {
-        return SPLIT_B ? 2 * STAGE_A + 2 * STAGE_S + k * L_STAGE_B : k * STAGE + STAGE_A;
+        return SPLIT_B ? 2 * STAGE_A + 2 * STAGE_S + k * STAGE_B : k * STAGE + STAGE_A;
     }
 };
 
@@ -310,10 +316,17 @@ __device__ __forceinline__ void dma4(rsrc_t r, uint32_t voff, uint32_t soff, voi
 // of the next chunk may stay in flight).
 __device__ __forceinline__ void wait_stage(int n)
 {
-    if (n == 9) __builtin_amdgcn_s_waitcnt(0x0079);
-    else if (n == 8) __builtin_amdgcn_s_waitcnt(0x0078);
-    else if (n == 4) __builtin_amdgcn_s_waitcnt(0x0074);
-    else __builtin_amdgcn_s_waitcnt(0x0070);
+    switch (n) {
+    case 10: __builtin_amdgcn_s_waitcnt(0x007A); break;
+    case 9: __builtin_amdgcn_s_waitcnt(0x0079); break;
+    case 8: __builtin_amdgcn_s_waitcnt(0x0078); break;
+    case 7: __builtin_amdgcn_s_waitcnt(0x0077); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0x0076); break;
+    case 5: __builtin_amdgcn_s_waitcnt(0x0075); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0x0074); break;
+    case 3: __builtin_amdgcn_s_waitcnt(0x0073); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0070); break;
+    }
     asm volatile("" ::: "memory");
 }
 // Workgroup barrier after wait_stage: every wave's DMA into the stage about
@@ -346,11 +359,13 @@ __device__ __forceinline__ uint32_t pack_bf16_hw(float a, float b)
 // as bf16 for coalesced 16-byte stores; f32 output or a residual in two
 // f32 passes (the residual added before the one rounding). Every thread of
 // the workgroup calls it; LDS_BYTES of smem are free to reuse.
-template <int SM, int BM, int LDS_BYTES>
-__device__ __forceinline__ void big_epilogue(const Fp8Operands& op, f32x4 (&acc)[BM / 32][L_NT],
-                                             uint8_t* smem, int m0, int n0, int split, int S)
+template <int SM, int BM, int BN, int LDS_BYTES>
+__device__ __forceinline__ void big_epilogue(const Fp8Operands& op,
+                                             f32x4 (&acc)[BM / 32][BN / 64], uint8_t* smem,
+                                             int m0, int n0, int split, int S)
 {
     constexpr int L_BM = BM, L_WM = BM / 2, L_MT = BM / 32;
+    constexpr int L_BN = BN, L_WN = BN / 4, L_NT = BN / 64;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -380,9 +395,10 @@ __device__ __forceinline__ void big_epilogue(const Fp8Operands& op, f32x4 (&acc)
     }
     if (!op.residual && !op.c_f32) {
         // bf16 output: the whole tile goes through LDS once as bf16, rows
-        // padded to 520 bytes (130 dwords: consecutive rows 2 banks apart),
-        // each lane writing 8 bytes per block; then 16-byte coalesced stores.
-        constexpr int RB = 520;
+        // padded by 8 bytes (2 BN + 8: 130 dwords at 256 columns, consecutive
+        // rows 2 banks apart), each lane writing 8 bytes per block; then
+        // 16-byte coalesced stores.
+        constexpr int RB = 2 * L_BN + 8;
         static_assert(L_BM * RB <= LDS_BYTES, "bf16 tile must fit the stage buffers");
         __syncthreads();
 #pragma unroll
@@ -435,7 +451,7 @@ __device__ __forceinline__ void big_epilogue(const Fp8Operands& op, f32x4 (&acc)
                     *reinterpret_cast<f32x4*>(cw + mi * 16 * CST + ni * 16) = acc[mi][ni];
         }
         __syncthreads();
-        // L_WM rows x 256 cols: each thread writes 8 consecutive outputs
+        // L_WM rows x L_BN cols: each thread writes 8 consecutive outputs
         for (int e = tid; e < L_WM * (L_BN / 8); e += 512) {
             const int r = e / (L_BN / 8);
             const int c8 = (e % (L_BN / 8)) * 8;
@@ -481,12 +497,12 @@ __device__ __forceinline__ void big_epilogue(const Fp8Operands& op, f32x4 (&acc)
     }
 }
 
-template <int SM, int BM>
+template <int SM, int BM, int BN>
 __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
 {
-    using T = BigTile<BM>;
+    using T = BigTile<BM, BN>;
     constexpr int L_BM = BM, L_WM = T::WM, L_MT = T::MT;
-    constexpr int L_STAGE_A = T::STAGE_A, L_STAGE = T::STAGE;
+    constexpr int L_BN = BN, L_WN = T::WN, L_NT = T::NT, NBP = T::NBP;
     // With three stages, chunk j + 2's DMA goes out in chunk j: a chunk
     // (~0.8 us at 64 rows, ~1.3 us at 192) is below the loaded HBM latency,
     // and weights that are not in the Infinity Cache (each layer of a real
@@ -516,32 +532,34 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     tile_of_block(blockIdx.x - split * tiles, tiles_m, tiles_n, &tm, &tn);
     const int m0 = tm * L_BM, n0 = tn * L_BN;
 
-    // DMA sources: wave w moves operand rows [32w, 32w+32) of A and of B
-    // (4 instructions each); lane i covers row 8q + (i >> 3) of block q and
-    // global piece (i & 7) ^ (row & 7). Rows past M (N) are clamped to the
-    // last row: they feed output rows (columns) that are never stored. Each
-    // lane keeps one 32-bit byte offset per block and operand; chunk j adds
-    // the scalar offset 128 * j.
+    // DMA sources: wave w moves operand rows [32w, 32w+32) of A (4
+    // instructions) and [8 NBP w, 8 NBP (w+1)) of B (NBP = BN / 64
+    // instructions); lane i covers row 8q + (i >> 3) of block q and global
+    // piece (i & 7) ^ (row & 7). Rows past M (N) are clamped to the last
+    // row: they feed output rows (columns) that are never stored. Each lane
+    // keeps one 32-bit byte offset per block and operand; chunk j adds the
+    // scalar offset 128 * j.
     const rsrc_t rq = make_rsrc(op.q), rw = make_rsrc(op.w), rs = make_rsrc(op.s);
     const int lr = lane >> 3;
     const int piece = ((lane & 7) ^ lr) * 16;     // rows 8q + lr share r & 7 = lr
-    uint32_t aoff[4], boff[4];
+    uint32_t aoff[4], boff[NBP];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int r = wave * 32 + q * 8 + lr;
-        aoff[q] = (uint32_t)min(m0 + r, M - 1) * (uint32_t)K + piece;
-        boff[q] = (uint32_t)min(n0 + r, N - 1) * (uint32_t)K + piece;
-    }
+    for (int q = 0; q < 4; ++q)
+        aoff[q] = (uint32_t)min(m0 + wave * 32 + q * 8 + lr, M - 1) * (uint32_t)K + piece;
+#pragma unroll
+    for (int q = 0; q < NBP; ++q)
+        boff[q] = (uint32_t)min(n0 + wave * 8 * NBP + q * 8 + lr, N - 1) * (uint32_t)K + piece;
     const uint32_t soff = (uint32_t)min(m0 + wave * 64 + lane, M - 1) * (uint32_t)op.s_ld * 4u;
     const uint32_t s_step = (uint32_t)op.s_step * 4u;
 
-    // DMA instruction `part` (0..8) of this wave: parts 0-3 move A rows of
-    // chunk ja into A stage abuf, then 4-7 B rows of chunk jw into B stage
-    // bbuf and 8 the row scales of chunk ja; with separate B stages the row
-    // scales come fourth (part 4) and the B rows last (5-8), so that the
-    // next chunk's wait can leave exactly the four B instructions in flight.
-    constexpr int kParts = 9;
-    constexpr int kFirstB = SPLIT_B ? 5 : 4, kScalePart = SPLIT_B ? 4 : 8;
+    // DMA instruction `part` (0 .. 4 + NBP) of this wave: parts 0-3 move A
+    // rows of chunk ja into A stage abuf, then NBP parts B rows of chunk jw
+    // into B stage bbuf and the last the row scales of chunk ja; with
+    // separate B stages the row scales come fourth (part 4) and the B rows
+    // last, so that the next chunk's wait can leave exactly the NBP B
+    // instructions in flight.
+    constexpr int kParts = 5 + NBP;
+    constexpr int kFirstB = SPLIT_B ? 5 : 4, kScalePart = SPLIT_B ? 4 : 4 + NBP;
     // DMA parts per row tile (MI355X: 2 over the first five of 8 row tiles,
     // 3 over the first three of 6 or 4, fewest cycles per chunk; 5 and 4
     // over the 2 row tiles of BM = 64, so that every part goes out)
@@ -559,7 +577,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
         } else {
             const int q = part - kFirstB;
             dma16(rw, boff[q], (uint32_t)jw * kChunk,
-                  smem + T::b_at(bbuf) + (wave * 32 + q * 8) * kChunk);
+                  smem + T::b_at(bbuf) + (wave * 8 * NBP + q * 8) * kChunk);
         }
     };
 
@@ -574,10 +592,15 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
             swc[ni][e] = SM == 1 ? op.sw[n] : 0.0f;
         }
     // A wave whose columns all lie past N still reads a valid scale row
-    // (its results are never stored). The row is uniform per wave: the
-    // block scales are scalar loads.
-    const int wblk = min((n0 + wn * L_WN) >> 7, (N - 1) >> 7);
-    const const_f32_ptr swb = (const_f32_ptr)(op.sw + (size_t)wblk * op.sw_ld);
+    // (its results are never stored). The rows are uniform per wave: the
+    // block scales are scalar loads. Where a wave's columns span two
+    // 128-column blocks (WN = 48 or 80), each 16-column block ni has its own.
+    constexpr int NSW = T::ONE_BLOCK ? 1 : L_NT;
+    const_f32_ptr swb[NSW];
+#pragma unroll
+    for (int k = 0; k < NSW; ++k)
+        swb[k] = (const_f32_ptr)(op.sw + (size_t)min((n0 + wn * L_WN + k * 16) >> 7, (N - 1) >> 7) *
+                                             op.sw_ld);
 
     // Per-lane LDS byte offsets inside a stage: fragment rows of A and B at
     // the two 16-byte slots this lane reads, and the row scale.
@@ -592,7 +615,12 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
 #pragma unroll
         for (int ni = 0; ni < L_NT; ++ni) acc[mi][ni] = f32x4{0, 0, 0, 0};
 
-    float sw_cur = SM == 0 ? swb[jb] : 1.0f, sw_nxt = 1.0f;
+    float sw_cur[NSW], sw_nxt[NSW];
+#pragma unroll
+    for (int k = 0; k < NSW; ++k) {
+        sw_cur[k] = SM == 0 ? swb[k][jb] : 1.0f;
+        sw_nxt[k] = 1.0f;
+    }
 
     // Software pipeline over the row tiles of a wave: the MFMAs of tile mi
     // run while the rescale FMAs of tile mi - 1 execute and the A fragment
@@ -601,19 +629,20 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     // live across the barrier.
     static_assert(L_MT % 2 == 0, "row tiles per wave must be even");
     f32x4 p[2][L_NT];
-    float sc[2] = {0.0f, 0.0f};
+    float sc[2][NSW] = {};
     auto rescale = [&](int mi, int slot) {
 #pragma unroll
         for (int ni = 0; ni < L_NT; ++ni) {
+            const float s = sc[slot][NSW == 1 ? 0 : ni];
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                acc[mi][ni][e] += p[slot][ni][e] * (SM == 0 ? sc[slot] : sc[slot] * swc[ni][e]);
+                acc[mi][ni][e] += p[slot][ni][e] * (SM == 0 ? s : s * swc[ni][e]);
             pin(acc[mi][ni]);
         }
     };
 
     // DMA instructions a wave issues per chunk (A rows, B rows, row scales).
-    const int n_parts = (wave * 32 < L_BM ? 4 : 0) + 4 + (SM != 2 && wave * 64 < L_BM ? 1 : 0);
+    const int n_parts = (wave * 32 < L_BM ? 4 : 0) + NBP + (SM != 2 && wave * 64 < L_BM ? 1 : 0);
 
     // One 128-wide chunk j held in A stage buf (a compile-time constant)
     // and B stage bst. The wave's nine DMA instructions (A rows and scales
@@ -627,7 +656,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
         // with three stages the newest instructions, the next chunk's DMA
         // (all nine parts, or its four B parts with three B stages), may
         // stay in flight; with two, everything lands
-        wait_stage(NB == 3 && j + 1 < je ? (SPLIT_B ? 4 : n_parts) : 0);
+        wait_stage(NB == 3 && j + 1 < je ? (SPLIT_B ? NBP : n_parts) : 0);
         stage_barrier();
         const bool more = j + 1 < je;
         const int ja = j + NS - 1, jw = j + NB - 1;
@@ -642,15 +671,21 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
         i32x8 b[L_NT];
 #pragma unroll
         for (int ni = 0; ni < L_NT; ++ni) b[ni] = frag(stb, b_row + ni * 16 * kChunk);
-        const float swj = sw_cur;
+        float swj[NSW];
+#pragma unroll
+        for (int k = 0; k < NSW; ++k) swj[k] = sw_cur[k];
         i32x8 a_[2];
         float sa_[2];
         a_[0] = frag(sta, a_row);
         sa_[0] = *reinterpret_cast<const float*>(sts + s_row);
         if constexpr (SM == 0) {
-            if (more) sw_nxt = swb[j + 1];
+            if (more) {
+#pragma unroll
+                for (int k = 0; k < NSW; ++k) sw_nxt[k] = swb[k][j + 1];
+            }
         }
-        sw_cur = sw_nxt;
+#pragma unroll
+        for (int k = 0; k < NSW; ++k) sw_cur[k] = sw_nxt[k];
 #pragma unroll
         for (int mi = 0; mi < L_MT; ++mi) {
             const int cur = mi & 1, prv = cur ^ 1;
@@ -682,7 +717,8 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
                 for (int ni = 0; ni < L_NT; ++ni)
                     acc[mi][ni] = mfma_e4m3(b[ni], a_[cur], acc[mi][ni]);
             } else {
-                sc[cur] = sa_[cur] * swj;
+#pragma unroll
+                for (int k = 0; k < NSW; ++k) sc[cur][k] = sa_[cur] * swj[k];
 #pragma unroll
                 for (int ni = 0; ni < L_NT; ++ni)
                     p[cur][ni] = mfma_e4m3(b[ni], a_[cur], f32x4{0, 0, 0, 0});
@@ -701,7 +737,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
         if (jb + 1 < je) {
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) issue_part(jb, jb + 1, ic<0>{}, 1, kFirstB + q);
+            for (int q = 0; q < NBP; ++q) issue_part(jb, jb + 1, ic<0>{}, 1, kFirstB + q);
         }
     }
     if constexpr (NB == 2) {
@@ -735,7 +771,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm256_kernel(Fp8Operands op)
     }
     if constexpr (SM != 2) rescale(L_MT - 1, (L_MT - 1) & 1);
 
-    big_epilogue<SM, BM, T::BYTES>(op, acc, smem, m0, n0, split, S);
+    big_epilogue<SM, BM, BN, T::BYTES>(op, acc, smem, m0, n0, split, S);
 }
 
 // Sums the K-split partials of the large-M GEMM in split order, adds the
@@ -775,93 +811,101 @@ hipError_t launch_splitk_reduce(const Fp8Operands& op, hipStream_t stream, const
 
 namespace {
 
-template <int BM>
+template <int BM, int BN>
 hipError_t launch_big(const Fp8Operands& op, hipStream_t stream, const LaunchTiming& t)
 {
-    const int tiles = ((op.M + BM - 1) / BM) * ((op.N + L_BN - 1) / L_BN);
+    const int tiles = ((op.M + BM - 1) / BM) * ((op.N + BN - 1) / BN);
     const dim3 grid(tiles * op.splits);
     if (op.splits > 1) {
         // the GEMM carries the start stamp, the reduction the stop stamp
         hipError_t e;
         if (op.w_block)
-            e = launch(fp8_gemm256_kernel<0, BM>, grid, dim3(512), 0, stream,
+            e = launch(fp8_gemm256_kernel<0, BM, BN>, grid, dim3(512), 0, stream,
                        LaunchTiming{t.start, nullptr}, op);
         else
-            e = launch(fp8_gemm256_kernel<1, BM>, grid, dim3(512), 0, stream,
+            e = launch(fp8_gemm256_kernel<1, BM, BN>, grid, dim3(512), 0, stream,
                        LaunchTiming{t.start, nullptr}, op);
         if (e != hipSuccess) return e;
         return launch_splitk_reduce(op, stream, LaunchTiming{nullptr, t.stop});
     }
     if (op.w_block)
-        return launch(fp8_gemm256_kernel<0, BM>, grid, dim3(512), 0, stream, t, op);
+        return launch(fp8_gemm256_kernel<0, BM, BN>, grid, dim3(512), 0, stream, t, op);
     if (op.s_step == 0)
-        return launch(fp8_gemm256_kernel<2, BM>, grid, dim3(512), 0, stream, t, op);
-    return launch(fp8_gemm256_kernel<1, BM>, grid, dim3(512), 0, stream, t, op);
+        return launch(fp8_gemm256_kernel<2, BM, BN>, grid, dim3(512), 0, stream, t, op);
+    return launch(fp8_gemm256_kernel<1, BM, BN>, grid, dim3(512), 0, stream, t, op);
 }
 
 }  // namespace
 
-// Measured cost of one 128-wide chunk per tile height (MI355X shader
-// cycles per wave and chunk, random E4M3 data): a taller tile does more MFMA
-// work per chunk, a shorter one fills the CUs in finer steps. 256, 192 and
-// 128 rows from in-kernel stamps at M = 4096; 64 rows fitted to M = 512
-// timings (its 40 KB of operands a chunk for 2 MFMA row tiles per wave make
-// it bound by operand reads rather than MFMA).
+// Measured cost per tile (MI355X shader cycles at ~1.9 GHz, random E4M3
+// data, weights from HBM): `chunk` per 128-wide chunk and `fixed` per
+// workgroup (prologue, epilogue), fitted to the GEMM-only times of the
+// config-1 shapes at M = 4096 (o_proj and down: one round of tiles each,
+// K = 4096 against 9728); 64 x 256 fitted to M = 512. A bigger tile does
+// more MFMA work per chunk, a smaller one fills the CUs in finer steps: at
+// M = 4096 the fit ranks the tiles as measured on every config-1 shape
+// (qkv 256 x 192 72.6 us against 75.7 at 256 x 256; o_proj 128 x 320 46.5
+// against 47.9 at 192 x 256; gate_up 256 x 256 193.0 against 212.2; down
+// 128 x 320 100.4 against 104.4), and at M = 512 as well (64 x 256 for qkv
+// and, with 3 K splits, o_proj; 128 x 320 for gate_up; 128 x 256 with 6
+// splits for down).
 struct TileCost {
-    int bm;
-    long cycles;
+    int bm, bn;
+    long chunk, fixed;
 };
-constexpr TileCost kTileCost[] = {{256, 2980}, {192, 2400}, {128, 2150}, {64, 1550}};
+constexpr TileCost kTileCost[] = {{256, 256, 2535, 16730}, {256, 192, 2569, 11650},
+                                  {192, 256, 2440, 12930}, {128, 320, 2327, 13880},
+                                  {128, 256, 1734, 9887},  {64, 256, 1550, 7000}};
 
-// Estimated time (us) of the large-M GEMM at tile height bm (chunk cost
-// `cycles`) with s K splits: rounds of (tile, split) workgroups over the
-// CUs (one 512-thread workgroup per CU) times the chunks of a split times
-// the chunk cost at ~1.9 GHz; a split adds the reduction: ~8 us of launch
-// and per-workgroup set-up, and the partials (M*N*4 bytes a split) read
-// back at ~5 TB/s.
-static double gemm_estimate(int M, int N, int K, int bm, long cycles, int s, long cus)
+// Estimated time (us) of the large-M GEMM with tile tc and s K splits:
+// rounds of (tile, split) workgroups over the CUs (one 512-thread
+// workgroup per CU) times a workgroup's cost (its chunks and the fixed
+// part) at ~1.9 GHz; a split adds the reduction: ~8 us of launch and
+// per-workgroup set-up, and the partials (M*N*4 bytes a split) read back
+// at ~5 TB/s.
+static double gemm_estimate(int M, int N, int K, const TileCost& tc, int s, long cus)
 {
-    const long tiles = (long)((M + bm - 1) / bm) * ((N + L_BN - 1) / L_BN);
+    const long tiles = (long)((M + tc.bm - 1) / tc.bm) * ((N + tc.bn - 1) / tc.bn);
     const int KC = K / kChunk;
     const long rounds = (tiles * s + cus - 1) / cus;
-    double t = (double)rounds * ((KC + s - 1) / s) * ((double)cycles / 1900.0);
+    double t = (double)rounds * ((double)((KC + s - 1) / s) * tc.chunk + tc.fixed) / 1900.0;
     if (s > 1) t += 8.0 + (double)s * M * N * 4.0 / 5.0e6;
     return t;
 }
 
-// Tile height and K splits of the large-M GEMM: the pair with the least
-// estimated time, splitting only when allowed, into at most 8 splits of at
-// least 4 chunks; ties go to the taller tile, then to fewer splits. A forced
-// tile height (HEPH_TUNE_GEMM_BM) fixes bm. So M = 4096 runs 256 rows for
-// N = 6144 and 19456 and 192 rows for N = 2560, all unsplit; M = 512 runs
-// qkv in 64 rows, o_proj in 64 rows and 3 splits, gate_up in 192 rows and
-// down in 128 rows and 6 splits.
-GemmPlan gemm_plan(int M, int N, int K, bool can_split, int forced)
+// Tile and K splits of the large-M GEMM: the pair with the least estimated
+// time, splitting only when allowed, into at most 8 splits of at least 4
+// chunks; ties go to the earlier tile of kTileCost, then to fewer splits.
+// A forced tile height (gemm_bm) or width (gemm_bn) keeps only the tiles
+// that have it.
+GemmPlan gemm_plan(int M, int N, int K, bool can_split, int forced_bm, int forced_bn)
 {
     // MI355X's 256 CUs, not the visible count: the plan (and the K-split
     // summation order with it) does not change under a CU mask or partition
     const long cus = kPlanCUs;
     const int KC = K / kChunk;
-    GemmPlan best{0, 1};
+    GemmPlan best{0, 0, 1};
     double best_t = -1.0;
     for (const auto& tc : kTileCost) {
-        if (forced >= 64 && tc.bm != forced) continue;
+        if (forced_bm >= 64 && tc.bm != forced_bm) continue;
+        if (forced_bn && tc.bn != forced_bn) continue;
         for (int s = 1; s <= (can_split ? 8 : 1); ++s) {
             if (s > 1 && KC / s < 4) break;
-            const double t = gemm_estimate(M, N, K, tc.bm, tc.cycles, s, cus);
+            const double t = gemm_estimate(M, N, K, tc, s, cus);
             if (best_t < 0.0 || t < best_t) {
                 best_t = t;
-                best = GemmPlan{tc.bm, s};
+                best = GemmPlan{tc.bm, tc.bn, s};
             }
         }
     }
+    if (best.bm == 0) best = GemmPlan{forced_bm >= 64 ? forced_bm : 256, 256, 1};
     return best;
 }
 
 bool gemm_splits_ready(const Fp8Operands& op)
 {
     if (!op.part || op.s_step == 0) return false;
-    const int s = gemm_plan(op.M, op.N, op.K, true, op.tune.gemm_bm).splits;
+    const int s = gemm_plan(op.M, op.N, op.K, true, op.tune.gemm_bm, op.tune.gemm_bn).splits;
     return s > 1 && op.part_bytes >= (size_t)s * op.M * op.N * 4;
 }
 
@@ -885,22 +929,31 @@ hipError_t launch_fp8_gemm(const Fp8Operands& op, hipStream_t stream,
         // K splits when the caller's scratch holds their partials (block or
         // per-channel weights with per-chunk activation scales).
         Fp8Operands o = op;
-        const GemmPlan plan = gemm_plan(o.M, o.N, o.K, gemm_splits_ready(o), o.tune.gemm_bm);
+        const GemmPlan plan = gemm_plan(o.M, o.N, o.K, gemm_splits_ready(o), o.tune.gemm_bm,
+                                        o.tune.gemm_bn);
         o.splits = plan.splits;
         const bool sk = o.splits > 1;
+        if (plan.bn == 192) {
+            *name = sk ? "fp8_gemm_256x192_splitk" : "fp8_gemm_256x192";
+            return launch_big<256, 192>(o, stream, t);
+        }
+        if (plan.bn == 320) {
+            *name = sk ? "fp8_gemm_128x320_splitk" : "fp8_gemm_128x320";
+            return launch_big<128, 320>(o, stream, t);
+        }
         switch (plan.bm) {
         case 64:
             *name = sk ? "fp8_gemm_64x256_splitk" : "fp8_gemm_64x256";
-            return launch_big<64>(o, stream, t);
+            return launch_big<64, 256>(o, stream, t);
         case 128:
             *name = sk ? "fp8_gemm_128x256_splitk" : "fp8_gemm_128x256";
-            return launch_big<128>(o, stream, t);
+            return launch_big<128, 256>(o, stream, t);
         case 192:
             *name = sk ? "fp8_gemm_192x256_splitk" : "fp8_gemm_192x256";
-            return launch_big<192>(o, stream, t);
+            return launch_big<192, 256>(o, stream, t);
         default:
             *name = sk ? "fp8_gemm_256x256_splitk" : "fp8_gemm_256x256";
-            return launch_big<256>(o, stream, t);
+            return launch_big<256, 256>(o, stream, t);
         }
     }
     const int tiles = ((op.M + BM - 1) / BM) * ((op.N + BN - 1) / BN);

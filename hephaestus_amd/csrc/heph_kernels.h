@@ -41,6 +41,7 @@ struct Tuning {
     int gemv_waves = 0;
     int gemv_u = 0;
     int gemm_bm = 0;
+    int gemm_bn = 0;
     int batch_split = 0;
     int wide_tiles = 0;
     int wide_waves = 0;
@@ -126,13 +127,14 @@ constexpr int kPlanCUs = 256;
 hipError_t launch_fp8_gemm(const Fp8Operands& op, hipStream_t stream,
                            const LaunchTiming& t, const char** name);
 
-// Tile height (64, 128, 192 or 256) and K splits (1 = none) of the
-// large-M GEMM for M x N x K, splits only if can_split; forced_bm fixes
-// the tile height (0 = automatic).
+// Tile (bm x bn: 64, 128, 192 or 256 x 256, 256 x 192, 128 x 320) and K
+// splits (1 = none) of the large-M GEMM for M x N x K, splits only if
+// can_split; forced_bm / forced_bn keep only the tiles of that height /
+// width (0 = automatic).
 struct GemmPlan {
-    int bm, splits;
+    int bm, bn, splits;
 };
-GemmPlan gemm_plan(int M, int N, int K, bool can_split, int forced_bm = 0);
+GemmPlan gemm_plan(int M, int N, int K, bool can_split, int forced_bm = 0, int forced_bn = 0);
 // Scratch bytes for the partials of the split plan (0 when it does not
 // split), and whether op's scratch (part) holds them for a plan of more
 // than one split.

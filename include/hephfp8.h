@@ -295,6 +295,9 @@ const char* heph_last_kernel(void);
  *   gemm_bm      tile height of the large-M GEMM: 64, 128, 192, 256; 1 selects
  *                the 128x128 GEMM (otherwise used only when M*K or N*K
  *                reaches 2^31)
+ *   gemm_bn      tile width of the large-M GEMM: 192, 256 or 320 (tiles
+ *                64/128/192/256 x 256, 256 x 192, 128 x 320; with gemm_bm
+ *                a pair that is not one of them keeps the built-in choice)
  *   batch_split  the 64-column K-split kernel for M <= 32 with 1x128 groups:
  *                -1 never, n in 1..64 always, with at least n K splits
  *   wide_tiles   the wide-tile batched-decode kernel for M <= 32: -1 never,
@@ -321,6 +324,7 @@ typedef struct heph_launch_overrides {
     int wide_waves;
     int split_spin_limit;
     int gemv_groups;
+    int gemm_bn;
 } heph_launch_overrides;
 
 int heph_fp8_linear_with(void* c, int c_dtype, const uint16_t* x_bf16,

@@ -141,12 +141,14 @@ def test_launch_overrides_validate(lib):
           dict(gemm_bm=192), dict(gemm_bm=64), dict(gemm_bm=1), dict(batch_split=-1),
           dict(batch_split=64), dict(wide_tiles=-1), dict(wide_tiles=4),
           dict(wide_tiles=2, wide_waves=16), dict(split_spin_limit=-1),
-          dict(split_spin_limit=1000), dict(gemv_groups=1), dict(gemv_groups=2), dict()]
+          dict(split_spin_limit=1000), dict(gemv_groups=1), dict(gemv_groups=2),
+          dict(gemm_bn=192), dict(gemm_bn=320), dict(gemm_bm=128, gemm_bn=320), dict()]
     bad = [dict(gemv_ks=16), dict(gemv_ks=3), dict(gemv_waves=2), dict(gemv_waves=6),
            dict(gemv_u=4),
            dict(gemm_bm=96), dict(batch_split=-2), dict(batch_split=65), dict(wide_tiles=3),
            dict(wide_tiles=8), dict(wide_tiles=-2), dict(wide_waves=2), dict(wide_waves=12),
-           dict(split_spin_limit=-2), dict(gemv_groups=3), dict(gemv_groups=-1)]
+           dict(split_spin_limit=-2), dict(gemv_groups=3), dict(gemv_groups=-1),
+           dict(gemm_bn=128), dict(gemm_bn=64)]
     for ov in ok:
         assert with_overrides(lib, **ov) != L.HEPH_ERR_FLAGS, ov
     for ov in bad:

@@ -835,17 +835,18 @@ def test_graph_capture_replays_match_eager():
 
 # ------------------------------------------------ large-M GEMM variants ----
 
-@pytest.fixture(params=[64, 128, 192, 256])
+@pytest.fixture(params=[(64, 256), (128, 256), (192, 256), (256, 256), (256, 192), (128, 320)],
+                ids=lambda t: f"{t[0]}x{t[1]}")
 def tile_m(request):
-    """Force the large-M kernel's tile height for one test."""
-    T.TUNE["gemm_bm"] = request.param
+    """Force the large-M kernel's tile (height x width) for one test."""
+    T.TUNE["gemm_bm"], T.TUNE["gemm_bn"] = request.param
     yield request.param
     T.TUNE.clear()
 
 
-def gemm_name(bm, block=True, split=False):
-    """Kernel name the large-M dispatch reports at a forced tile height."""
-    return f"fp8_gemm_{bm}x256" + ("_splitk" if split else "")
+def gemm_name(tile, block=True, split=False):
+    """Kernel name the large-M dispatch reports for a forced tile."""
+    return f"fp8_gemm_{tile[0]}x{tile[1]}" + ("_splitk" if split else "")
 
 
 @pytest.mark.parametrize("mode", ["block", "channel_token", "channel_g128"])
@@ -887,7 +888,7 @@ def test_large_m_short_k(K, tile_m):
     qw, sw = O.gen_weight(67 + K, N, K)
     c, q_ws, _ = run_linear(qw, sw, x, M=M, N=N, K=K)
     assert HK.last_kernel() == gemm_name(tile_m)
-    check_close(host_bf16(c), O.quant_linear(x, qw, sw), f"K={K} BM={tile_m}")
+    check_close(host_bf16(c), O.quant_linear(x, qw, sw), f"K={K} tile={tile_m}")
     qo, _ = O.quant_act(x, 128)
     assert np.array_equal(q_ws.cpu().numpy().reshape(M, K), qo)
 
@@ -1273,10 +1274,10 @@ def test_batch_split_give_up_is_counted_and_leaves_flags_ready():
 
 @pytest.mark.parametrize("out,resid", [("bf16", False), ("f32", True)])
 def test_large_m_split_k_every_tile(out, resid, tile_m):
-    # Few tiles (M = 200, N = 272) and 17 chunks: every forced tile height
-    # splits K (ragged splits of 4 and 5 chunks) through its own stage
-    # layout: three whole stages at 64 and 128 rows, two A + three B
-    # stages at 192, two at 256. Random data against the oracle, residual
+    # Few tiles (M = 200, N = 272) and 17 chunks: every forced tile splits
+    # K (ragged splits of 4 and 5 chunks) through its own stage layout:
+    # three whole stages at 64 and 128 x 256, two A + three B stages at
+    # 192 x 256, 256 x 192 and 128 x 320, two at 256 x 256. Random data against the oracle, residual
     # added before the one rounding, codes bit-exact.
     M, N, K = 200, 272, 2176
     x = O.gen_act_bf16(95, M, K, outlier_p=1e-3)
@@ -1321,15 +1322,24 @@ def test_large_m_split_k_exact_and_repeatable():
     assert np.array_equal(outs[0], bf16_of(exact.astype(np.float32)))
 
 
-def test_large_m_tile_choice_fills_the_cus():
-    # At M = 4096 the automatic tile height minimises rounds of tiles over
-    # 256 CUs times the per-chunk cost of the height: 256 for N = 6144
-    # (384 tiles, 2 rounds), 192 for N = 2560 (220 tiles, 1 round), 256 for
-    # N = 19456 (1216 tiles, 5 rounds).
-    x = O.gen_act_bf16(70, 4096, 256)
-    for N, want in ((6144, 256), (2560, 192), (19456, 256)):
-        if torch.cuda.get_device_properties(0).multi_processor_count != 256:
-            pytest.skip("expectations are for a 256-CU MI355X")
-        qw, sw = O.gen_weight(71, N, 256)
-        run_linear(qw, sw, x, M=4096, N=N, K=256)
-        assert HK.last_kernel() == f"fp8_gemm_{want}x256", N
+@pytest.mark.parametrize("M", [512, 4096])
+def test_large_m_tile_choice(M):
+    # The automatic tile (and K splits, where the workspace holds their
+    # partials) minimises the estimated rounds of tiles over 256 CUs times a
+    # tile's chunk and fixed costs; on the config-1 shapes it picks the tiles
+    # measured fastest on MI355X (GEMM alone): at M = 4096 256 x 192 for qkv
+    # (512 tiles, 2 rounds), 128 x 320 for o_proj and down (256 tiles, 1
+    # round), 256 x 256 for gate_up; at M = 512 64 x 256 for qkv and (3
+    # splits) o_proj, 128 x 320 for gate_up, 128 x 256 with splits for down.
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("expectations are for a 256-CU MI355X")
+    want = {4096: {"qkv": "256x192", "o_proj": "128x320", "gate_up": "256x256",
+                   "down": "128x320"},
+            512: {"qkv": "64x256", "o_proj": "64x256_splitk", "gate_up": "128x320",
+                  "down": "128x256_splitk"}}[M]
+    for name, tile in want.items():
+        N, K = SHAPES[name]
+        q_ws, s_ws = HK.workspace(M, K, n=N)
+        run_linear(np.zeros((N, K), np.uint8), np.ones((-(-N // 128), K // 128), np.float32),
+                   np.zeros((M, K), np.uint16), M=M, N=N, K=K, q_ws=q_ws, s_ws=s_ws)
+        assert HK.last_kernel() == f"fp8_gemm_{tile}", (M, name, HK.last_kernel())
