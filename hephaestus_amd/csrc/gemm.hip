@@ -218,25 +218,26 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8Operands op)
 }
 
 // ---------------------------------------------------------------------------
-// Large-M kernel: BMx256 tile per 512-thread workgroup (8 waves of
-// (BM/2)x64, (BM/32)x4 MFMA 16x16x128 each). The weight fragment is the
+// Large-M kernel: BMxBN tile per 512-thread workgroup (8 waves of
+// (BM/2)x(BN/4), (BM/32)x(BN/64) MFMA 16x16x128 each). The weight fragment is the
 // MFMA's first operand, so lane l holds row l&15 of each 16x16 output block
 // at columns 4*(l>>4) .. +3: one activation-scale product per row tile and
 // chunk, and four consecutive outputs to pack. Operand tiles reach LDS by
 // direct DMA (buffer_load_dwordx4 ... lds, 1 KB = 8 rows per instruction,
 // no VGPR staging); a 16-byte piece p of row r lands in slot p ^ (r & 7),
 // which spreads the fragment reads over the banks. Stages of A BM*128 B,
-// B 32 KB and row scales BM*4 B (two, or three where LDS allows: see
+// B BN*128 B and row scales BM*4 B (two, or three where LDS allows: see
 // BigTile); one barrier per 128-wide chunk:
 //   wait own DMA of chunk j -> barrier (chunk j visible everywhere, and
 //   every wave is done with the stage read in chunk j-1) -> DMA chunk j+1
 //   (j+2 with three stages) into that stage -> contract chunk j.
 // The chunk loop is unrolled by the stage count so that each stage's LDS
 // addresses are fixed registers plus instruction offsets (the B stage of
-// the 192-row tile, three against two A stages, is a run-time base), and
+// the tiles with three B against two A stages is a run-time base), and
 // the DMA advances through K
 // with a scalar offset only: apart from the rescale (one FMA per
-// accumulator and chunk, one multiply per row tile) the loop holds almost
+// accumulator and chunk, one multiply per row tile, or per row tile and
+// 16-column block where a wave's columns span two weight blocks) the loop holds almost
 // no VALU work, because a wave's VALU instructions do not overlap its own
 // MFMAs. The block scales come through the scalar cache.
 // The compiler does not model the DMA's LDS writes, so the waits are
@@ -247,10 +248,10 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8Operands op)
 // a time, the residual added before the one rounding.
 namespace {
 
-// Tile height BM in {64, 128, 192, 256}: the 8 waves form a 2 x 4 grid of
-// (BM/2) x 64 wave tiles. A smaller BM trades MFMA work per chunk for a
-// tile count that fills the CUs (e.g. 220 tiles of 192 x 256 instead of
-// 160 of 256 x 256 at M = 4096, N = 2560).
+// Tile BM x BN, BM in {64, 128, 192, 256}, BN in {192, 256, 320}: the 8
+// waves form a 2 x 4 grid of (BM/2) x (BN/4) wave tiles. A smaller tile
+// trades MFMA work per chunk for a tile count that fills the CUs (e.g. 256
+// tiles of 128 x 320 instead of 160 of 256 x 256 at M = 4096, N = 2560).
 template <int BM, int BN>
 struct BigTile {
     static_assert(BM == 64 || BM == 128 || BM == 192 || BM == 256, "tile height");
@@ -918,11 +919,11 @@ size_t gemm_split_bytes(int M, int N, int K)
 hipError_t launch_fp8_gemm(const Fp8Operands& op, hipStream_t stream,
                            const LaunchTiming& t, const char** name)
 {
-    // The 256-column DMA kernel for every M (N % 16 == 0 keeps every 8-wide
-    // output group inside the row), splitting K when its tiles leave CUs
-    // idle; its 32-bit operand offsets need M*K and N*K below 2^31, else the
-    // 128x128 kernel. (Without splits the two run alike below M = 128; the
-    // 256-column kernel is 1.3-2x faster from there on, MI355X.)
+    // The DMA kernel (tiles of 192-320 columns) for every M (N % 16 == 0
+    // keeps every 8-wide output group inside the row), splitting K when its
+    // tiles leave CUs idle; its 32-bit operand offsets need M*K and N*K below
+    // 2^31, else the 128x128 kernel. (Without splits the two run alike below
+    // M = 128; the DMA kernel is 1.3-2x faster from there on, MI355X.)
     const bool small_offsets = (long)op.M * op.K < (1L << 31) && (long)op.N * op.K < (1L << 31);
     const bool force_128 = op.tune.gemm_bm == 1;
     if (small_offsets && !force_128) {
