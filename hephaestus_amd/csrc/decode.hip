@@ -183,13 +183,25 @@ __device__ __forceinline__ void head_norm_rope(float& a, float& b, float g_lo, f
     head_finish(a, b, g_lo, g_hi, c, s, eps, wave_sum64(ss));
 }
 
+// The V cache in 64-key blocks: key j, kv head kh, dim d at byte
+//   ((j / 64 * n_kv + kh) * 8 + d / 16) * 1024 + (j % 64) * 16 + d % 16,
+// i.e. [n_keys / 64][n_kv][8 dim chunks][64 keys][16 dims]: the 64 keys of
+// one block and one 16-dim chunk are 1 KB in a row, which one wave of the
+// values kernel reads with one 16-byte load per lane. Whole blocks are
+// allocated (the keys of the last block past n_keys are padding).
+constexpr int kVBlock = 64;
+__host__ __device__ __forceinline__ size_t vblk_off(int j, int kh, int d, int n_kv)
+{
+    return ((((size_t)(j / kVBlock) * n_kv + kh) * 8 + d / 16) << 10) + (j % kVBlock) * 16 + d % 16;
+}
+
 // One wave per head (D = 128), lane l holding elements l and l + 64. Waves
 // 0..H-1 take the q heads (normalized and rotated in place), H..H+KVH-1 the
-// k heads (normalized, rotated and quantized into the cache slot),
-// H+KVH.. the v heads (quantized).
+// k heads (normalized, rotated and quantized into K cache row pos),
+// H+KVH.. the v heads (quantized into V cache position pos).
 __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
-    uint16_t* qkv, const uint16_t* q_gamma, const uint16_t* k_gamma, uint8_t* k_slot,
-    uint8_t* v_slot, const float* kv_inv, int n_heads, int n_kv, int pos, double theta, float eps)
+    uint16_t* qkv, const uint16_t* q_gamma, const uint16_t* k_gamma, uint8_t* k_cache,
+    uint8_t* v_cache, const float* kv_inv, int n_heads, int n_kv, int pos, double theta, float eps)
 {
     constexpr int D = 128;
     const int h = blockIdx.x;
@@ -199,8 +211,8 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
     if (h >= n_heads + n_kv) {                // v: quantize only
         const int kh = h - n_heads - n_kv;
         const float inv = kv_inv[n_kv + kh];
-        v_slot[kh * D + l] = (uint8_t)e4m3_sat(a * inv);
-        v_slot[kh * D + l + 64] = (uint8_t)e4m3_sat(b * inv);
+        v_cache[vblk_off(pos, kh, l, n_kv)] = (uint8_t)e4m3_sat(a * inv);
+        v_cache[vblk_off(pos, kh, l + 64, n_kv)] = (uint8_t)e4m3_sat(b * inv);
         return;
     }
     const uint16_t* gamma = h < n_heads ? q_gamma : k_gamma;
@@ -213,6 +225,7 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
     } else {
         const int kh = h - n_heads;
         const float inv = kv_inv[kh];
+        uint8_t* k_slot = k_cache + (size_t)pos * n_kv * D;
         k_slot[kh * D + l] = (uint8_t)e4m3_sat(a * inv);
         k_slot[kh * D + l + 64] = (uint8_t)e4m3_sat(b * inv);
     }
@@ -234,12 +247,12 @@ __device__ __forceinline__ void decode16(const uint4& w, float* f)
     }
 }
 
-// Attention over the E4M3 cache: three kernels over splits of kAttnSplit
-// keys, one workgroup per (kv head, split) serving all G query heads that
-// share the kv head, so every K and V byte is read once:
-//   A  scores: thread t of a workgroup holds dims 16c .. 16c+15 (c = t & 7)
-//      of keys j = 128*split + (t >> 3) + 32i (i < 4), one 16-byte load
-//      each (eight lanes read a key's 128-byte row). Per head g:
+// Attention over the E4M3 cache in two kernels:
+//   A  scores, one workgroup per (kv head, split of kAttnSplit keys) serving
+//      the G query heads that share the kv head (every K byte read once):
+//      thread t holds dims 16c .. 16c+15 (c = t & 7) of keys
+//      j = 128*split + (t >> 3) + 32i (i < 4), one 16-byte load each (eight
+//      lanes read a key's 128-byte row). Per head g:
 //        part_c = sum over those 16 dims in order (fma), then
 //        s_j = (((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7))) * (sk * f32(1/sqrt(128)))
 //      written to the workspace, with the split's max m_s and
@@ -247,31 +260,30 @@ __device__ __forceinline__ void decode16(const uint4& w, float* f)
 //      j = 128*split + ks + 32i, where slots4 sums 32 slot values as
 //      ((a0+a1)+(a2+a3)) + ((a4+a5)+(a6+a7)) per wave (8 slots) and the
 //      four waves in order
-//   B  values: m = max over splits of m_s; sum = fold over 64 slots
-//      (v[l] += v[l + h], h = 32 .. 1) of the per-slot fma sums (slot l:
-//      splits l, l+64, ... in order) of l_s * exp(m_s - m);
-//      p_j = bf16(exp(s_j - m) * (1/sum)) (the
-//      reference's probability, kernels.mojo:1003-1019, global max and sum);
-//      per (head, dim): a_ks = sum over i in order of p_j * v_j (fma), then
-//      slots4 over ks -> r_split
-//   C  out_d = bf16((sum over splits of r_split[d], in split order) * sv)
-// The same block index maps to the same (kv head, split) in A and B, so a
-// split's scores are read back on the XCD (L2) that wrote them. The CPU
-// restatement repeats every order above.
+//   B  values, one workgroup per (query head, 16-dim chunk) over all keys
+//      (attn_values_kernel): m = max over splits of m_s; sum = fold over 64
+//      slots (v[l] += v[l + h], h = 32 .. 1) of the per-slot fma sums (slot
+//      l: splits l, l+64, ... in order) of l_s * exp(m_s - m);
+//      p_j = bf16(exp(s_j - m) * (1/sum)) (the reference's probability,
+//      kernels.mojo:1003-1019, global max and sum); out_d = bf16(sum over
+//      keys of p_j * v_j[d] * sv) in the order that kernel states.
+// A workgroup of B reads the scores of one head and one 16-byte chunk of
+// each of its kv head's V rows; a values output needs every key, and
+// finishing it in one workgroup replaces a third launch that summed
+// per-split partial outputs. The CPU restatement repeats every order above.
 constexpr int kAttnSplit = 128;
-// Keys per thread of the scores and values kernels: the split's 128 keys
-// sit in 128 / kAttnKPT key slots of 8 lanes, a workgroup of 1024 /
-// kAttnKPT threads. The summation orders (and the CPU restatement) follow
+// Keys per thread of the scores kernel: the split's 128 keys sit in
+// 128 / kAttnKPT key slots of 8 lanes, a workgroup of 1024 / kAttnKPT
+// threads. The summation orders (and the CPU restatement) follow
 // kAttnKPT = 4; 2 (eight waves, half the work each) measured slower on
-// MI355X (20.9 against 20.4 us for the three launches at 4097 keys): the
-// VALU work per SIMD is the same and one workgroup already sits on each CU.
+// MI355X: the VALU work per SIMD is the same and one workgroup already sits
+// on each CU.
 constexpr int kAttnKPT = 4;
 
 struct AttnWs {
     float* scores;   // [n_heads][n_keys]
     float* smax;     // [n_heads][n_splits]
     float* ssum;     // [n_heads][n_splits]
-    float* partial;  // [n_heads][n_splits][128]
 };
 
 __device__ __forceinline__ AttnWs attn_ws(float* ws, int n_heads, int n_keys, int n_splits)
@@ -280,7 +292,6 @@ __device__ __forceinline__ AttnWs attn_ws(float* ws, int n_heads, int n_keys, in
     w.scores = ws;
     w.smax = w.scores + (size_t)n_heads * n_keys;
     w.ssum = w.smax + (size_t)n_heads * n_splits;
-    w.partial = w.ssum + (size_t)n_heads * n_splits;
     return w;
 }
 
@@ -321,8 +332,8 @@ struct QkvPrep {
     const uint16_t* qkv;     // [n_heads + 2 n_kv, 128] bf16: q heads, k heads, v heads
     const uint16_t* q_gamma;
     const uint16_t* k_gamma;
-    uint8_t* k_slot;         // [n_kv, 128] codes of the new key
-    uint8_t* v_slot;
+    uint8_t* k_slot;         // [n_kv, 128] codes of the new key (its K cache row)
+    uint8_t* v_cache;        // the blocked V cache; the new key is position n_keys - 1
     const float* kv_inv;     // n_kv K entries, then n_kv V entries
     const uint16_t* rope;    // (cos, sin) bf16 of the 64 pairs at the new key's
                              // position, or nullptr: computed here (rope_cs)
@@ -425,7 +436,9 @@ __global__ __launch_bounds__(1024 / KPT) void attn_scores_kernel(
                 knew[l + 64] = hi;
             }
         }
-        if (last && t < D) prep.v_slot[kh * D + t] = (uint8_t)e4m3_sat(vx * prep.kv_inv[n_kv + kh]);
+        if (last && t < D)
+            prep.v_cache[vblk_off(n_keys - 1, kh, t, n_kv)] =
+                (uint8_t)e4m3_sat(vx * prep.kv_inv[n_kv + kh]);
         __syncthreads();
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -534,175 +547,152 @@ __global__ __launch_bounds__(1024 / KPT) void attn_scores_kernel(
     }
 }
 
-template <int G, int KPT>
-__global__ __launch_bounds__(1024 / KPT) void attn_pv_kernel(float* ws, const uint8_t* vc,
-                                                            int n_kv, int n_keys, int n_splits)
+// Values: one workgroup per (query head, 16-dim chunk) over all the keys,
+// so each output is finished inside the workgroup. Wave w takes the 64-key
+// blocks b = w, w + 16, w + 32, ... (lane l key 64b + l, one 16-byte load
+// of the block's chunk), kValBlocks blocks per pass with every load of a
+// pass in flight, the next pass issued before the current one is used.
+constexpr int kValWaves = 16;
+constexpr int kValBlocks = 5;
+
+template <int G>
+__global__ __launch_bounds__(64 * kValWaves) void attn_values_kernel(
+    uint16_t* out, const float* ws, const uint8_t* vc, const float* kv_scale, int n_kv,
+    int n_keys, int n_splits)
 {
-    constexpr int D = 128;
-    constexpr int NT = 1024 / KPT, SLOTS = kAttnSplit / KPT, NW = SLOTS / 8;
-    const int kh = blockIdx.x % n_kv, split = blockIdx.x / n_kv;
-    const int t = threadIdx.x, ks = t >> 3, c = t & 7, wave = t >> 6;
-    const AttnWs w = attn_ws(ws, n_kv * G, n_keys, n_splits);
-    const size_t row = (size_t)n_kv * D;
-    const int j0 = split * kAttnSplit + ks;
+    constexpr int NW = kValWaves, NB = kValBlocks;
+    // kv head kh's workgroups are blockIdx kh + n_kv * i: with 8 kv heads
+    // they share one XCD (and its L2) with each other and with the scores
+    // kernel's workgroups of kh, which use the same rule
+    const int kh = blockIdx.x % n_kv, i = blockIdx.x / n_kv;
+    const int g = i % G, c = i / G, h = kh * G + g;
+    const int t = threadIdx.x, l = t & 63, wave = t >> 6;
+    const AttnWs w = attn_ws(const_cast<float*>(ws), n_kv * G, n_keys, n_splits);
+    const int n_blocks = (n_keys + kVBlock - 1) / kVBlock;
+    const int n_pass = (n_blocks + NW * NB - 1) / (NW * NB);
+    const float* sh = w.scores + (size_t)h * n_keys;
+    const uint8_t* vh = vc + vblk_off(l, kh, 16 * c, n_kv);
+    const size_t vstep = (size_t)n_kv * 8 * 1024;   // bytes per 64-key block
 
-    // Loads in the order their data is needed: a wave's loads complete in
-    // issue order, so the split statistics and this thread's scores (written
-    // by the scores kernel, near in the cache hierarchy) go out before the V
-    // rows (HBM), and the statistics and probabilities are worked out while
-    // the V rows are in flight. Up to 64 splits (8192 keys) lane l holds
-    // split l's max and sum.
-    const int l = t & 63;
-    float ms[G], ls[G];
+    // Loads in the order their data is needed (a wave's loads complete in
+    // issue order): the split statistics (lane l: split l up to 64 splits),
+    // then the scores (both written by the scores kernel, near in the cache
+    // hierarchy), then the V blocks (HBM).
+    const size_t base = (size_t)h * n_splits;
+    const float ms = l < n_splits ? w.smax[base + l] : -3.4e38f;
+    const float ls = l < n_splits ? w.ssum[base + l] : 0.0f;
+    float sa[NB], sb[NB];
+    uint4 va[NB], vb[NB];
+    auto issue = [&](int pass, float (&sj)[NB], uint4 (&vv)[NB]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const size_t base = (size_t)(kh * G + g) * n_splits;
-        ms[g] = l < n_splits ? w.smax[base + l] : -3.4e38f;
-        ls[g] = l < n_splits ? w.ssum[base + l] : 0.0f;
-    }
-    float sj[KPT][G];
+        for (int k = 0; k < NB; ++k) {
+            const int b = (pass * NB + k) * NW + wave;
+            if (b < n_blocks) sj[k] = sh[min(kVBlock * b + l, n_keys - 1)];
+        }
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-        const int j = min(j0 + SLOTS * i, n_keys - 1);
-#pragma unroll
-        for (int g = 0; g < G; ++g) sj[i][g] = w.scores[(size_t)(kh * G + g) * n_keys + j];
-    }
-    uint4 vv[KPT];
-#pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-        const int j = min(j0 + SLOTS * i, n_keys - 1);
-        vv[i] = ldg16u(vc + (size_t)j * row + kh * D + 16 * c);
-    }
+        for (int k = 0; k < NB; ++k) {
+            const int b = (pass * NB + k) * NW + wave;
+            if (b < n_blocks) vv[k] = ldg16u(vh + b * vstep);
+        }
+    };
+    issue(0, sa, va);
 
-    // global max and sum per head from the split statistics, computed by
-    // every wave on its own (no barrier): lane l takes splits l, l + 64, ...
-    // (sum: fma in that order), the max over all lanes, the sum folded as
-    // v[l] += v[l + h], h = 32 .. 1
-    float mloc[G], inv[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const size_t base = (size_t)(kh * G + g) * n_splits;
-        float m = -3.4e38f, a = 0.0f;
-        if (n_splits <= 64) {
-            m = wave_max64(ms[g]);
-            if (l < n_splits) a = __builtin_fmaf(ls[g], expf(ms[g] - m), 0.0f);
-        } else {
-            for (int s = l; s < n_splits; s += 64) m = fmaxf(m, w.smax[base + s]);
-            m = wave_max64(m);
-            for (int s = l; s < n_splits; s += 64)
-                a = __builtin_fmaf(w.ssum[base + s], expf(w.smax[base + s] - m), a);
-        }
-        mloc[g] = m;
-        inv[g] = __fdiv_rn(1.0f, wave_sum64(a));
+    // global max and 1/sum per head from the split statistics, by every
+    // wave (no barrier): the max over all splits, the sum of l_s * exp(m_s -
+    // m) by fma per lane over splits l, l + 64, ..., folded as v[l] +=
+    // v[l + h], h = 32 .. 1
+    float m, a = 0.0f;
+    if (n_splits <= 64) {
+        m = wave_max64(ms);
+        if (l < n_splits) a = __builtin_fmaf(ls, expf(ms - m), 0.0f);
+    } else {
+        m = -3.4e38f;
+        for (int s = l; s < n_splits; s += 64) m = fmaxf(m, w.smax[base + s]);
+        m = wave_max64(m);
+        for (int s = l; s < n_splits; s += 64)
+            a = __builtin_fmaf(w.ssum[base + s], expf(w.smax[base + s] - m), a);
     }
+    const float inv = __fdiv_rn(1.0f, wave_sum64(a));
 
-    // p for this thread's keys, then its value sums (G heads x 16 dims)
-    float acc[G][16];
+    // p_j = bf16(exp(s_j - m) * inv) (the reference's probability,
+    // kernels.mojo:1003-1019); per lane an fma chain over its keys in block
+    // order; keys past n_keys (the last block's padding) are skipped
+    float acc[16];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+    auto consume = [&](int pass, const float (&sj)[NB], const uint4 (&vv)[NB])
+        __attribute__((always_inline)) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[g][e] = 0.0f;
+        for (int k = 0; k < NB; ++k) {
+            const int j = kVBlock * ((pass * NB + k) * NW + wave) + l;
+            if (j < n_keys) {
+                const float pj = round_bf16(expf(sj[k] - m) * inv);
+                float v16[16];
+                decode16(vv[k], v16);
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-        float v16[16];
-        decode16(vv[i], v16);
-        const bool live = j0 + SLOTS * i < n_keys;
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float pj = live ? round_bf16(expf(sj[i][g] - mloc[g]) * inv[g]) : 0.0f;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[g][e] = __builtin_fmaf(pj, v16[e], acc[g][e]);
-        }
-    }
-    // sum over the wave's 8 key slots (lanes 8k + c) by the tree of
-    // slots_reduce, ((k0+k1)+(k2+k3))+((k4+k5)+(k6+k7)), but scattering the
-    // results: pairs k^1 by row_ror:8 on all 16G values; pairs k^2 by one
-    // v_permlane16_swap per pair of values (even rows keep the first half,
-    // odd rows the second); pairs k^4 by one v_permlane32_swap per pair of
-    // the remaining 8G (the lower half keeps the first half). A lane then
-    // holds the 4G sums o = 8G * (row & 1) + 4G * (lane >= 32) + i, i < 4G,
-    // of the flattened (head, dim) index g * 16 + e: a third of the
-    // cross-lane work of reducing every value everywhere, same sums.
-    __shared__ float wsum[NW][G][D];
-    if constexpr (G >= 4) {
-        constexpr int V = 16 * G;
-        float* f = &acc[0][0];
-#pragma unroll
-        for (int i = 0; i < V; ++i) f[i] = dpp_add<0x128>(f[i]);
-        float h2[V / 2];
-#pragma unroll
-        for (int i = 0; i < V / 2; ++i) {
-            const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(f[i]),
-                                                            __float_as_uint(f[i + V / 2]), false, false);
-            h2[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-        }
-        float h4[V / 4];
-#pragma unroll
-        for (int i = 0; i < V / 4; ++i) {
-            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(h2[i]),
-                                                            __float_as_uint(h2[i + V / 4]), false, false);
-            h4[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-        }
-        const int lane = t & 63;
-        if ((lane & 8) == 0) {   // k even; its row partner k + 1 holds the same sums
-            const int o0 = (V / 2) * ((lane >> 4) & 1) + (V / 4) * (lane >> 5);
-#pragma unroll
-            for (int i = 0; i < V / 4; ++i) {
-                const int o = o0 + i;
-                wsum[wave][o >> 4][16 * c + (o & 15)] = h4[i];
+                for (int e = 0; e < 16; ++e) acc[e] = __builtin_fmaf(pj, v16[e], acc[e]);
             }
         }
-    } else {
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[g][e] = slots_reduce<false>(acc[g][e]);
-        if ((t & 63) < 8) {
-#pragma unroll
-            for (int g = 0; g < G; ++g)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) wsum[wave][g][16 * c + e] = acc[g][e];
-        }
+    };
+    for (int p = 0; p < n_pass; p += 2) {
+        if (p + 1 < n_pass) issue(p + 1, sb, vb);
+        consume(p, sa, va);
+        if (p + 1 >= n_pass) break;
+        if (p + 2 < n_pass) issue(p + 2, sa, va);
+        consume(p + 1, sb, vb);
     }
-    __syncthreads();
-    for (int o = t; o < G * D; o += NT) {
-        const int g = o / D, d = o % D;
-        float r = wsum[0][g][d];
-#pragma unroll
-        for (int v = 1; v < NW; ++v) r += wsum[v][g][d];
-        w.partial[((size_t)(kh * G + g) * n_splits + split) * D + d] = r;
-    }
-}
 
-__global__ __launch_bounds__(128) void attn_combine_kernel(uint16_t* out, const float* ws,
-                                                           const float* kv_scale, int n_heads,
-                                                           int n_kv, int n_keys, int n_splits)
-{
-    const int h = blockIdx.x, d = threadIdx.x;
-    const AttnWs w = attn_ws(const_cast<float*>(ws), n_heads, n_keys, n_splits);
-    const float* p = w.partial + (size_t)h * n_splits * 128 + d;
-    float v = 0.0f;
-    if (n_splits <= 64) {
-        // up to 8192 keys: every split's partial in flight at once (one
-        // round trip), then summed in split order
-        float x[64];
+    // Sum of the 16 values over the 64 lanes, halving the values per lane at
+    // each level: lanes l, l ^ 32 by v_permlane32_swap (the lower half keeps
+    // values 0-7), l ^ 16 by v_permlane16_swap (even rows keep the first
+    // half), l ^ 8 by row_ror:8 and l, 7 - l within 8 lanes by
+    // row_half_mirror (each lane sending the half its partner keeps), then
+    // l ^ 2 and l ^ 1 on the one value left. Lane l ends with value
+    // 8*bit5 + 4*bit4 + 2*bit3 + bit2 of l, summed (with x_k the lane sums
+    // and T_q = ((x_q + x_q+32) + (x_q+16 + x_q+48)) + ((x_q+8 + x_q+40) +
+    // (x_q+24 + x_q+56))) as ((T0 + T7) + (T2 + T5)) + ((T1 + T6) + (T3 + T4)).
+    float h8[8];
 #pragma unroll
-        for (int u = 0; u < 64; ++u) x[u] = u < n_splits ? p[u * 128] : 0.0f;
-#pragma unroll
-        for (int u = 0; u < 64; ++u)
-            if (u < n_splits) v += x[u];
-    } else {
-        int s = 0;
-        for (; s + 8 <= n_splits; s += 8) {  // eight loads in flight, summed in order
-            float x[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) x[u] = p[(s + u) * 128];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v += x[u];
-        }
-        for (; s < n_splits; ++s) v += p[s * 128];
+    for (int e = 0; e < 8; ++e) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[e]),
+                                                        __float_as_uint(acc[e + 8]), false, false);
+        h8[e] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     }
-    out[(size_t)h * 128 + d] = f32_to_bf16(v * kv_scale[n_kv + h / (n_heads / n_kv)]);
+    float h4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(h8[e]),
+                                                        __float_as_uint(h8[e + 4]), false, false);
+        h4[e] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    const bool b3 = l & 8, b2 = l & 4;
+    float h2[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const float send = b3 ? h4[e] : h4[e + 2], keep = b3 ? h4[e + 2] : h4[e];
+        h2[e] = keep + __int_as_float(
+                           __builtin_amdgcn_mov_dpp(__float_as_int(send), 0x128, 0xf, 0xf, false));
+    }
+    float h1;
+    {
+        const float send = b2 ? h2[0] : h2[1], keep = b2 ? h2[1] : h2[0];
+        h1 = keep + __int_as_float(
+                        __builtin_amdgcn_mov_dpp(__float_as_int(send), 0x141, 0xf, 0xf, false));
+    }
+    h1 = dpp_add<0x4E>(h1);
+    h1 = dpp_add<0xB1>(h1);
+    // the 16 waves: pairs (2u, 2u + 1), then ((r0 + r1) + (r2 + r3)) +
+    // ((r4 + r5) + (r6 + r7)); times the V scale, bf16
+    __shared__ float wsum[NW][16];
+    if ((l & 3) == 0) wsum[wave][8 * (l >> 5) + 4 * ((l >> 4) & 1) + 2 * b3 + b2] = h1;
+    __syncthreads();
+    if (t < 16) {
+        float r8[NW / 2];
+#pragma unroll
+        for (int u = 0; u < NW / 2; ++u) r8[u] = wsum[2 * u][t] + wsum[2 * u + 1][t];
+        const float r = ((r8[0] + r8[1]) + (r8[2] + r8[3])) + ((r8[4] + r8[5]) + (r8[6] + r8[7]));
+        out[(size_t)h * 128 + 16 * c + t] = f32_to_bf16(r * kv_scale[n_kv + kh]);
+    }
 }
 
 __global__ __launch_bounds__(256) void silu_mul_kernel(uint16_t* out, const uint16_t* gate,
@@ -791,8 +781,8 @@ hipError_t launch_attention(uint16_t* out, const uint16_t* q, const uint8_t* kc,
     else
         attn_scores_kernel<G, false, kAttnKPT><<<blocks, NT, 0, s>>>(ws, q, kc, kv_scale, n_kv,
                                                                     n_keys, splits, prep);
-    attn_pv_kernel<G, kAttnKPT><<<blocks, NT, 0, s>>>(ws, vc, n_kv, n_keys, splits);
-    attn_combine_kernel<<<n_kv * G, 128, 0, s>>>(out, ws, kv_scale, n_kv * G, n_kv, n_keys, splits);
+    attn_values_kernel<G><<<n_kv * G * 8, 64 * kValWaves, 0, s>>>(out, ws, vc, kv_scale, n_kv,
+                                                                  n_keys, splits);
     return hipGetLastError();
 }
 
@@ -837,11 +827,11 @@ int heph_rmsnorm(void* out_bf16, const void* in_bf16, const void* gamma_bf16, in
 }
 
 int heph_qk_norm_rope_kv(void* qkv_bf16, const void* q_gamma, const void* k_gamma,
-                         uint8_t* k_slot, uint8_t* v_slot, const float* kv_inv_scale,
+                         uint8_t* k_cache, uint8_t* v_cache, const float* kv_inv_scale,
                          int n_heads, int n_kv_heads, int head_dim, int pos, double theta,
                          float eps, void* stream)
 {
-    if (!qkv_bf16 || !q_gamma || !k_gamma || !k_slot || !v_slot || !kv_inv_scale)
+    if (!qkv_bf16 || !q_gamma || !k_gamma || !k_cache || !v_cache || !kv_inv_scale)
         return HEPH_ERR_NULL;
     if (head_dim != 128 || n_kv_heads < 1 || n_heads < n_kv_heads || n_heads % n_kv_heads ||
         pos < 0)
@@ -849,7 +839,7 @@ int heph_qk_norm_rope_kv(void* qkv_bf16, const void* q_gamma, const void* k_gamm
     if (int st = check_device()) return st;
     qk_norm_rope_kv_kernel<<<n_heads + 2 * n_kv_heads, 64, 0, static_cast<hipStream_t>(stream)>>>(
         static_cast<uint16_t*>(qkv_bf16), static_cast<const uint16_t*>(q_gamma),
-        static_cast<const uint16_t*>(k_gamma), k_slot, v_slot, kv_inv_scale, n_heads,
+        static_cast<const uint16_t*>(k_gamma), k_cache, v_cache, kv_inv_scale, n_heads,
         n_kv_heads, pos, theta, eps);
     return status_of(hipGetLastError());
 }
@@ -870,7 +860,7 @@ size_t heph_attention_ws_bytes(int n_heads, int n_keys)
 {
     if (n_heads < 1 || n_keys < 1) return 0;
     const size_t splits = (size_t)(n_keys + kAttnSplit - 1) / kAttnSplit;
-    return 4 * (size_t)n_heads * ((size_t)n_keys + splits * (2 + 128));
+    return 4 * (size_t)n_heads * ((size_t)n_keys + 2 * splits);
 }
 
 
@@ -934,7 +924,7 @@ int heph_attention_qkv_fp8kv(void* out_bf16, const void* qkv_bf16, const void* q
     prep.q_gamma = static_cast<const uint16_t*>(q_gamma);
     prep.k_gamma = static_cast<const uint16_t*>(k_gamma);
     prep.k_slot = k_cache + slot;
-    prep.v_slot = v_cache + slot;
+    prep.v_cache = v_cache;
     prep.kv_inv = kv_inv_scale;
     prep.rope = rope_table ? static_cast<const uint16_t*>(rope_table) + (size_t)pos * 128
                            : nullptr;

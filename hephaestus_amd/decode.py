@@ -58,10 +58,42 @@ def rmsnorm(out, x, gamma, eps: float = 1e-6) -> None:
     _call("heph_rmsnorm", _ptr(out), _ptr(x), _ptr(gamma), rows, cols, eps, _stream())
 
 
-def qk_norm_rope_kv(qkv, q_gamma, k_gamma, k_slot, v_slot, kv_inv, n_heads: int, n_kv: int,
+# The V cache holds 64-key blocks [n_blocks, n_kv, 8, 64, 16] (key j, kv head
+# h, dim d at [j // 64, h, d // 16, j % 64, d % 16]); the K cache rows
+# [n_keys, n_kv, 128].
+V_BLOCK = 64
+
+
+def v_blocks(rows):
+    """[n, n_kv, 128] V codes (numpy or torch) -> the blocked layout
+    [ceil(n/64), n_kv, 8, 64, 16], the padding keys zero."""
+    n, n_kv = rows.shape[0], rows.shape[1]
+    nb = -(-n // V_BLOCK)
+    if isinstance(rows, torch.Tensor):
+        pad = torch.zeros((nb * V_BLOCK, n_kv, 128), dtype=rows.dtype, device=rows.device)
+        pad[:n] = rows
+        return pad.view(nb, V_BLOCK, n_kv, 8, 16).permute(0, 2, 3, 1, 4).contiguous()
+    pad = np.zeros((nb * V_BLOCK, n_kv, 128), dtype=rows.dtype)
+    pad[:n] = rows
+    return np.ascontiguousarray(pad.reshape(nb, V_BLOCK, n_kv, 8, 16).transpose(0, 2, 3, 1, 4))
+
+
+def v_rows(blocks, n: int | None = None):
+    """The inverse of v_blocks: [nb, n_kv, 8, 64, 16] -> [n, n_kv, 128]
+    (n = nb * 64 by default)."""
+    nb, n_kv = blocks.shape[0], blocks.shape[1]
+    n = nb * V_BLOCK if n is None else n
+    if isinstance(blocks, torch.Tensor):
+        return blocks.permute(0, 3, 1, 2, 4).reshape(nb * V_BLOCK, n_kv, 128)[:n]
+    return blocks.transpose(0, 3, 1, 2, 4).reshape(nb * V_BLOCK, n_kv, 128)[:n]
+
+
+def qk_norm_rope_kv(qkv, q_gamma, k_gamma, k_cache, v_cache, kv_inv, n_heads: int, n_kv: int,
                     pos: int, theta: float = 1e6, eps: float = 1e-6) -> None:
-    _call("heph_qk_norm_rope_kv", _ptr(qkv), _ptr(q_gamma), _ptr(k_gamma), _ptr(k_slot),
-          _ptr(v_slot), _ptr(kv_inv), n_heads, n_kv, 128, pos, theta, eps, _stream())
+    """q/k norm + RoPE at pos (q in place), k and v codes into key pos of
+    k_cache (rows) and v_cache (64-key blocks, v_blocks' layout)."""
+    _call("heph_qk_norm_rope_kv", _ptr(qkv), _ptr(q_gamma), _ptr(k_gamma), _ptr(k_cache),
+          _ptr(v_cache), _ptr(kv_inv), n_heads, n_kv, 128, pos, theta, eps, _stream())
 
 
 def attention_ws(n_heads: int, n_keys: int, device="cuda") -> torch.Tensor:
@@ -72,6 +104,13 @@ def attention_ws(n_heads: int, n_keys: int, device="cuda") -> torch.Tensor:
 
 def attention_fp8kv(out, q, k_cache, v_cache, kv_scale, n_heads: int, n_kv: int,
                     n_keys: int, ws: torch.Tensor | None = None) -> None:
+    """k_cache: rows [>= n_keys, n_kv, 128]; v_cache: 64-key blocks
+    (v_blocks' layout) of at least ceil(n_keys / 64) blocks."""
+    # (a key count the library refuses is left to its status code)
+    if 0 < n_keys <= L.ATTN_MAX_KEYS and \
+            v_cache.numel() < -(-n_keys // V_BLOCK) * V_BLOCK * n_kv * 128:
+        raise ValueError(f"v_cache of {v_cache.numel()} bytes holds fewer than "
+                         f"ceil({n_keys}/64) blocks")
     if ws is None:
         ws = attention_ws(n_heads, n_keys, device=out.device)
     _call("heph_attention_fp8kv", _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache),
@@ -98,6 +137,8 @@ def attention_qkv_fp8kv(out, qkv, q_gamma, k_gamma, k_cache, v_cache, kv_scale, 
         ws = attention_ws(n_heads, pos + 1, device=out.device)
     if rope is not None and rope.shape[0] <= pos:
         raise ValueError(f"rope table of {rope.shape[0]} rows has no row {pos}")
+    if 0 <= pos < L.ATTN_MAX_KEYS and v_cache.numel() < (pos // V_BLOCK + 1) * V_BLOCK * n_kv * 128:
+        raise ValueError(f"v_cache of {v_cache.numel()} bytes has no block for key {pos}")
     _call("heph_attention_qkv_fp8kv", _ptr(out), _ptr(qkv), _ptr(q_gamma), _ptr(k_gamma),
           _ptr(k_cache), _ptr(v_cache), _ptr(kv_scale), _ptr(kv_inv),
           None if rope is None else _ptr(rope), 0 if rope is None else rope.shape[0],
@@ -185,8 +226,9 @@ def conditioned_init(cfg: Qwen3Config, seed: int = 0, device="cuda") -> Qwen3Fp8
 # --------------------------------------------------------------- KV cache ----
 
 class KVCache:
-    """E4M3 codes k, v [n_layers, max_ctx, n_kv, 128] with f32 scales
-    [n_layers, 2*n_kv] (K heads then V heads) and their reciprocals."""
+    """E4M3 codes k [n_layers, max_ctx, n_kv, 128] and v in 64-key blocks
+    [n_layers, ceil(max_ctx/64), n_kv, 8, 64, 16] (v_blocks' layout) with f32
+    scales [n_layers, 2*n_kv] (K heads then V heads) and their reciprocals."""
 
     def __init__(self, cfg: Qwen3Config, max_ctx: int, device="cuda"):
         if max_ctx > L.ATTN_MAX_KEYS:
@@ -194,7 +236,8 @@ class KVCache:
         shape = (cfg.n_layers, max_ctx, cfg.n_kv_heads, cfg.head_dim)
         self.cfg, self.max_ctx = cfg, max_ctx
         self.k = torch.zeros(shape, dtype=torch.uint8, device=device)
-        self.v = torch.zeros(shape, dtype=torch.uint8, device=device)
+        self.v = torch.zeros((cfg.n_layers, -(-max_ctx // V_BLOCK), cfg.n_kv_heads, 8, V_BLOCK,
+                              16), dtype=torch.uint8, device=device)
         self.scale = torch.ones(cfg.n_layers, 2 * cfg.n_kv_heads, dtype=torch.float32,
                                 device=device)
         self.inv = torch.ones_like(self.scale)
@@ -216,8 +259,11 @@ class KVCache:
                 inv = (np.float32(1.0) / s).astype(np.float32)
                 scale[li, j * cfg.n_kv_heads:(j + 1) * cfg.n_kv_heads] = s
                 inv_t = torch.from_numpy(inv).to(x.device).view(1, -1, 1)
-                codes = (x * inv_t).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
-                dst[li, :n_pos] = codes.view(torch.uint8)
+                codes = (x * inv_t).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8)
+                if dst is self.k:
+                    dst[li, :n_pos] = codes
+                else:
+                    dst[li, :-(-n_pos // V_BLOCK)] = v_blocks(codes)
         self.scale.copy_(torch.from_numpy(scale))
         self.inv.copy_(torch.from_numpy((np.float32(1.0) / scale).astype(np.float32)))
 
@@ -305,11 +351,11 @@ class Qwen3Decoder:
             self._norm_linear(self.qkv, lw.attn_norm, lw.qkv, H, eps, rec, li, "attn_norm")
             rec(li, "qkv", self.qkv)
             if rec.tracing:
-                qk_norm_rope_kv(self.qkv, lw.q_norm, lw.k_norm, kv.k[li, pos], kv.v[li, pos],
+                qk_norm_rope_kv(self.qkv, lw.q_norm, lw.k_norm, kv.k[li], kv.v[li],
                                 kv.inv[li], NH, NKV, pos, cfg.theta, eps)
                 rec(li, "q_rope", self.qkv[:, :Q])
                 rec(li, "k_codes", kv.k[li, pos])
-                rec(li, "v_codes", kv.v[li, pos])
+                rec(li, "v_codes", kv.v[li, pos // V_BLOCK, :, :, pos % V_BLOCK])
                 attention_fp8kv(self.att, self.qkv, kv.k[li], kv.v[li], kv.scale[li], NH, NKV,
                                 pos + 1, self.attn_ws)
             else:
@@ -370,7 +416,10 @@ def host_model(w: Qwen3Fp8Weights) -> dict:
 
 
 def host_kv(kv: KVCache) -> dict:
-    return {"k": kv.k.cpu().numpy(), "v": kv.v.cpu().numpy(),
+    """Host copies in the oracle's form (v as rows [n_layers, max_ctx, n_kv,
+    128])."""
+    v = np.stack([v_rows(b, kv.max_ctx) for b in kv.v.cpu().numpy()])
+    return {"k": kv.k.cpu().numpy(), "v": v,
             "scale": kv.scale.cpu().numpy(), "inv": kv.inv.cpu().numpy()}
 
 

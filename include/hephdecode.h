@@ -39,29 +39,40 @@ int heph_rmsnorm(void* out_bf16, const void* in_bf16, const void* gamma_bf16, in
                  int cols, float eps, void* stream);
 
 /*
+ * The KV cache layouts (E4M3 codes, head_dim 128):
+ *   K: rows [n_keys][n_kv_heads][128]; key j's row at j * n_kv_heads * 128.
+ *   V: 64-key blocks [ceil(n_keys/64)][n_kv_heads][8][64][16]: key j, kv
+ *      head h, dim d at ((j/64 * n_kv_heads + h) * 8 + d/16) * 1024 +
+ *      (j%64) * 16 + d%16. Whole blocks are allocated: a V cache of
+ *      n_keys keys holds ceil(n_keys/64) * 64 * n_kv_heads * 128 bytes (the
+ *      padding keys of the last block are never used as values).
+ * The reference's cache is [MAX_KEYS, kv_out] rows (kernels.mojo:917); V's
+ * blocks let one 64-lane load read 64 keys of one 16-dim chunk.
+ */
+
+/*
  * On the qkv output of one token ([n_heads + 2*n_kv_heads, 128] bf16):
  * per-head RMSNorm of q (q_gamma) and k (k_gamma), RoPE of both at `pos`
  * (theta), q written back in place; k and v quantized to E4M3 with
- * code = e4m3(clamp(x * kv_inv_scale[h], +-448)) into k_slot / v_slot
- * ([n_kv_heads, 128] codes each). kv_inv_scale: n_kv_heads K entries, then
- * n_kv_heads V entries. Replaces the q/k _rms_norm calls and
+ * code = e4m3(clamp(x * kv_inv_scale[h], +-448)) into key `pos` of
+ * k_cache / v_cache (the layouts above). kv_inv_scale: n_kv_heads K
+ * entries, then n_kv_heads V entries. Replaces the q/k _rms_norm calls and
  * apply_rope_qk_inplace of forward.mojo:474-500 (kernels.mojo:709-796) and
  * the cache write of k/v (forward.mojo:415-431).
  */
 int heph_qk_norm_rope_kv(void* qkv_bf16, const void* q_gamma, const void* k_gamma,
-                         uint8_t* k_slot, uint8_t* v_slot, const float* kv_inv_scale,
+                         uint8_t* k_cache, uint8_t* v_cache, const float* kv_inv_scale,
                          int n_heads, int n_kv_heads, int head_dim, int pos, double theta,
                          float eps, void* stream);
 
 /*
  * One query token over n_keys cached keys: out[h] = sum_j p_j * v_j with
- * p = bf16(softmax(q.k_j * sk / sqrt(128))), K and V E4M3 codes
- * [n_keys, n_kv_heads, 128] scaled by kv_scale (K entries, then V).
+ * p = bf16(softmax(q.k_j * sk / sqrt(128))), K and V E4M3 codes in the
+ * layouts above scaled by kv_scale (K entries, then V), in two launches.
  * n_heads / n_kv_heads (query heads per kv head) must be 1, 2, 4 or 8.
  * ws: device scratch of heph_attention_ws_bytes(n_heads, n_keys) bytes
- * (scores, and per 128-key split the max, sum and value sums), 16-byte
- * aligned. Replaces attention (src/hephaestus/kernels.mojo:923-1035,
- * :1183-1240).
+ * (scores, and per 128-key split the max and sum), 16-byte aligned.
+ * Replaces attention (src/hephaestus/kernels.mojo:923-1035, :1183-1240).
  */
 size_t heph_attention_ws_bytes(int n_heads, int n_keys);
 int heph_attention_fp8kv(void* out_bf16, const void* q_bf16, const uint8_t* k_cache,
@@ -80,11 +91,10 @@ int heph_attention_fp8kv(void* out_bf16, const void* q_bf16, const uint8_t* k_ca
 int heph_rope_table_bf16(void* table_bf16, int n_pos, int head_dim, double theta, void* stream);
 
 /*
- * heph_qk_norm_rope_kv on qkv_bf16 with k_slot / v_slot = cache row `pos`
- * (k_cache / v_cache + pos * n_kv_heads * 128), then heph_attention_fp8kv
- * over pos + 1 keys with the rotated q: the same out, the same cache
- * bytes, in the attention's three launches (the scores kernel prepares q
- * and the new key's k and v itself). q in qkv_bf16 is left as it was (not
+ * heph_qk_norm_rope_kv on qkv_bf16 into key `pos` of k_cache / v_cache,
+ * then heph_attention_fp8kv over pos + 1 keys with the rotated q: the same
+ * out, the same cache bytes, in the attention's two launches (the scores
+ * kernel prepares q and the new key's k and v itself). q in qkv_bf16 is left as it was (not
  * rotated in place). ws: heph_attention_ws_bytes(n_heads, pos + 1) bytes.
  * rope_table: a heph_rope_table_bf16 table of n_rope_pos rows (for this
  * theta and head_dim), or NULL to compute pos's cos/sin in the call

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define HEPH_ABI_VERSION 5
+#define HEPH_ABI_VERSION 6
 
 /* status codes */
 #define HEPH_OK                 0

@@ -12,9 +12,10 @@
  *   rmsnorm        HF Qwen3RMSNorm as the engine calls it, forward.mojo:45-81
  *   qk_norm_rope   forward.mojo:474-500, rope kernels.mojo:709-762
  *   attention      kernels.mojo:923-1035 (fp32 scores, bf16 probabilities
- *                  from the global max and sum), reductions split over
- *                  128-key blocks as decode.hip runs them (the sum of
- *                  exponentials as split sums rescaled to the global max)
+ *                  from the global max and sum), the max and the sum of
+ *                  exponentials split over 128-key blocks as decode.hip runs
+ *                  them (split sums rescaled to the global max), the value
+ *                  sums in the lane and wave order of its values kernel
  *   silu_mul       kernels.mojo:1243-1255
  *   argmax         kernels.mojo:1376-1433 (bf16 logits, lowest index on ties)
  */
@@ -143,6 +144,17 @@ static float slots4(const float* a)
     return ((wv[0] + wv[1]) + wv[2]) + wv[3];
 }
 
+/* The values kernel's sum of 64 lane values x[l] (decode.hip,
+ * attn_values_kernel): T_q over the lanes q + 8m, then the eight T_q. */
+static float lanes64(const float* x)
+{
+    float T[8];
+    for (int q = 0; q < 8; ++q)
+        T[q] = ((x[q] + x[q + 32]) + (x[q + 16] + x[q + 48])) +
+               ((x[q + 8] + x[q + 40]) + (x[q + 24] + x[q + 56]));
+    return ((T[0] + T[7]) + (T[2] + T[5])) + ((T[1] + T[6]) + (T[3] + T[4]));
+}
+
 int heph_oracle_attention_fp8kv(uint16_t* out, const uint16_t* q, const uint8_t* kc,
                                 const uint8_t* vc, const float* kv_scale, int n_heads, int n_kv,
                                 int n_keys)
@@ -154,8 +166,11 @@ int heph_oracle_attention_fp8kv(uint16_t* out, const uint16_t* q, const uint8_t*
      *   split: m_s = max; l_s = slots4 over ks of (sum over i of exp(s - m_s))
      *   total: m = max m_s; sum = fold64 of per-slot fma sums of
      *          l_s * exp(m_s - m) (slot = split mod 64); p = bf16(exp(s - m)/sum)
-     *   values: per split and dim, a_ks = fma chain over i, slots4 over ks;
-     *          splits summed in order; times sv, bf16 */
+     *   values: per dim, 16 waves w x 64 lanes l: an fma chain of p_j v_j
+     *          over the 64-key blocks b = w, w + 16, ... (key j = 64b + l
+     *          below n_keys), lanes64 per wave, the waves as pairs
+     *          (2u, 2u + 1) then ((r0 + r1) + (r2 + r3)) + ((r4 + r5) +
+     *          (r6 + r7)); times sv, bf16 */
     enum { D = 128, SPLIT = 128 };
     const int NS = (n_keys + SPLIT - 1) / SPLIT;
     float* sc = malloc(sizeof(float) * (size_t)n_keys);
@@ -208,22 +223,23 @@ int heph_oracle_attention_fp8kv(uint16_t* out, const uint16_t* q, const uint8_t*
         for (int sp = 0; sp < NS; ++sp) part[sp & 63] = fmaf(ls[sp], expf(ms[sp] - m), part[sp & 63]);
         const float inv = 1.0f / fold(part, 64);
         for (int j = 0; j < n_keys; ++j) sc[j] = rb(expf(sc[j] - m) * inv);
-        float tot[D];
-        for (int d = 0; d < D; ++d) tot[d] = 0.0f;
-        for (int sp = 0; sp < NS; ++sp) {
-            for (int d = 0; d < D; ++d) {
-                float a[32];
-                for (int ks = 0; ks < 32; ++ks) {
-                    a[ks] = 0.0f;
-                    for (int i = 0; i < 4; ++i) {
-                        const int j = sp * SPLIT + ks + 32 * i;
-                        if (j < n_keys) a[ks] = fmaf(sc[j], dec[vc[j * row + kh * D + d]], a[ks]);
-                    }
+        for (int d = 0; d < D; ++d) {
+            float wv[16];
+            for (int w = 0; w < 16; ++w) {
+                float x[64];
+                for (int l = 0; l < 64; ++l) {
+                    float a = 0.0f;
+                    for (int j = 64 * w + l; j < n_keys; j += 64 * 16)
+                        a = fmaf(sc[j], dec[vc[j * row + kh * D + d]], a);
+                    x[l] = a;
                 }
-                tot[d] += slots4(a);
+                wv[w] = lanes64(x);
             }
+            float r8[8];
+            for (int u = 0; u < 8; ++u) r8[u] = wv[2 * u] + wv[2 * u + 1];
+            const float r = ((r8[0] + r8[1]) + (r8[2] + r8[3])) + ((r8[4] + r8[5]) + (r8[6] + r8[7]));
+            out[(size_t)h * D + d] = tob(r * kv_scale[n_kv + kh]);
         }
-        for (int d = 0; d < D; ++d) out[(size_t)h * D + d] = tob(tot[d] * kv_scale[n_kv + kh]);
     }
     free(sc);
     free(ms);

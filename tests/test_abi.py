@@ -26,7 +26,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_version_and_strerror(lib):
-    assert lib.heph_abi_version() == 5
+    assert lib.heph_abi_version() == 6
     for code in range(0, -12, -1):
         msg = L.strerror(code)
         assert msg and msg != "unknown status", code
@@ -208,8 +208,8 @@ def test_decode_ops_reject(lib):
     assert q(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 30, 8, 128, 0, 1e6, 1e-6, None) == L.HEPH_ERR_SHAPE
     a = lib.heph_attention_fp8kv
     ws = lib.heph_attention_ws_bytes(32, 4097)
-    # scores, then per 128-key split: max, sum and 128 value sums per head
-    assert ws == 4 * 32 * (4097 + 33 * (2 + 128))
+    # scores, then per 128-key split: max and sum per head
+    assert ws == 4 * 32 * (4097 + 33 * 2)
     # query heads per kv head: 1, 2, 4 or 8
     assert a(FAKE, FAKE, FAKE, FAKE, FAKE, 24, 8, 128, 10, FAKE, ws, None) == L.HEPH_ERR_SHAPE
     assert a(FAKE, FAKE, FAKE, FAKE, FAKE, 32, 2, 128, 10, FAKE, ws, None) == L.HEPH_ERR_SHAPE
@@ -315,3 +315,26 @@ def test_swiglu_linear_rejects(lib):
     assert call(qb=100) == L.HEPH_ERR_WORKSPACE
     assert call(sf=10) == L.HEPH_ERR_WORKSPACE
     assert call(act=ODD) == L.HEPH_ERR_ALIGN
+
+
+def test_v_cache_block_layout():
+    # decode.v_blocks / v_rows against the V cache byte formula of
+    # hephdecode.h: key j, kv head h, dim d at
+    # ((j/64 * n_kv + h) * 8 + d/16) * 1024 + (j%64) * 16 + d%16
+    import numpy as np
+    import torch
+    from hephaestus_amd import decode as DEC
+    rng = np.random.default_rng(7)
+    for n, n_kv in ((1, 2), (64, 8), (65, 8), (300, 4)):
+        rows = rng.integers(0, 256, size=(n, n_kv, 128), dtype=np.uint8)
+        blk = DEC.v_blocks(rows)
+        assert blk.shape == (-(-n // 64), n_kv, 8, 64, 16)
+        flat = blk.reshape(-1)
+        j, h, d = (rng.integers(0, n, 500), rng.integers(0, n_kv, 500), rng.integers(0, 128, 500))
+        off = ((j // 64 * n_kv + h) * 8 + d // 16) * 1024 + (j % 64) * 16 + d % 16
+        assert np.array_equal(flat[off], rows[j, h, d])
+        assert np.array_equal(DEC.v_rows(blk, n), rows)
+        assert not DEC.v_rows(blk)[n:].any()                  # zero padding keys
+        tb = DEC.v_blocks(torch.from_numpy(rows))
+        assert np.array_equal(tb.numpy(), blk)
+        assert np.array_equal(DEC.v_rows(tb, n).numpy(), rows)

@@ -129,16 +129,22 @@ def test_qk_norm_rope_kv_bit_exact(pos):
     qg, kg = rng_bf16(2, 128), rng_bf16(3, 128)
     inv = (np.random.default_rng(4).random(2 * NKV, dtype=np.float32) * 100 + 1).astype(np.float32)
     d = dev(qkv)
-    k = torch.zeros(NKV * 128, dtype=torch.uint8, device="cuda")
-    v = torch.zeros_like(k)
+    # caches up to key pos: K rows, V 64-key blocks; key pos written, the
+    # other bytes left zero
+    k = torch.zeros(pos + 1, NKV, 128, dtype=torch.uint8, device="cuda")
+    v = torch.zeros(pos // 64 + 1, NKV, 8, 64, 16, dtype=torch.uint8, device="cuda")
     DEC.qk_norm_rope_kv(d, dev(qg), dev(kg), k, v, dev(inv), NH, NKV, pos, 1e6, 1e-6)
     torch.cuda.synchronize()
     q_o, k_o, v_o = O.qk_norm_rope_kv(qkv, qg, kg, inv, NH, NKV, pos)
     got = host(d)
     assert np.array_equal(got[:NH * 128], q_o)
     assert np.array_equal(got[NH * 128:], qkv[NH * 128:])       # k, v rows untouched
-    assert np.array_equal(host(k), k_o)
-    assert np.array_equal(host(v), v_o)
+    assert np.array_equal(host(k[pos]).reshape(-1), k_o)
+    assert int(k[:pos].count_nonzero()) == 0
+    vr = DEC.v_rows(host(v))
+    assert np.array_equal(vr[pos].reshape(-1), v_o)
+    vr[pos] = 0
+    assert not vr.any()
 
 
 # Two bf16-rounded results of nearly equal values differ by at most one bf16
@@ -167,7 +173,7 @@ def test_attention_vs_oracle(n):
     kc, vc = codes(rng, (n, NKV, 128)), codes(rng, (n, NKV, 128))
     sc = (rng.random(2 * NKV, dtype=np.float32) * 0.02 + 0.005).astype(np.float32)
     out = torch.empty(NH * 128, dtype=torch.bfloat16, device="cuda")
-    DEC.attention_fp8kv(out, dev(q), dev(kc), dev(vc), dev(sc), NH, NKV, n)
+    DEC.attention_fp8kv(out, dev(q), dev(kc), dev(DEC.v_blocks(vc)), dev(sc), NH, NKV, n)
     torch.cuda.synchronize()
     mostly_equal(host(out), O.attention_fp8kv(q, kc, vc, sc, NH, NKV, n), f"attention n={n}")
 
@@ -180,7 +186,8 @@ def test_attention_decodes_every_e4m3_code():
     kc = np.full((1, NKV, 128), 0x30, np.uint8)
     q = rng_bf16(9, NH * 128)
     out = torch.empty(NH * 128, dtype=torch.bfloat16, device="cuda")
-    DEC.attention_fp8kv(out, dev(q), dev(kc), dev(vc), dev(np.ones(4, np.float32)), NH, NKV, 1)
+    DEC.attention_fp8kv(out, dev(q), dev(kc), dev(DEC.v_blocks(vc)), dev(np.ones(4, np.float32)),
+                        NH, NKV, 1)
     torch.cuda.synchronize()
     got = f32(host(out))
     table = O.e4m3_decode_table().astype(np.float64)
@@ -194,16 +201,19 @@ def test_attention_rejects_long_context_and_small_workspace():
     with pytest.raises(HephError):
         DEC.attention_fp8kv(z, z, z, z, z, 32, 8, L.ATTN_MAX_KEYS + 1, ws=z)
     with pytest.raises(HephError):
-        DEC.attention_fp8kv(z, z, z, z, z, 32, 8, 100, ws=z)
+        # a V cache of the two 64-key blocks 100 keys take; the workspace short
+        v = torch.zeros(2 * 64 * 8 * 128, dtype=torch.uint8, device="cuda")
+        DEC.attention_fp8kv(z, z, z, v, z, 32, 8, 100, ws=z)
 
 
 @pytest.mark.parametrize("nh,nkv", [(32, 8), (8, 8), (8, 4), (16, 2)], ids=["g4", "g1", "g2", "g8"])
 @pytest.mark.parametrize("pos", [0, 1, 127, 128, 300, 4096])
 def test_attention_qkv_matches_separate_ops(pos, nh, nkv):
-    # heph_attention_qkv_fp8kv against heph_qk_norm_rope_kv into cache row
+    # heph_attention_qkv_fp8kv against heph_qk_norm_rope_kv into cache key
     # pos followed by heph_attention_fp8kv over pos + 1 keys: the same output
-    # bits and the same cache bytes (the new row included, every other row
-    # untouched), with garbage in the new row beforehand; q in qkv stays raw.
+    # bits and the same cache bytes (the new key included, every other key
+    # and the V blocks' padding untouched), with garbage in the new key
+    # beforehand; q in qkv stays raw.
     rng = np.random.default_rng(1000 + pos + nh)
     qkv = rng_bf16(pos + 7, (nh + 2 * nkv) * 128, 2.0)
     qg, kg = rng_bf16(pos + 8, 128), rng_bf16(pos + 9, 128)
@@ -212,15 +222,19 @@ def test_attention_qkv_matches_separate_ops(pos, nh, nkv):
     kc, vc = codes(rng, (pos + 1, nkv, 128)), codes(rng, (pos + 1, nkv, 128))
     ws = DEC.attention_ws(nh, pos + 1)
 
+    vb = DEC.v_blocks(vc)
+
     # separate ops
-    q_sep, k_sep, v_sep = dev(qkv), dev(kc), dev(vc)
+    q_sep, k_sep, v_sep = dev(qkv), dev(kc), dev(vb)
     out_sep = torch.empty(nh * 128, dtype=torch.bfloat16, device="cuda")
-    DEC.qk_norm_rope_kv(q_sep, dev(qg), dev(kg), k_sep[pos], v_sep[pos], dev(inv), nh, nkv, pos,
-                        1e6, 1e-6)
+    DEC.qk_norm_rope_kv(q_sep, dev(qg), dev(kg), k_sep, v_sep, dev(inv), nh, nkv, pos, 1e6, 1e-6)
     DEC.attention_fp8kv(out_sep, q_sep, k_sep, v_sep, dev(sc), nh, nkv, pos + 1, ws)
+    vr = DEC.v_rows(host(v_sep))
+    assert np.array_equal(vr[:pos], vc[:pos]) and not vr[pos + 1:].any()
+    assert not np.array_equal(vr[pos], vc[pos])
     # one call, with the cos/sin from a table and computed in the call
     for rope in (DEC.rope_table(pos + 1 + 3 * (pos % 2), 1e6), None):
-        q_one, k_one, v_one = dev(qkv), dev(kc), dev(vc)
+        q_one, k_one, v_one = dev(qkv), dev(kc), dev(vb)
         out_one = torch.empty_like(out_sep)
         DEC.attention_qkv_fp8kv(out_one, q_one, dev(qg), dev(kg), k_one, v_one, dev(sc),
                                 dev(inv), nh, nkv, pos, 1e6, 1e-6, ws, rope)
@@ -253,7 +267,8 @@ def test_attention_qkv_rejects():
     with pytest.raises(HephError):
         DEC.attention_qkv_fp8kv(z, z, z, z, z, z, z, z, 32, 8, L.ATTN_MAX_KEYS, ws=z)
     with pytest.raises(HephError):
-        DEC.attention_qkv_fp8kv(z, z, z, z, z, z, z, z, 32, 8, 99, ws=z)
+        v = torch.zeros(2 * 64 * 8 * 128, dtype=torch.uint8, device="cuda")
+        DEC.attention_qkv_fp8kv(z, z, z, z, z, v, z, z, 32, 8, 99, ws=z)
 
 
 def test_silu_mul_vs_oracle():
