@@ -255,22 +255,18 @@ __device__ __forceinline__ void decode16(const uint4& w, float* f)
 //      lanes read a key's 128-byte row). Per head g:
 //        part_c = sum over those 16 dims in order (fma), then
 //        s_j = (((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7))) * (sk * f32(1/sqrt(128)))
-//      written to the workspace, with the split's max m_s and
-//        l_s = slots4 over ks of (sum over i in order of exp(s_j - m_s)),
-//      j = 128*split + ks + 32i, where slots4 sums 32 slot values as
-//      ((a0+a1)+(a2+a3)) + ((a4+a5)+(a6+a7)) per wave (8 slots) and the
-//      four waves in order
+//      written to the workspace
 //   B  values, one workgroup per (query head, 16-dim chunk) over all keys
-//      (attn_values_kernel): m = max over splits of m_s; sum = fold over 64
-//      slots (v[l] += v[l + h], h = 32 .. 1) of the per-slot fma sums (slot
-//      l: splits l, l+64, ... in order) of l_s * exp(m_s - m);
-//      p_j = bf16(exp(s_j - m) * (1/sum)) (the reference's probability,
-//      kernels.mojo:1003-1019, global max and sum); out_d = bf16(sum over
-//      keys of p_j * v_j[d] * sv) in the order that kernel states.
+//      (attn_values_kernel): the global max m and sum of exp(s_j - m) over
+//      the head's keys, p_j = bf16(exp(s_j - m) * (1/sum)) (the reference's
+//      probability, kernels.mojo:1003-1019, global max and sum), and
+//      out_d = bf16(sum over keys of p_j * v_j[d] * sv), in the orders that
+//      kernel states.
 // A workgroup of B reads the scores of one head and one 16-byte chunk of
-// each of its kv head's V rows; a values output needs every key, and
-// finishing it in one workgroup replaces a third launch that summed
-// per-split partial outputs. The CPU restatement repeats every order above.
+// each of its kv head's V rows; the softmax statistics and each output need
+// every key, and finishing them in one workgroup replaces per-split
+// statistics and a third launch that summed per-split partial outputs. The
+// CPU restatement repeats every order above.
 constexpr int kAttnSplit = 128;
 // Keys per thread of the scores kernel: the split's 128 keys sit in
 // 128 / kAttnKPT key slots of 8 lanes, a workgroup of 1024 / kAttnKPT
@@ -280,19 +276,16 @@ constexpr int kAttnSplit = 128;
 // on each CU.
 constexpr int kAttnKPT = 4;
 
-struct AttnWs {
-    float* scores;   // [n_heads][n_keys]
-    float* smax;     // [n_heads][n_splits]
-    float* ssum;     // [n_heads][n_splits]
-};
+// The workspace holds the scores [n_heads][n_keys] (fp32).
 
-__device__ __forceinline__ AttnWs attn_ws(float* ws, int n_heads, int n_keys, int n_splits)
+// Sum of 16 per-wave values: pairs (2u, 2u + 1), then
+// ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7)).
+__device__ __forceinline__ float sum16_waves(const float* r)
 {
-    AttnWs w;
-    w.scores = ws;
-    w.smax = w.scores + (size_t)n_heads * n_keys;
-    w.ssum = w.smax + (size_t)n_heads * n_splits;
-    return w;
+    float r8[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) r8[u] = r[2 * u] + r[2 * u + 1];
+    return ((r8[0] + r8[1]) + (r8[2] + r8[3])) + ((r8[4] + r8[5]) + (r8[6] + r8[7]));
 }
 
 // x + (the value of lane l ^ 1, l ^ 2 or l ^ 4 within each 8-lane group),
@@ -361,7 +354,6 @@ __global__ __launch_bounds__(1024 / KPT) void attn_scores_kernel(
     constexpr int SLOTS = kAttnSplit / KPT, NW = SLOTS / 8;   // key slots, waves
     const int kh = blockIdx.x % n_kv, split = blockIdx.x / n_kv;
     const int t = threadIdx.x, ks = t >> 3, c = t & 7;
-    const AttnWs w = attn_ws(ws, n_kv * G, n_keys, n_splits);
     const size_t row = (size_t)n_kv * D;
     const int j0 = split * kAttnSplit + ks;
     // The cache rows go out after the loads of q (or of the raw projection
@@ -501,49 +493,7 @@ __global__ __launch_bounds__(1024 / KPT) void attn_scores_kernel(
         const int j = j0 + SLOTS * i;
 #pragma unroll
         for (int g = 0; g < G; ++g)
-            if (c == g && j < n_keys) w.scores[(size_t)(kh * G + g) * n_keys + j] = sc[i][g];
-    }
-    // split max and sum of exp(s - m_s): within a wave over its 8 key slots
-    // (all 8 lanes of a slot hold its scores), then over the NW waves in LDS
-    __shared__ float wst[2][NW][G];
-    const int wave = t >> 6;
-    float mw[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float m = -3.4e38f;
-#pragma unroll
-        for (int i = 0; i < KPT; ++i)
-            if (j0 + SLOTS * i < n_keys) m = fmaxf(m, sc[i][g]);
-        mw[g] = slots_reduce<true>(m);
-    }
-    if ((t & 63) == 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) wst[0][wave][g] = mw[g];
-    }
-    __syncthreads();
-    float aw[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float m = wst[0][0][g];
-#pragma unroll
-        for (int v = 1; v < NW; ++v) m = fmaxf(m, wst[0][v][g]);
-        float a = 0.0f;
-#pragma unroll
-        for (int i = 0; i < KPT; ++i)
-            if (j0 + SLOTS * i < n_keys) a += expf(sc[i][g] - m);
-        aw[g] = slots_reduce<false>(a);
-        if (t == g) w.smax[(size_t)(kh * G + g) * n_splits + split] = m;
-    }
-    if ((t & 63) == 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) wst[1][wave][g] = aw[g];
-    }
-    __syncthreads();
-    if (t < G) {
-        float l = wst[1][0][t];
-#pragma unroll
-        for (int v = 1; v < NW; ++v) l += wst[1][v][t];
-        w.ssum[(size_t)(kh * G + t) * n_splits + split] = l;
+            if (c == g && j < n_keys) ws[(size_t)(kh * G + g) * n_keys + j] = sc[i][g];
     }
 }
 
@@ -554,11 +504,14 @@ __global__ __launch_bounds__(1024 / KPT) void attn_scores_kernel(
 // pass in flight, the next pass issued before the current one is used.
 constexpr int kValWaves = 16;
 constexpr int kValBlocks = 5;
+static_assert(kValWaves == 16, "sum16_waves folds 16 waves");
 
-template <int G>
+// ONE: n_keys <= kValWaves * kValBlocks * 64, one pass (its own kernel, so
+// that the register allocation of the common case is its own).
+template <int G, bool ONE>
 __global__ __launch_bounds__(64 * kValWaves) void attn_values_kernel(
     uint16_t* out, const float* ws, const uint8_t* vc, const float* kv_scale, int n_kv,
-    int n_keys, int n_splits)
+    int n_keys)
 {
     constexpr int NW = kValWaves, NB = kValBlocks;
     // kv head kh's workgroups are blockIdx kh + n_kv * i: with 8 kv heads
@@ -567,20 +520,15 @@ __global__ __launch_bounds__(64 * kValWaves) void attn_values_kernel(
     const int kh = blockIdx.x % n_kv, i = blockIdx.x / n_kv;
     const int g = i % G, c = i / G, h = kh * G + g;
     const int t = threadIdx.x, l = t & 63, wave = t >> 6;
-    const AttnWs w = attn_ws(const_cast<float*>(ws), n_kv * G, n_keys, n_splits);
     const int n_blocks = (n_keys + kVBlock - 1) / kVBlock;
-    const int n_pass = (n_blocks + NW * NB - 1) / (NW * NB);
-    const float* sh = w.scores + (size_t)h * n_keys;
+    const int n_pass = ONE ? 1 : (n_blocks + NW * NB - 1) / (NW * NB);
+    const float* sh = ws + (size_t)h * n_keys;
     const uint8_t* vh = vc + vblk_off(l, kh, 16 * c, n_kv);
     const size_t vstep = (size_t)n_kv * 8 * 1024;   // bytes per 64-key block
 
     // Loads in the order their data is needed (a wave's loads complete in
-    // issue order): the split statistics (lane l: split l up to 64 splits),
-    // then the scores (both written by the scores kernel, near in the cache
-    // hierarchy), then the V blocks (HBM).
-    const size_t base = (size_t)h * n_splits;
-    const float ms = l < n_splits ? w.smax[base + l] : -3.4e38f;
-    const float ls = l < n_splits ? w.ssum[base + l] : 0.0f;
+    // issue order): the scores (written by the scores kernel, near in the
+    // cache hierarchy), then the V blocks (HBM).
     float sa[NB], sb[NB];
     uint4 va[NB], vb[NB];
     auto issue = [&](int pass, float (&sj)[NB], uint4 (&vv)[NB]) __attribute__((always_inline)) {
@@ -595,24 +543,43 @@ __global__ __launch_bounds__(64 * kValWaves) void attn_values_kernel(
             if (b < n_blocks) vv[k] = ldg16u(vh + b * vstep);
         }
     };
-    issue(0, sa, va);
+    if (ONE) issue(0, sa, va);
 
-    // global max and 1/sum per head from the split statistics, by every
-    // wave (no barrier): the max over all splits, the sum of l_s * exp(m_s -
-    // m) by fma per lane over splits l, l + 64, ..., folded as v[l] +=
-    // v[l + h], h = 32 .. 1
-    float m, a = 0.0f;
-    if (n_splits <= 64) {
-        m = wave_max64(ms);
-        if (l < n_splits) a = __builtin_fmaf(ls, expf(ms - m), 0.0f);
+    // The head's max m and sum of exp(s_j - m) over all its keys: per lane
+    // over its keys in block order (the sum by plain adds), then over the
+    // wave (wave_max64 / wave_sum64), then over the 16 waves in LDS (the sum
+    // as sum16_waves). With one pass (n_keys <= 16 * 5 * 64) every score is
+    // already in registers; longer contexts read the scores again.
+    __shared__ float red[2][NW];
+    float mx = -3.4e38f;
+    if (ONE) {
+#pragma unroll
+        for (int k = 0; k < NB; ++k)
+            if (kVBlock * (k * NW + wave) + l < n_keys) mx = fmaxf(mx, sa[k]);
     } else {
-        m = -3.4e38f;
-        for (int s = l; s < n_splits; s += 64) m = fmaxf(m, w.smax[base + s]);
-        m = wave_max64(m);
-        for (int s = l; s < n_splits; s += 64)
-            a = __builtin_fmaf(w.ssum[base + s], expf(w.smax[base + s] - m), a);
+        for (int j = kVBlock * wave + l; j < n_keys; j += kVBlock * NW) mx = fmaxf(mx, sh[j]);
     }
-    const float inv = __fdiv_rn(1.0f, wave_sum64(a));
+    mx = wave_max64(mx);
+    if (l == 0) red[0][wave] = mx;
+    __syncthreads();
+    float m = red[0][0];
+#pragma unroll
+    for (int v = 1; v < NW; ++v) m = fmaxf(m, red[0][v]);
+    float a = 0.0f;
+    if (ONE) {   // sa then holds exp(s_j - m)
+#pragma unroll
+        for (int k = 0; k < NB; ++k)
+            if (kVBlock * (k * NW + wave) + l < n_keys) {
+                sa[k] = expf(sa[k] - m);
+                a += sa[k];
+            }
+    } else {
+        for (int j = kVBlock * wave + l; j < n_keys; j += kVBlock * NW) a += expf(sh[j] - m);
+    }
+    a = wave_sum64(a);
+    if (l == 0) red[1][wave] = a;
+    __syncthreads();
+    const float inv = __fdiv_rn(1.0f, sum16_waves(red[1]));
 
     // p_j = bf16(exp(s_j - m) * inv) (the reference's probability,
     // kernels.mojo:1003-1019); per lane an fma chain over its keys in block
@@ -620,13 +587,14 @@ __global__ __launch_bounds__(64 * kValWaves) void attn_values_kernel(
     float acc[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
-    auto consume = [&](int pass, const float (&sj)[NB], const uint4 (&vv)[NB])
+    // (have_e: sj holds exp(s_j - m) already)
+    auto consume = [&](int pass, const float (&sj)[NB], const uint4 (&vv)[NB], bool have_e)
         __attribute__((always_inline)) {
 #pragma unroll
         for (int k = 0; k < NB; ++k) {
             const int j = kVBlock * ((pass * NB + k) * NW + wave) + l;
             if (j < n_keys) {
-                const float pj = round_bf16(expf(sj[k] - m) * inv);
+                const float pj = round_bf16((have_e ? sj[k] : expf(sj[k] - m)) * inv);
                 float v16[16];
                 decode16(vv[k], v16);
 #pragma unroll
@@ -634,12 +602,17 @@ __global__ __launch_bounds__(64 * kValWaves) void attn_values_kernel(
             }
         }
     };
-    for (int p = 0; p < n_pass; p += 2) {
-        if (p + 1 < n_pass) issue(p + 1, sb, vb);
-        consume(p, sa, va);
-        if (p + 1 >= n_pass) break;
-        if (p + 2 < n_pass) issue(p + 2, sa, va);
-        consume(p + 1, sb, vb);
+    if (ONE) {
+        consume(0, sa, va, true);
+    } else {
+        issue(0, sa, va);
+        for (int p = 0; p < n_pass; p += 2) {
+            if (p + 1 < n_pass) issue(p + 1, sb, vb);
+            consume(p, sa, va, false);
+            if (p + 1 >= n_pass) break;
+            if (p + 2 < n_pass) issue(p + 2, sa, va);
+            consume(p + 1, sb, vb, false);
+        }
     }
 
     // Sum of the 16 values over the 64 lanes, halving the values per lane at
@@ -687,11 +660,10 @@ __global__ __launch_bounds__(64 * kValWaves) void attn_values_kernel(
     if ((l & 3) == 0) wsum[wave][8 * (l >> 5) + 4 * ((l >> 4) & 1) + 2 * b3 + b2] = h1;
     __syncthreads();
     if (t < 16) {
-        float r8[NW / 2];
+        float r[NW];
 #pragma unroll
-        for (int u = 0; u < NW / 2; ++u) r8[u] = wsum[2 * u][t] + wsum[2 * u + 1][t];
-        const float r = ((r8[0] + r8[1]) + (r8[2] + r8[3])) + ((r8[4] + r8[5]) + (r8[6] + r8[7]));
-        out[(size_t)h * 128 + 16 * c + t] = f32_to_bf16(r * kv_scale[n_kv + kh]);
+        for (int v = 0; v < NW; ++v) r[v] = wsum[v][t];
+        out[(size_t)h * 128 + 16 * c + t] = f32_to_bf16(sum16_waves(r) * kv_scale[n_kv + kh]);
     }
 }
 
@@ -781,8 +753,12 @@ hipError_t launch_attention(uint16_t* out, const uint16_t* q, const uint8_t* kc,
     else
         attn_scores_kernel<G, false, kAttnKPT><<<blocks, NT, 0, s>>>(ws, q, kc, kv_scale, n_kv,
                                                                     n_keys, splits, prep);
-    attn_values_kernel<G><<<n_kv * G * 8, 64 * kValWaves, 0, s>>>(out, ws, vc, kv_scale, n_kv,
-                                                                  n_keys, splits);
+    if (n_keys <= kValWaves * kValBlocks * kVBlock)
+        attn_values_kernel<G, true><<<n_kv * G * 8, 64 * kValWaves, 0, s>>>(out, ws, vc, kv_scale,
+                                                                            n_kv, n_keys);
+    else
+        attn_values_kernel<G, false><<<n_kv * G * 8, 64 * kValWaves, 0, s>>>(out, ws, vc, kv_scale,
+                                                                             n_kv, n_keys);
     return hipGetLastError();
 }
 
@@ -859,8 +835,7 @@ int heph_rope_table_bf16(void* table_bf16, int n_pos, int head_dim, double theta
 size_t heph_attention_ws_bytes(int n_heads, int n_keys)
 {
     if (n_heads < 1 || n_keys < 1) return 0;
-    const size_t splits = (size_t)(n_keys + kAttnSplit - 1) / kAttnSplit;
-    return 4 * (size_t)n_heads * ((size_t)n_keys + 2 * splits);
+    return 4 * (size_t)n_heads * (size_t)n_keys;
 }
 
 

@@ -71,7 +71,7 @@ int heph_qk_norm_rope_kv(void* qkv_bf16, const void* q_gamma, const void* k_gamm
  * layouts above scaled by kv_scale (K entries, then V), in two launches.
  * n_heads / n_kv_heads (query heads per kv head) must be 1, 2, 4 or 8.
  * ws: device scratch of heph_attention_ws_bytes(n_heads, n_keys) bytes
- * (scores, and per 128-key split the max and sum), 16-byte aligned.
+ * (the fp32 scores), 16-byte aligned.
  * Replaces attention (src/hephaestus/kernels.mojo:923-1035, :1183-1240).
  */
 size_t heph_attention_ws_bytes(int n_heads, int n_keys);

@@ -12,10 +12,9 @@
  *   rmsnorm        HF Qwen3RMSNorm as the engine calls it, forward.mojo:45-81
  *   qk_norm_rope   forward.mojo:474-500, rope kernels.mojo:709-762
  *   attention      kernels.mojo:923-1035 (fp32 scores, bf16 probabilities
- *                  from the global max and sum), the max and the sum of
- *                  exponentials split over 128-key blocks as decode.hip runs
- *                  them (split sums rescaled to the global max), the value
- *                  sums in the lane and wave order of its values kernel
+ *                  from the global max and sum), the sum of exponentials and
+ *                  the value sums in the lane and wave order of decode.hip's
+ *                  values kernel
  *   silu_mul       kernels.mojo:1243-1255
  *   argmax         kernels.mojo:1376-1433 (bf16 logits, lowest index on ties)
  */
@@ -132,18 +131,6 @@ void heph_oracle_qk_norm_rope_kv(uint16_t* qkv, const uint16_t* q_gamma, const u
     }
 }
 
-/* 32 key-slot values a[ks] summed as the attention kernels do: per group
- * of 8 slots ((a0+a1)+(a2+a3)) + ((a4+a5)+(a6+a7)), the four groups in order. */
-static float slots4(const float* a)
-{
-    float wv[4];
-    for (int w = 0; w < 4; ++w) {
-        const float* b = a + 8 * w;
-        wv[w] = ((b[0] + b[1]) + (b[2] + b[3])) + ((b[4] + b[5]) + (b[6] + b[7]));
-    }
-    return ((wv[0] + wv[1]) + wv[2]) + wv[3];
-}
-
 /* The values kernel's sum of 64 lane values x[l] (decode.hip,
  * attn_values_kernel): T_q over the lanes q + 8m, then the eight T_q. */
 static float lanes64(const float* x)
@@ -155,33 +142,30 @@ static float lanes64(const float* x)
     return ((T[0] + T[7]) + (T[2] + T[5])) + ((T[1] + T[6]) + (T[3] + T[4]));
 }
 
+/* The values kernel's sum of its 16 waves' values: pairs, then a tree. */
+static float waves16(const float* r)
+{
+    float r8[8];
+    for (int u = 0; u < 8; ++u) r8[u] = r[2 * u] + r[2 * u + 1];
+    return ((r8[0] + r8[1]) + (r8[2] + r8[3])) + ((r8[4] + r8[5]) + (r8[6] + r8[7]));
+}
+
 int heph_oracle_attention_fp8kv(uint16_t* out, const uint16_t* q, const uint8_t* kc,
                                 const uint8_t* vc, const float* kv_scale, int n_heads, int n_kv,
                                 int n_keys)
 {
-    /* Splits of 128 keys; key j = 128*split + ks + 32*i (key slot ks < 32,
-     * i < 4). Orders (decode.hip runs the same):
+    /* Orders (decode.hip runs the same), with 16 waves w x 64 lanes l
+     * holding the keys j = 64(w + 16k) + l, k = 0, 1, ... (in that order):
      *   score: per 16-dim chunk c an fma chain over its dims, then
      *          ((c0+c1)+(c2+c3)) + ((c4+c5)+(c6+c7)), times sk/sqrt(128)
-     *   split: m_s = max; l_s = slots4 over ks of (sum over i of exp(s - m_s))
-     *   total: m = max m_s; sum = fold64 of per-slot fma sums of
-     *          l_s * exp(m_s - m) (slot = split mod 64); p = bf16(exp(s - m)/sum)
-     *   values: per dim, 16 waves w x 64 lanes l: an fma chain of p_j v_j
-     *          over the 64-key blocks b = w, w + 16, ... (key j = 64b + l
-     *          below n_keys), lanes64 per wave, the waves as pairs
-     *          (2u, 2u + 1) then ((r0 + r1) + (r2 + r3)) + ((r4 + r5) +
-     *          (r6 + r7)); times sv, bf16 */
-    enum { D = 128, SPLIT = 128 };
-    const int NS = (n_keys + SPLIT - 1) / SPLIT;
+     *   softmax: m = max over all keys; per lane the sum of exp(s_j - m)
+     *          over its keys by plain adds, fold64 per wave, waves16;
+     *          p = bf16(exp(s - m) * (1/sum))
+     *   values: per dim, per lane an fma chain of p_j v_j over its keys,
+     *          lanes64 per wave, waves16; times sv, bf16 */
+    enum { D = 128 };
     float* sc = malloc(sizeof(float) * (size_t)n_keys);
-    float* ms = malloc(sizeof(float) * (size_t)NS);
-    float* ls = malloc(sizeof(float) * (size_t)NS);
-    if (!sc || !ms || !ls) {
-        free(sc);
-        free(ms);
-        free(ls);
-        return -1;
-    }
+    if (!sc) return -1;
     float dec[256];
     for (int c = 0; c < 256; ++c) dec[c] = heph_oracle_e4m3_decode((uint8_t)c);
     const size_t row = (size_t)n_kv * D;
@@ -203,26 +187,20 @@ int heph_oracle_attention_fp8kv(uint16_t* out, const uint16_t* q, const uint8_t*
             sc[j] = s * qk_scale;
         }
         float m = -3.4e38f;
-        for (int sp = 0; sp < NS; ++sp) {
-            float mx = -3.4e38f;
-            for (int j = sp * SPLIT; j < n_keys && j < (sp + 1) * SPLIT; ++j) mx = fmaxf(mx, sc[j]);
-            float a[32];
-            for (int ks = 0; ks < 32; ++ks) {
-                a[ks] = 0.0f;
-                for (int i = 0; i < 4; ++i) {
-                    const int j = sp * SPLIT + ks + 32 * i;
-                    if (j < n_keys) a[ks] += expf(sc[j] - mx);
-                }
+        for (int j = 0; j < n_keys; ++j) m = fmaxf(m, sc[j]);
+        for (int j = 0; j < n_keys; ++j) sc[j] = expf(sc[j] - m);
+        float sw[16];
+        for (int w = 0; w < 16; ++w) {
+            float x[64];
+            for (int l = 0; l < 64; ++l) {
+                float a = 0.0f;
+                for (int j = 64 * w + l; j < n_keys; j += 64 * 16) a += sc[j];
+                x[l] = a;
             }
-            ms[sp] = mx;
-            ls[sp] = slots4(a);
-            m = fmaxf(m, mx);
+            sw[w] = fold(x, 64);
         }
-        float part[64];
-        for (int t = 0; t < 64; ++t) part[t] = 0.0f;
-        for (int sp = 0; sp < NS; ++sp) part[sp & 63] = fmaf(ls[sp], expf(ms[sp] - m), part[sp & 63]);
-        const float inv = 1.0f / fold(part, 64);
-        for (int j = 0; j < n_keys; ++j) sc[j] = rb(expf(sc[j] - m) * inv);
+        const float inv = 1.0f / waves16(sw);
+        for (int j = 0; j < n_keys; ++j) sc[j] = rb(sc[j] * inv);
         for (int d = 0; d < D; ++d) {
             float wv[16];
             for (int w = 0; w < 16; ++w) {
@@ -235,15 +213,10 @@ int heph_oracle_attention_fp8kv(uint16_t* out, const uint16_t* q, const uint8_t*
                 }
                 wv[w] = lanes64(x);
             }
-            float r8[8];
-            for (int u = 0; u < 8; ++u) r8[u] = wv[2 * u] + wv[2 * u + 1];
-            const float r = ((r8[0] + r8[1]) + (r8[2] + r8[3])) + ((r8[4] + r8[5]) + (r8[6] + r8[7]));
-            out[(size_t)h * D + d] = tob(r * kv_scale[n_kv + kh]);
+            out[(size_t)h * D + d] = tob(waves16(wv) * kv_scale[n_kv + kh]);
         }
     }
     free(sc);
-    free(ms);
-    free(ls);
     return 0;
 }
 

@@ -208,8 +208,8 @@ def test_decode_ops_reject(lib):
     assert q(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 30, 8, 128, 0, 1e6, 1e-6, None) == L.HEPH_ERR_SHAPE
     a = lib.heph_attention_fp8kv
     ws = lib.heph_attention_ws_bytes(32, 4097)
-    # scores, then per 128-key split: max and sum per head
-    assert ws == 4 * 32 * (4097 + 33 * 2)
+    # the fp32 scores
+    assert ws == 4 * 32 * 4097
     # query heads per kv head: 1, 2, 4 or 8
     assert a(FAKE, FAKE, FAKE, FAKE, FAKE, 24, 8, 128, 10, FAKE, ws, None) == L.HEPH_ERR_SHAPE
     assert a(FAKE, FAKE, FAKE, FAKE, FAKE, 32, 2, 128, 10, FAKE, ws, None) == L.HEPH_ERR_SHAPE
