@@ -251,8 +251,9 @@ __device__ __forceinline__ void decode16(const uint4& w, float* f)
 //   A  scores, one workgroup per (kv head, split of kAttnSplit keys) serving
 //      the G query heads that share the kv head (every K byte read once):
 //      thread t holds dims 16c .. 16c+15 (c = t & 7) of keys
-//      j = 128*split + (t >> 3) + 32i (i < 4), one 16-byte load each (eight
-//      lanes read a key's 128-byte row). Per head g:
+//      j = kAttnSplit*split + (t >> 3) + (kAttnSplit/kAttnKPT)*i
+//      (i < kAttnKPT), one 16-byte load each (eight lanes read a key's
+//      128-byte row). Per head g:
 //        part_c = sum over those 16 dims in order (fma), then
 //        s_j = (((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7))) * (sk * f32(1/sqrt(128)))
 //      written to the workspace
@@ -267,14 +268,15 @@ __device__ __forceinline__ void decode16(const uint4& w, float* f)
 // every key, and finishing them in one workgroup replaces per-split
 // statistics and a third launch that summed per-split partial outputs. The
 // CPU restatement repeats every order above.
-constexpr int kAttnSplit = 128;
-// Keys per thread of the scores kernel: the split's 128 keys sit in
-// 128 / kAttnKPT key slots of 8 lanes, a workgroup of 1024 / kAttnKPT
-// threads. The summation orders (and the CPU restatement) follow
-// kAttnKPT = 4; 2 (eight waves, half the work each) measured slower on
-// MI355X: the VALU work per SIMD is the same and one workgroup already sits
-// on each CU.
-constexpr int kAttnKPT = 4;
+// Keys per split and per thread of the scores kernel: the split's keys sit
+// in kAttnSplit / kAttnKPT key slots of 8 lanes, a workgroup of
+// 8 * kAttnSplit / kAttnKPT threads; a score's arithmetic does not depend
+// on either. On MI355X at 4097 keys (graph-replayed decode step, ms per
+// token): 256 keys x 2 per thread (136 workgroups of 1024 threads) 1.682,
+// 256 x 4 1.687, 128 x 4 1.727, 64 x 2 1.712, 512 x 4 1.743, 256 x 8 1.727:
+// fewer workgroups each prepare the query heads once for more keys.
+constexpr int kAttnSplit = 256;
+constexpr int kAttnKPT = 2;
 
 // The workspace holds the scores [n_heads][n_keys] (fp32).
 
@@ -295,26 +297,6 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_add(float x)
 {
     return x + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
-}
-
-// Over the 8 key slots of a wave (lanes 8k + c, k < 8): the max, or the
-// sum ((a0+a1)+(a2+a3)) + ((a4+a5)+(a6+a7)); the result in every lane.
-// Pairs k^1 by row_ror:8, then rows 0-1 / 2-3 by v_permlane16_swap, then
-// the two halves by v_permlane32_swap (each pair's sum is the same value
-// in both lanes, as float addition commutes).
-template <bool MAX>
-__device__ __forceinline__ float slots_reduce(float x)
-{
-    const float y = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xf, 0xf, false));
-    x = MAX ? fmaxf(x, y) : x + y;
-    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                      false);
-    x = MAX ? fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]))
-            : __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
-    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                      false);
-    return MAX ? fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]))
-               : __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
 }
 
 // The token's q/k/v preparation done by the scores kernel in its QKV form
@@ -339,14 +321,14 @@ struct QkvPrep {
 // have left in memory, with the same arithmetic (head_norm_rope): its G
 // query heads, and in the split holding the new key (the last) that key's
 // k and v rows, quantized into the cache (the values kernel reads v from
-// there). The G q heads and the new key's k go round-robin to the four
+// there). The G q heads and the new key's k go round-robin to the NW
 // waves, every raw load issued before the first reduction, a wave's heads
 // folded together; v takes one element per thread; the rotated
 // q heads and the new key's codes meet in LDS after one barrier, and the
 // new key's score uses those codes instead of the cache row loaded at the
 // start. All of it runs while the cache loads are in flight.
 template <int G, bool QKV, int KPT>
-__global__ __launch_bounds__(1024 / KPT) void attn_scores_kernel(
+__global__ __launch_bounds__(8 * kAttnSplit / KPT) void attn_scores_kernel(
     float* ws, const uint16_t* q, const uint8_t* kc, const float* kv_scale, int n_kv,
     int n_keys, int n_splits, QkvPrep prep)
 {
@@ -369,7 +351,7 @@ __global__ __launch_bounds__(1024 / KPT) void attn_scores_kernel(
     float qv[G][16];
     if constexpr (QKV) {
         // normalized heads: items 0..G-1 the q heads kh*G + g, item G the
-        // new key's k row (last split only), round-robin over the four
+        // new key's k row (last split only), round-robin over the NW
         // waves; a wave's heads fold their sums of squares together (the
         // same per-head order as wave_sum64). The new key's v row is
         // quantized one element per thread.
@@ -746,7 +728,7 @@ hipError_t launch_attention(uint16_t* out, const uint16_t* q, const uint8_t* kc,
 {
     const int splits = (n_keys + kAttnSplit - 1) / kAttnSplit;
     const int blocks = n_kv * splits;
-    constexpr int NT = 1024 / kAttnKPT;
+    constexpr int NT = 8 * kAttnSplit / kAttnKPT;
     if (prep.qkv)
         attn_scores_kernel<G, true, kAttnKPT><<<blocks, NT, 0, s>>>(ws, q, kc, kv_scale, n_kv,
                                                                    n_keys, splits, prep);

@@ -207,7 +207,7 @@ def test_attention_rejects_long_context_and_small_workspace():
 
 
 @pytest.mark.parametrize("nh,nkv", [(32, 8), (8, 8), (8, 4), (16, 2)], ids=["g4", "g1", "g2", "g8"])
-@pytest.mark.parametrize("pos", [0, 1, 127, 128, 300, 4096])
+@pytest.mark.parametrize("pos", [0, 1, 127, 128, 255, 256, 300, 4096])
 def test_attention_qkv_matches_separate_ops(pos, nh, nkv):
     # heph_attention_qkv_fp8kv against heph_qk_norm_rope_kv into cache key
     # pos followed by heph_attention_fp8kv over pos + 1 keys: the same output
