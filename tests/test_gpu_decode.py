@@ -165,7 +165,9 @@ def mostly_equal(got, want, what):
         f"{what}: max rel {err:.2e}"
 
 
-@pytest.mark.parametrize("n", [1, 2, 300, 511, 512, 513, 4097, 20000])
+# 5120 keys: the last one-pass values launch; 5121 and 12000: the multi-pass
+# form with two and three passes (an even and an odd count); 20000: four
+@pytest.mark.parametrize("n", [1, 2, 300, 511, 512, 513, 4097, 5120, 5121, 12000, 20000])
 def test_attention_vs_oracle(n):
     NH, NKV = 32, 8
     rng = np.random.default_rng(n)
@@ -194,6 +196,28 @@ def test_attention_decodes_every_e4m3_code():
     nan = np.isnan(table)
     assert np.array_equal(np.isnan(got), nan)
     assert np.array_equal(got[~nan], table[~nan])
+
+
+def test_attention_max_context_exact():
+    # ATTN_MAX_KEYS = 2^18 keys, every K row the same: every score is the
+    # same, p_j = bf16(exp(0) * 2^-18) = 2^-18 exactly, and with V values in
+    # {0.5, 1, 1.5, 2} (v[j, d] = 0.5 * (1 + (j + d) % 4)) every partial sum
+    # is a multiple of 2^-19 below 4, exact in any order: out = 1.25 for every
+    # head and dim (the multi-pass values kernel over 4096 blocks)
+    NH, NKV, n = 32, 8, L.ATTN_MAX_KEYS
+    assert n == 1 << 18
+    q = dev(rng_bf16(5, NH * 128))
+    kc = torch.full((n, NKV, 128), 0x3A, dtype=torch.uint8, device="cuda")
+    codes4 = torch.tensor([0x30, 0x38, 0x3C, 0x40], dtype=torch.uint8, device="cuda")
+    j = torch.arange(n, device="cuda").view(n, 1, 1)
+    d = torch.arange(128, device="cuda").view(1, 1, 128)
+    vc = DEC.v_blocks(codes4[(j + d) % 4].expand(n, NKV, 128))
+    sc = torch.ones(2 * NKV, dtype=torch.float32, device="cuda")
+    out = torch.empty(NH * 128, dtype=torch.bfloat16, device="cuda")
+    DEC.attention_fp8kv(out, q, kc, vc, sc, NH, NKV, n)
+    torch.cuda.synchronize()
+    got = f32(host(out))
+    assert np.all(got == 1.25), np.unique(got)[:8]
 
 
 def test_attention_rejects_long_context_and_small_workspace():
