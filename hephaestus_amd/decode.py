@@ -129,8 +129,8 @@ def attention_qkv_fp8kv(out, qkv, q_gamma, k_gamma, k_cache, v_cache, kv_scale, 
                         n_heads: int, n_kv: int, pos: int, theta: float = 1e6,
                         eps: float = 1e-6, ws: torch.Tensor | None = None,
                         rope: torch.Tensor | None = None) -> None:
-    """qk_norm_rope_kv into cache row pos, then attention_fp8kv over pos + 1
-    keys, in the attention's three launches (the same out and cache bytes;
+    """qk_norm_rope_kv into cache key pos, then attention_fp8kv over pos + 1
+    keys, in the attention's two launches (the same out and cache bytes;
     q in qkv is not rotated in place). rope: a rope_table of more than pos
     rows for this theta, or None to compute pos's cos/sin in the call."""
     if ws is None:
