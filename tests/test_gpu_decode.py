@@ -180,6 +180,21 @@ def test_attention_vs_oracle(n):
     mostly_equal(host(out), O.attention_fp8kv(q, kc, vc, sc, NH, NKV, n), f"attention n={n}")
 
 
+@pytest.mark.parametrize("nh,nkv,n", [(16, 2, 7000), (8, 8, 7000), (8, 4, 300), (16, 2, 65)],
+                         ids=["g8-multipass", "g1-multipass", "g2", "g8-one-block"])
+def test_attention_gqa_vs_oracle(nh, nkv, n):
+    # the other query-per-kv ratios through both values-kernel forms
+    rng = np.random.default_rng(n + nh)
+    q = rng_bf16(n + 1, nh * 128, 3.0)
+    kc, vc = codes(rng, (n, nkv, 128)), codes(rng, (n, nkv, 128))
+    sc = (rng.random(2 * nkv, dtype=np.float32) * 0.02 + 0.005).astype(np.float32)
+    out = torch.empty(nh * 128, dtype=torch.bfloat16, device="cuda")
+    DEC.attention_fp8kv(out, dev(q), dev(kc), dev(DEC.v_blocks(vc)), dev(sc), nh, nkv, n)
+    torch.cuda.synchronize()
+    mostly_equal(host(out), O.attention_fp8kv(q, kc, vc, sc, nh, nkv, n),
+                 f"attention {nh}/{nkv} n={n}")
+
+
 def test_attention_decodes_every_e4m3_code():
     # one key: p = 1 and out = bf16(e4m3(v) * 1), so the hardware converter
     # must reproduce the E4M3FN table for all 256 codes (NaN for 0x7F/0xFF)
