@@ -266,7 +266,7 @@ struct BigTile {
     static constexpr int STAGE = STAGE_A + STAGE_B + STAGE_S;
     // LDS stages. A short chunk is below the loaded HBM latency, so where
     // LDS allows, the DMA runs two chunks ahead: three whole stages (64 and
-    // 128 rows by 256 columns); else two A/scale stages and three B stages
+    // 128 rows by 256 columns, 64 x 192); else two A/scale stages and three B stages
     // (the weights, streamed from HBM in a real prefill, get the extra
     // chunk: 192 x 256, 256 x 192, 128 x 320); else two (256 x 256).
     static constexpr int kLds = 160 * 1024;
@@ -847,16 +847,18 @@ hipError_t launch_big(const Fp8Operands& op, hipStream_t stream, const LaunchTim
 // M = 4096 the fit ranks the tiles as measured on every config-1 shape
 // (qkv 256 x 192 72.6 us against 75.7 at 256 x 256; o_proj 128 x 320 46.5
 // against 47.9 at 192 x 256; gate_up 256 x 256 193.0 against 212.2; down
-// 128 x 320 100.4 against 104.4), and at M = 512 as well (64 x 256 for qkv
-// and, with 3 K splits, o_proj; 128 x 320 for gate_up; 128 x 256 with 6
-// splits for down).
+// 128 x 320 100.4 against 104.4), and at M = 512 as well (64 x 192 for qkv,
+// 256 tiles, one round: 18.7 against 21.6 us at 64 x 256; 64 x 256 with 3 K
+// splits for o_proj; 128 x 320 for gate_up; 128 x 256 with 6 splits for
+// down). 64 x 192 is fitted to M = 512 qkv alone.
 struct TileCost {
     int bm, bn;
     long chunk, fixed;
 };
 constexpr TileCost kTileCost[] = {{256, 256, 2535, 16730}, {256, 192, 2569, 11650},
                                   {192, 256, 2440, 12930}, {128, 320, 2327, 13880},
-                                  {128, 256, 1734, 9887},  {64, 256, 1550, 7000}};
+                                  {128, 256, 1734, 9887},  {64, 256, 1550, 7000},
+                                  {64, 192, 1300, 6000}};
 
 // Estimated time (us) of the large-M GEMM with tile tc and s K splits:
 // rounds of (tile, split) workgroups over the CUs (one 512-thread
@@ -888,6 +890,9 @@ GemmPlan gemm_plan(int M, int N, int K, bool can_split, int forced_bm, int force
     GemmPlan best{0, 0, 1};
     double best_t = -1.0;
     for (const auto& tc : kTileCost) {
+        // 64 x 192 only where its fit holds (M >= 256): below, the K-split
+        // plans of the small-M routes stay with the tiles they were measured on
+        if (tc.bm == 64 && tc.bn == 192 && M < 256 && forced_bn != 192) continue;
         if (forced_bm >= 64 && tc.bm != forced_bm) continue;
         if (forced_bn && tc.bn != forced_bn) continue;
         for (int s = 1; s <= (can_split ? 8 : 1); ++s) {
@@ -934,6 +939,10 @@ hipError_t launch_fp8_gemm(const Fp8Operands& op, hipStream_t stream,
                                         o.tune.gemm_bn);
         o.splits = plan.splits;
         const bool sk = o.splits > 1;
+        if (plan.bn == 192 && plan.bm == 64) {
+            *name = sk ? "fp8_gemm_64x192_splitk" : "fp8_gemm_64x192";
+            return launch_big<64, 192>(o, stream, t);
+        }
         if (plan.bn == 192) {
             *name = sk ? "fp8_gemm_256x192_splitk" : "fp8_gemm_256x192";
             return launch_big<256, 192>(o, stream, t);

@@ -296,7 +296,7 @@ const char* heph_last_kernel(void);
  *                the 128x128 GEMM (otherwise used only when M*K or N*K
  *                reaches 2^31)
  *   gemm_bn      tile width of the large-M GEMM: 192, 256 or 320 (tiles
- *                64/128/192/256 x 256, 256 x 192, 128 x 320; a gemm_bm and
+ *                64/128/192/256 x 256, 64/256 x 192, 128 x 320; a gemm_bm and
  *                gemm_bn that form none of these run gemm_bm x 256)
  *   batch_split  the 64-column K-split kernel for M <= 32 with 1x128 groups:
  *                -1 never, n in 1..64 always, with at least n K splits

@@ -835,7 +835,8 @@ def test_graph_capture_replays_match_eager():
 
 # ------------------------------------------------ large-M GEMM variants ----
 
-@pytest.fixture(params=[(64, 256), (128, 256), (192, 256), (256, 256), (256, 192), (128, 320)],
+@pytest.fixture(params=[(64, 256), (128, 256), (192, 256), (256, 256), (64, 192), (256, 192),
+                        (128, 320)],
                 ids=lambda t: f"{t[0]}x{t[1]}")
 def tile_m(request):
     """Force the large-M kernel's tile (height x width) for one test."""
@@ -1329,13 +1330,14 @@ def test_large_m_tile_choice(M):
     # tile's chunk and fixed costs; on the config-1 shapes it picks the tiles
     # measured fastest on MI355X (GEMM alone): at M = 4096 256 x 192 for qkv
     # (512 tiles, 2 rounds), 128 x 320 for o_proj and down (256 tiles, 1
-    # round), 256 x 256 for gate_up; at M = 512 64 x 256 for qkv and (3
-    # splits) o_proj, 128 x 320 for gate_up, 128 x 256 with splits for down.
+    # round), 256 x 256 for gate_up; at M = 512 64 x 192 for qkv (256 tiles,
+    # 1 round), 64 x 256 with 3 splits for o_proj, 128 x 320 for gate_up,
+    # 128 x 256 with splits for down.
     if torch.cuda.get_device_properties(0).multi_processor_count != 256:
         pytest.skip("expectations are for a 256-CU MI355X")
     want = {4096: {"qkv": "256x192", "o_proj": "128x320", "gate_up": "256x256",
                    "down": "128x320"},
-            512: {"qkv": "64x256", "o_proj": "64x256_splitk", "gate_up": "128x320",
+            512: {"qkv": "64x192", "o_proj": "64x256_splitk", "gate_up": "128x320",
                   "down": "128x256_splitk"}}[M]
     for name, tile in want.items():
         N, K = SHAPES[name]
