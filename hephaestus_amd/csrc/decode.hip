@@ -41,22 +41,6 @@ __device__ __forceinline__ uint32_t e4m3_sat(float v)
     return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v, v, 0, false) & 0xFFu;
 }
 
-// Sum over the 256 threads of a workgroup: s[t] for t < 256 in LDS, folded
-// as s[t] += s[t + h] for h = 128, 64, ..., 1 (the order the CPU repeats).
-__device__ __forceinline__ float block_sum256(float v, float* s)
-{
-    const int t = threadIdx.x;
-    s[t] = v;
-    __syncthreads();
-    for (int h = 128; h > 0; h >>= 1) {
-        if (t < h) s[t] += s[t + h];
-        __syncthreads();
-    }
-    const float r = s[0];
-    __syncthreads();
-    return r;
-}
-
 // Sum over the 64 lanes of a wave, folded as v[l] += v[l + h] for
 // h = 32, 16, ..., 1; the result is lane 0's.
 __device__ __forceinline__ float wave_sum64(float v) { return wave_fold_sum64(v); }
