@@ -93,6 +93,8 @@ SIGNATURES = {
 }
 
 ATTN_MAX_KEYS = 262144
+# HEPH_ABI_VERSION of include/hephfp8.h that these signatures follow
+ABI_VERSION = 6
 
 
 class HephLibraryMissing(ImportError):
@@ -112,6 +114,10 @@ def lib():
             f = getattr(L, name)
             f.restype = res
             f.argtypes = args
+        if L.heph_abi_version() != ABI_VERSION:
+            raise HephLibraryMissing(
+                f"{LIB_PATH} has ABI version {L.heph_abi_version()}, this binding follows "
+                f"{ABI_VERSION}: rebuild it")
         _lib = L
     return _lib
 

@@ -26,7 +26,11 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_version_and_strerror(lib):
-    assert lib.heph_abi_version() == 6
+    assert lib.heph_abi_version() == 6 == L.ABI_VERSION
+    # the header's define, the built library and the Python binding agree
+    import re
+    hdr = open(L.HEADERS[0]).read()
+    assert int(re.search(r"#define HEPH_ABI_VERSION (\d+)", hdr).group(1)) == L.ABI_VERSION
     for code in range(0, -12, -1):
         msg = L.strerror(code)
         assert msg and msg != "unknown status", code
